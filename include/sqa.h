@@ -1,0 +1,88 @@
+/*
+ * sqa.h - C ABI of libsqa.so, the MI355X (gfx950) paged small-q attention
+ * library. Plain pointers, integers and sizes only; no torch types. Every
+ * function returns a status and never throws across the boundary.
+ *
+ * Tensor contract (reference: /root/reference/csrc/small_q_attention_ext.cu:976-1002,
+ * /root/reference/src/small_q_attention/cuda.py:61-78):
+ *   query        [batch, q_len, num_query_heads, 128]  fp16, contiguous, device
+ *   key_cache    [num_pages, 16, num_kv_heads, 128]    fp16, contiguous, device
+ *   value_cache  same shape as key_cache
+ *   block_tables [batch, max_pages] int32, device
+ *   seq_lens     [batch] int32, device; KV length including the q_len draft tokens
+ *   output       [batch, q_len, num_query_heads, 128]  fp16, device (written)
+ * Draft row qi of sequence b attends to tokens t < seq_lens[b] - q_len + qi + 1,
+ * query head h reads kv head h / (num_query_heads / num_kv_heads), scale 128^-1/2.
+ * Rows that see no token are written as 0 (reference v2-v5 merge, .cu:365).
+ * q_len * (num_query_heads / num_kv_heads) must be <= 64.
+ */
+#ifndef SQA_H_
+#define SQA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define SQA_OK 0
+#define SQA_ERR_INVALID 1     /* bad argument (shape, null pointer, ...) */
+#define SQA_ERR_UNSUPPORTED 2 /* outside the supported contract (head_dim, page size, rows) */
+#define SQA_ERR_WORKSPACE 3   /* workspace missing or too small */
+#define SQA_ERR_HIP 4         /* HIP runtime error (launch, device query) */
+
+/*
+ * Chooses the split-KV decomposition.
+ * Replaces the reference chunking policy (csrc/small_q_attention_ext.cu:1096-1099,
+ * :1171-1178; default chunk_keys=512 at src/small_q_attention/cuda.py:127).
+ *   chunk_keys > 0: each split owns ceil(chunk_keys / 16) pages (reference meaning).
+ *   chunk_keys == 0: automatic, from the device's compute-unit count.
+ * max_seq_len <= 0 means "unknown": the plan covers max_pages * 16 tokens.
+ * Writes *num_splits >= 1 and *pages_per_split >= 1.
+ */
+int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int num_kv_heads,
+                    int max_seq_len, int max_pages, int chunk_keys, int* num_splits,
+                    int* pages_per_split);
+
+/*
+ * Device workspace bytes sqa_paged_mtp_attention needs for num_splits splits
+ * (0 when num_splits == 1). Replaces the per-call torch::empty of the partial
+ * buffers in the reference launchers (csrc/small_q_attention_ext.cu:1102-1104).
+ */
+size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv_heads,
+                           int num_splits);
+
+/*
+ * Runs the op asynchronously on `stream` (a hipStream_t; NULL = default stream).
+ * Replaces the launchers small_q_attention_v0..v5 and their pybind entries
+ * forward, forward_v1..forward_v5 (csrc/small_q_attention_ext.cu:969-1378,
+ * :1380-1390). num_splits/pages_per_split come from sqa_plan_splits.
+ * `workspace` must hold sqa_workspace_bytes(...) bytes (may be NULL when
+ * num_splits == 1). Allocates nothing and never synchronises.
+ * `timing_events`: NULL, or an array of 3 hipEvent_t recorded on `stream`
+ * before the partial kernel, between the two kernels and after the merge
+ * kernel (used by the benchmark to time the partial kernel alone).
+ */
+int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void* value_cache,
+                            const int32_t* block_tables, const int32_t* seq_lens, void* output,
+                            void* workspace, size_t workspace_bytes, int batch, int q_len,
+                            int num_query_heads, int num_kv_heads, int head_dim,
+                            int64_t num_pages, int page_size, int max_pages, int num_splits,
+                            int pages_per_split, void* stream, void** timing_events);
+
+/* Compute units of `device` (256 on MI355X), or -1 on error. */
+int sqa_device_cu_count(int device);
+
+/* Message for the last non-zero status returned on this thread. */
+const char* sqa_last_error(void);
+
+/* Library version string. */
+const char* sqa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SQA_H_ */

@@ -1,0 +1,124 @@
+/*
+ * Scalar double-precision brute force of paged small-q (MTP) attention.
+ *
+ * TEST INFRASTRUCTURE ONLY: loaded by oracle/cbrute.py for tests/ and the
+ * bench's CPU baseline; the product library never links it.
+ *
+ * Mathematics of /root/reference/src/small_q_attention/reference.py:46-72:
+ *   scale = D^-1/2 (:46); query head qh reads kv head qh / (Hq/Hkv) (:67);
+ *   draft row qi of sequence b sees tokens t < seq_lens[b] - Q + qi + 1 (:63);
+ *   token t is slot t % page of physical page block_tables[b, t / page]
+ *   (:54-59); out = softmax(q . k * scale) @ v (:68-70).
+ * Rows with no visible token are written as 0 (the reference raises for them,
+ * reference.py:52-53; the split-KV kernels of the reference write 0,
+ * csrc/small_q_attention_ext.cu:365).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+static double g_half_table[65536];
+static int g_table_ready = 0;
+
+/* IEEE-754 binary16 bit pattern -> double. */
+static double half_bits_to_double(uint16_t h) {
+  const int sign = h >> 15;
+  const int expo = (h >> 10) & 31;
+  const int mant = h & 1023;
+  double v;
+  if (expo == 0) {
+    v = ldexp((double)mant, -24);
+  } else if (expo == 31) {
+    v = mant ? NAN : INFINITY;
+  } else {
+    v = ldexp((double)(mant | 1024), expo - 25);
+  }
+  return sign ? -v : v;
+}
+
+static void build_table(void) {
+  if (g_table_ready) return;
+  for (int i = 0; i < 65536; ++i) g_half_table[i] = half_bits_to_double((uint16_t)i);
+  g_table_ready = 1;
+}
+
+double sqa_oracle_half_to_double(uint16_t bits) { return half_bits_to_double(bits); }
+
+/*
+ * q:  [B, Q, Hq, D] fp16 bits;  kc, vc: [num_pages, page, Hkv, D] fp16 bits;
+ * bt: [B, max_pages] int32;  sl: [B] int32;  out: [B, Q, Hq, D] double.
+ * Returns 0, or -1 if a page id read by the computation lies outside
+ * [0, num_pages), or -2 if a sequence needs more than max_pages pages.
+ */
+int sqa_oracle_f64(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                   const int32_t* bt, const int32_t* sl, double* out,
+                   int B, int Q, int Hq, int Hkv, int D, int page, int max_pages,
+                   long long num_pages) {
+  build_table();
+  const int group = Hq / Hkv;
+  const double scale = 1.0 / sqrt((double)D);
+  const long long rows = (long long)B * Q * Hq;
+  int status = 0;
+
+  for (int b = 0; b < B; ++b) {
+    const long long len = sl[b];
+    const long long pages_used = (len + page - 1) / page;
+    if (pages_used > max_pages) return -2;
+    for (long long p = 0; p < pages_used; ++p) {
+      const int32_t pid = bt[(long long)b * max_pages + p];
+      if (pid < 0 || pid >= num_pages) return -1;
+    }
+  }
+
+#pragma omp parallel
+  {
+    double* logits = NULL;
+    long long cap = 0;
+    double* qv = (double*)malloc(sizeof(double) * (size_t)D);
+    double* acc = (double*)malloc(sizeof(double) * (size_t)D);
+#pragma omp for schedule(dynamic, 1)
+    for (long long row = 0; row < rows; ++row) {
+      const int qh = (int)(row % Hq);
+      const int qi = (int)((row / Hq) % Q);
+      const int b = (int)(row / ((long long)Hq * Q));
+      const int kvh = qh / group;
+      const long long visible = (long long)sl[b] - Q + qi + 1;
+      double* o = out + row * D;
+      if (visible <= 0) {
+        for (int d = 0; d < D; ++d) o[d] = 0.0;
+        continue;
+      }
+      if (visible > cap) {
+        free(logits);
+        cap = visible;
+        logits = (double*)malloc(sizeof(double) * (size_t)cap);
+      }
+      for (int d = 0; d < D; ++d) qv[d] = g_half_table[q[row * D + d]];
+      double peak = -INFINITY;
+      for (long long t = 0; t < visible; ++t) {
+        const long long pid = bt[(long long)b * max_pages + t / page];
+        const uint16_t* kr = kc + ((pid * page + t % page) * Hkv + kvh) * (long long)D;
+        double s = 0.0;
+        for (int d = 0; d < D; ++d) s += qv[d] * g_half_table[kr[d]];
+        s *= scale;
+        logits[t] = s;
+        if (s > peak) peak = s;
+      }
+      double denom = 0.0;
+      for (int d = 0; d < D; ++d) acc[d] = 0.0;
+      for (long long t = 0; t < visible; ++t) {
+        const double w = exp(logits[t] - peak);
+        denom += w;
+        const long long pid = bt[(long long)b * max_pages + t / page];
+        const uint16_t* vr = vc + ((pid * page + t % page) * Hkv + kvh) * (long long)D;
+        for (int d = 0; d < D; ++d) acc[d] += w * g_half_table[vr[d]];
+      }
+      for (int d = 0; d < D; ++d) o[d] = acc[d] / denom;
+    }
+    free(logits);
+    free(qv);
+    free(acc);
+  }
+  return status;
+}

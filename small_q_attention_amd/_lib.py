@@ -1,0 +1,107 @@
+"""ctypes binding of ``libsqa.so`` (C ABI in ``include/sqa.h``) and the torch custom op.
+
+There is no fallback: if the library is missing or fails to load, every entry
+point raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+from . import build as _build
+
+_LOCK = threading.Lock()
+_LIB = None
+
+SQA_OK = 0
+
+# (name, restype, argtypes) for every symbol include/sqa.h declares.
+_C = ctypes
+_SIGNATURES = [
+    ("sqa_plan_splits", _C.c_int,
+     [_C.c_int] * 8 + [_C.POINTER(_C.c_int), _C.POINTER(_C.c_int)]),
+    ("sqa_workspace_bytes", _C.c_size_t, [_C.c_int] * 5),
+    ("sqa_paged_mtp_attention", _C.c_int,
+     [_C.c_void_p] * 7 + [_C.c_size_t] + [_C.c_int] * 5 + [_C.c_int64] + [_C.c_int] * 4
+     + [_C.c_void_p, _C.c_void_p]),
+    ("sqa_device_cu_count", _C.c_int, [_C.c_int]),
+    ("sqa_last_error", _C.c_char_p, []),
+    ("sqa_version", _C.c_char_p, []),
+]
+EXPORTED = [name for name, _, _ in _SIGNATURES]
+
+
+def library_path() -> Path:
+    return _build.LIB_PATH
+
+
+def load(verbose: bool = False, build_if_missing: bool = True):
+    """Load ``libsqa.so`` (building it first if it does not exist yet)."""
+    global _LIB
+    with _LOCK:
+        if _LIB is None:
+            path = _build.LIB_PATH
+            if not path.exists():
+                if not build_if_missing:
+                    raise RuntimeError(f"{path} is not built; run small_q_attention_amd.build")
+                _build.build(verbose=verbose)
+            try:
+                lib = ctypes.CDLL(str(path))
+            except OSError as exc:
+                raise RuntimeError(f"cannot load {path}: {exc}") from exc
+            for name, res, args in _SIGNATURES:
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _LIB = lib
+        return _LIB
+
+
+def last_error(lib) -> str:
+    msg = lib.sqa_last_error()
+    return msg.decode() if msg else "unknown error"
+
+
+def plan_splits(device_index: int, batch: int, q_len: int, num_query_heads: int,
+                num_kv_heads: int, max_seq_len: int, max_pages: int, chunk_keys: int):
+    lib = load()
+    ns, pps = ctypes.c_int(0), ctypes.c_int(0)
+    rc = lib.sqa_plan_splits(device_index, batch, q_len, num_query_heads, num_kv_heads,
+                             max_seq_len, max_pages, chunk_keys, ctypes.byref(ns), ctypes.byref(pps))
+    if rc != SQA_OK:
+        raise RuntimeError(f"sqa_plan_splits failed: {last_error(lib)}")
+    return ns.value, pps.value
+
+
+def workspace_bytes(batch: int, q_len: int, num_query_heads: int, num_kv_heads: int,
+                    num_splits: int) -> int:
+    return int(load().sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, num_splits))
+
+
+def launch(query, key_cache, value_cache, block_tables, seq_lens, output, workspace,
+           num_splits: int, pages_per_split: int, stream_handle: int, timing_events=None):
+    """Call ``sqa_paged_mtp_attention`` on raw device pointers of torch tensors."""
+    lib = load()
+    b, q_len, hq, d = query.shape
+    ev = None
+    if timing_events is not None:
+        ev = (ctypes.c_void_p * 3)(*[ctypes.c_void_p(int(e)) for e in timing_events])
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    rc = lib.sqa_paged_mtp_attention(
+        query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+        block_tables.data_ptr(), seq_lens.data_ptr(), output.data_ptr(),
+        ws_ptr, ws_bytes, b, q_len, hq, key_cache.shape[2], d,
+        key_cache.shape[0], key_cache.shape[1], block_tables.shape[1],
+        num_splits, pages_per_split, stream_handle, ev)
+    if rc != SQA_OK:
+        raise RuntimeError(f"sqa_paged_mtp_attention failed: {last_error(lib)}")
+
+
+def custom_op():
+    """The ``sqa::paged_mtp_attention`` torch custom op (registered on first use)."""
+    from . import _op
+
+    return _op.paged_mtp_attention

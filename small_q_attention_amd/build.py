@@ -1,0 +1,78 @@
+"""Builds ``libsqa.so`` (the gfx950 HIP library) in-tree with hipcc.
+
+The reference JIT-compiles its CUDA source through
+``torch.utils.cpp_extension.load`` on the first ``load_vN`` call
+(``/root/reference/src/small_q_attention/cuda.py:16-37``). Here the library is
+one plain shared object with a C ABI, compiled once for gfx950 by hipcc; every
+``load_vN`` returns a handle to the same library.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+CSRC = PKG_DIR / "csrc"
+INCLUDE = REPO_DIR / "include"
+LIB_PATH = PKG_DIR / "libsqa.so"
+SOURCES = [CSRC / "sqa_kernels.hip", CSRC / "sqa_capi.hip"]
+HEADERS = [CSRC / "sqa_internal.h", INCLUDE / "sqa.h"]
+ARCH = "gfx950"
+
+
+def hipcc_path() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found; ROCm is required to build libsqa.so")
+
+
+def build_command(output: Path = LIB_PATH):
+    return [
+        hipcc_path(),
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        # Packed fp32 VALU ops are kept out of the generated code.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        f"-I{INCLUDE}",
+        f"-I{CSRC}",
+        *[str(s) for s in SOURCES],
+        "-o", str(output),
+    ]
+
+
+def is_stale() -> bool:
+    if not LIB_PATH.exists():
+        return True
+    built = LIB_PATH.stat().st_mtime
+    return any(p.stat().st_mtime > built for p in SOURCES + HEADERS)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile ``libsqa.so`` (always; callers decide whether a rebuild is due)."""
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = build_command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    errors = [ln for ln in (res.stdout + res.stderr).splitlines()
+              if "packed-fp32-ops" not in ln and "unknown target feature" not in ln.lower()]
+    if res.returncode != 0:
+        raise RuntimeError("hipcc failed building libsqa.so:\n" + "\n".join(errors))
+    if verbose and errors:
+        print("\n".join(errors), flush=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print(LIB_PATH)

@@ -1,0 +1,197 @@
+// C ABI of libsqa.so (declared in include/sqa.h). Validates arguments, plans
+// the split-KV decomposition and launches the gfx950 kernels of
+// sqa_kernels.hip on the caller's stream. Allocates nothing.
+#include "sqa.h"
+#include "sqa_internal.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(SQA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Target workgroups per compute unit for the automatic plan, and the fewest
+// pages one split may own (two pages per wave keeps the prefetch busy).
+constexpr int kWgPerCu = 2;
+constexpr int kMinPagesPerSplit = 2 * sqa::kWaves;
+
+std::mutex g_cu_mutex;
+std::vector<int> g_cu_count;  // cached per device
+
+long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+extern "C" {
+
+const char* sqa_last_error(void) { return g_last_error.c_str(); }
+
+const char* sqa_version(void) { return "sqa 0.1.0 gfx950"; }
+
+int sqa_device_cu_count(int device) {
+  std::lock_guard<std::mutex> lock(g_cu_mutex);
+  if (device < 0) return -1;
+  if ((int)g_cu_count.size() <= device) g_cu_count.resize(device + 1, 0);
+  if (g_cu_count[device] == 0) {
+    int n = 0;
+    hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess || n <= 0) {
+      hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
+      return -1;
+    }
+    g_cu_count[device] = n;
+  }
+  return g_cu_count[device];
+}
+
+int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int num_kv_heads,
+                    int max_seq_len, int max_pages, int chunk_keys, int* num_splits,
+                    int* pages_per_split) {
+  if (!num_splits || !pages_per_split) return fail(SQA_ERR_INVALID, "null output pointer");
+  if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_query_heads <= 0 || max_pages <= 0)
+    return fail(SQA_ERR_INVALID, "batch, q_len, heads and max_pages must be positive");
+  if (chunk_keys < 0) return fail(SQA_ERR_INVALID, "chunk_keys must be >= 0");
+  long long pages = max_pages;
+  if (max_seq_len > 0) {
+    const long long need = ceil_div(max_seq_len, sqa::kPageSize);
+    pages = need < pages ? need : pages;
+  }
+  long long pps;
+  if (chunk_keys > 0) {
+    pps = ceil_div(chunk_keys, sqa::kPageSize);
+  } else {
+    int cus = sqa_device_cu_count(device);
+    if (cus <= 0) return SQA_ERR_HIP;
+    const long long items = (long long)batch * num_kv_heads;
+    const long long target = (long long)cus * kWgPerCu;
+    const long long splits = ceil_div(target, items);
+    pps = ceil_div(pages, splits);
+    if (pps < kMinPagesPerSplit) pps = kMinPagesPerSplit;
+  }
+  if (pps > pages) pps = pages;
+  if (pps < 1) pps = 1;
+  long long splits = ceil_div(pages, pps);
+  if (splits < 1) splits = 1;
+  if ((long long)batch * num_kv_heads * splits > 0x7fffffffLL)
+    return fail(SQA_ERR_INVALID, "grid too large");
+  *num_splits = (int)splits;
+  *pages_per_split = (int)pps;
+  return SQA_OK;
+}
+
+size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv_heads,
+                           int num_splits) {
+  if (num_splits <= 1 || batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_query_heads <= 0)
+    return 0;
+  const size_t rows = (size_t)q_len * (num_query_heads / num_kv_heads);
+  const size_t items = (size_t)batch * num_kv_heads * num_splits * rows;
+  return items * (sqa::kHeadDim + 2) * sizeof(float);
+}
+
+int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void* value_cache,
+                            const int32_t* block_tables, const int32_t* seq_lens, void* output,
+                            void* workspace, size_t workspace_bytes, int batch, int q_len,
+                            int num_query_heads, int num_kv_heads, int head_dim,
+                            int64_t num_pages, int page_size, int max_pages, int num_splits,
+                            int pages_per_split, void* stream, void** timing_events) {
+  if (!query || !key_cache || !value_cache || !block_tables || !seq_lens || !output)
+    return fail(SQA_ERR_INVALID, "null tensor pointer");
+  if (batch <= 0 || q_len <= 0 || num_query_heads <= 0 || num_kv_heads <= 0)
+    return fail(SQA_ERR_INVALID, "batch, q_len and head counts must be positive");
+  if (num_pages <= 0 || max_pages <= 0)
+    return fail(SQA_ERR_INVALID, "empty KV cache is not supported");
+  if (num_query_heads % num_kv_heads != 0)
+    return fail(SQA_ERR_INVALID, "num_query_heads must be divisible by num_kv_heads");
+  if (head_dim != sqa::kHeadDim)
+    return fail(SQA_ERR_UNSUPPORTED, "head_dim must be %d (got %d)", sqa::kHeadDim, head_dim);
+  if (page_size != sqa::kPageSize)
+    return fail(SQA_ERR_UNSUPPORTED, "page_size must be %d (got %d)", sqa::kPageSize, page_size);
+  const int group = num_query_heads / num_kv_heads;
+  const long long rows = (long long)q_len * group;
+  if (rows > sqa::kMaxRows)
+    return fail(SQA_ERR_UNSUPPORTED, "q_len * group = %lld exceeds %d", rows, sqa::kMaxRows);
+  if (num_splits <= 0 || pages_per_split <= 0)
+    return fail(SQA_ERR_INVALID, "num_splits and pages_per_split must be positive");
+  // A plan covering fewer than max_pages pages (built from a known
+  // max_seq_len) processes only the first num_splits * pages_per_split pages of
+  // each sequence, as the reference launchers do with their max_seq_len.
+  if ((long long)batch * num_kv_heads * num_splits > 0x7fffffffLL)
+    return fail(SQA_ERR_INVALID, "grid too large");
+  const size_t need = sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, num_splits);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(SQA_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
+                workspace ? workspace_bytes : (size_t)0);
+
+  hipStream_t s = (hipStream_t)stream;
+  hipEvent_t* ev = (hipEvent_t*)timing_events;
+
+  sqa::PartialArgs pa;
+  pa.q = (const _Float16*)query;
+  pa.k = (const _Float16*)key_cache;
+  pa.v = (const _Float16*)value_cache;
+  pa.block_tables = block_tables;
+  pa.seq_lens = seq_lens;
+  pa.out = (_Float16*)output;
+  const size_t items = (size_t)batch * num_kv_heads * num_splits * rows;
+  pa.part_o = num_splits > 1 ? (float*)workspace : nullptr;
+  pa.part_ml = num_splits > 1 ? (float*)workspace + items * sqa::kHeadDim : nullptr;
+  pa.num_pages = num_pages;
+  pa.batch = batch;
+  pa.q_len = q_len;
+  pa.hq = num_query_heads;
+  pa.hkv = num_kv_heads;
+  pa.group = group;
+  pa.rows = (int)rows;
+  pa.max_pages = max_pages;
+  pa.pages_per_split = pages_per_split;
+  pa.num_splits = num_splits;
+  pa.scale_log2 = (float)(1.4426950408889634 / sqrt((double)head_dim));
+
+  hipError_t e;
+  if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+  if ((e = sqa::launch_partial(pa, s)) != hipSuccess) return hip_fail(e, "partial kernel launch");
+  if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+  if (num_splits > 1) {
+    sqa::MergeArgs ma;
+    ma.part_o = pa.part_o;
+    ma.part_ml = pa.part_ml;
+    ma.seq_lens = seq_lens;
+    ma.out = pa.out;
+    ma.batch = batch;
+    ma.q_len = q_len;
+    ma.hq = num_query_heads;
+    ma.hkv = num_kv_heads;
+    ma.group = group;
+    ma.rows = (int)rows;
+    ma.max_pages = max_pages;
+    ma.pages_per_split = pages_per_split;
+    ma.num_splits = num_splits;
+    if ((e = sqa::launch_merge(ma, s)) != hipSuccess) return hip_fail(e, "merge kernel launch");
+  }
+  if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+  return SQA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,259 @@
+"""Drop-in op boundary: ``load_v0..load_v5`` and ``forward_v0..forward_v5``.
+
+Mirrors ``/root/reference/src/small_q_attention/cuda.py`` (same names,
+parameter order, defaults and exception classes) over one gfx950 library,
+``libsqa.so``, reached through the ``sqa::paged_mtp_attention`` torch custom op.
+All six ``forward_vN`` run the same HIP kernels (split-KV partial kernel with
+GQA and draft-row reuse, plus the log-sum-exp merge kernel); the version
+number only selects which of the reference's argument checks apply.
+
+Validation order follows the reference: ``RuntimeError`` when no GPU is
+present (``cuda.py:65-66``); ``ValueError`` for inputs off the device,
+non-contiguous, not fp16, an unsupported ``q_len`` or ``head_dim``
+(``cuda.py:67-77``), a GQA group other than 4 for v3-v5 (``:208-209``),
+``chunk_keys <= 0`` (``:149-150``) and ``token_group`` not in {2, 4}
+(``:329-330``); then ``RuntimeError`` for the launcher's shape checks
+(``csrc/small_q_attention_ext.cu:976-1002``).
+
+Deliberate contract differences:
+* ``q_len`` 16 is accepted (the reference allows 2, 4, 8): ``q_len * group``
+  must be at most 64 rows.
+* ``page_size`` must be 16 and ``head_dim`` 128 (the reference's launchers take
+  any page size, but every reference caller uses 16).
+* ``chunk_keys=None`` selects the automatic split plan (from the CU count).
+* ``token_group`` (v5) is validated and otherwise ignored: every draft row
+  already shares one K/V load.
+* ``verbose`` echoes the hipcc command if the library has to be built.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+from . import _lib
+
+SUPPORTED_Q_LENS = (2, 4, 8, 16)
+HEAD_DIM = 128
+PAGE_SIZE = 16
+MAX_ROWS = 64
+
+
+def _load(verbose: bool = False):
+    return _lib.load(verbose=bool(verbose))
+
+
+class _Module:
+    """What ``load_vN`` returns: the reference's extension-module attribute names."""
+
+    def __init__(self, lib):
+        self.lib = lib
+
+    def forward(self, query, key_cache, value_cache, block_tables, seq_lens, page_size):
+        return _run(query, key_cache, value_cache, block_tables, seq_lens, page_size, None, 0)
+
+    def forward_v1(self, query, key_cache, value_cache, block_tables, seq_lens, page_size):
+        return _run(query, key_cache, value_cache, block_tables, seq_lens, page_size, None, 0)
+
+    def forward_v2(self, query, key_cache, value_cache, block_tables, seq_lens, page_size,
+                   chunk_keys):
+        return _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
+                    chunk_keys, -1)
+
+    def forward_v3(self, query, key_cache, value_cache, block_tables, seq_lens, page_size,
+                   chunk_keys, max_seq_len):
+        return _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
+                    chunk_keys, max_seq_len or -1)
+
+    forward_v4 = forward_v3
+
+    def forward_v5(self, query, key_cache, value_cache, block_tables, seq_lens, page_size,
+                   chunk_keys, token_group, max_seq_len):
+        return _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
+                    chunk_keys, max_seq_len or -1)
+
+
+_MODULE = None
+
+
+def _module(verbose):
+    global _MODULE
+    if _MODULE is None:
+        _MODULE = _Module(_load(verbose))
+    return _MODULE
+
+
+def load_v0(verbose: bool = False):
+    """Load ``libsqa.so`` (building it on first use if absent)."""
+    return _module(verbose)
+
+
+load_v1 = load_v2 = load_v3 = load_v4 = load_v5 = load_v0
+
+
+def _check_python_contract(tag, query, key_cache, value_cache, block_tables, seq_lens,
+                           gqa4: bool):
+    """The reference's Python-side checks (``cuda.py:65-77,85-95,138-150,197-211``)."""
+    import torch
+
+    if not torch.cuda.is_available():
+        raise RuntimeError(f"a ROCm GPU is required for the {tag} kernel")
+    tensors = (query, key_cache, value_cache, block_tables, seq_lens)
+    if any(not t.is_cuda for t in tensors):
+        raise ValueError(f"all {tag} inputs must be GPU tensors")
+    if any(t.device != query.device for t in tensors):
+        raise ValueError(f"all {tag} inputs must be on the same device")
+    if any(not t.is_contiguous() for t in tensors):
+        raise ValueError(f"all {tag} inputs must be contiguous")
+    if any(t.dtype != torch.float16 for t in (query, key_cache, value_cache)):
+        raise ValueError(f"{tag} requires FP16 Q/K/V")
+    if query.ndim < 2 or query.shape[1] not in SUPPORTED_Q_LENS:
+        raise ValueError(f"{tag} supports q_len 2, 4, 8 or 16")
+    if query.shape[-1] != HEAD_DIM:
+        raise ValueError(f"{tag} supports head_dim 128")
+    if gqa4:
+        if (key_cache.ndim < 3 or query.ndim < 3 or key_cache.shape[2] == 0
+                or query.shape[2] % key_cache.shape[2] != 0
+                or query.shape[2] // key_cache.shape[2] != 4):
+            raise ValueError(f"{tag} requires a GQA group size of exactly 4 (Hq/Hkv = 32/8)")
+
+
+def _check_launcher_contract(query, key_cache, value_cache, block_tables, seq_lens, page_size):
+    """The launcher's checks (``csrc/small_q_attention_ext.cu:976-1002``) -> RuntimeError."""
+    import torch
+
+    if query.ndim != 4:
+        raise RuntimeError("query must be [B, Q, Hq, D]")
+    if key_cache.ndim != 4:
+        raise RuntimeError("key_cache must be [P, page, Hkv, D]")
+    if value_cache.shape != key_cache.shape:
+        raise RuntimeError("value_cache shape mismatch")
+    if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise RuntimeError("block_tables and seq_lens must be int32")
+    if block_tables.ndim != 2:
+        raise RuntimeError("block_tables must be [B, max_pages]")
+    batch, q_len, hq, dim = query.shape
+    num_pages, cache_page, hkv, kdim = key_cache.shape
+    if hkv == 0 or hq % hkv != 0:
+        raise RuntimeError("Hq must be divisible by Hkv")
+    if kdim != dim:
+        raise RuntimeError("key_cache head_dim does not match query")
+    if int(page_size) != cache_page:
+        raise RuntimeError("page_size argument does not match cache")
+    if seq_lens.numel() != batch:
+        raise RuntimeError("seq_lens batch mismatch")
+    if block_tables.shape[0] != batch:
+        raise RuntimeError("block_tables batch mismatch")
+    if num_pages <= 0 or block_tables.shape[1] <= 0:
+        raise RuntimeError("empty KV cache is not supported")
+    if batch == 0:
+        raise RuntimeError("batch must be positive")
+    if cache_page != PAGE_SIZE:
+        raise ValueError("this build supports page_size 16")
+    if q_len * (hq // hkv) > MAX_ROWS:
+        raise ValueError("q_len * (Hq / Hkv) must be at most 64")
+
+
+def _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
+         chunk_keys: Optional[int], max_seq_len: int):
+    """Plan the split-KV grid and run the custom op.
+
+    ``max_seq_len``: > 0 known; -1 measure with ``seq_lens.max().item()`` (a host
+    sync, as the reference v2 launcher always does and v3-v5 do for 0,
+    ``csrc/small_q_attention_ext.cu:1097,1173-1176``); 0 unknown, plan over the
+    whole block-table row (no sync).
+    """
+    _check_launcher_contract(query, key_cache, value_cache, block_tables, seq_lens, page_size)
+    if max_seq_len == -1:
+        max_seq_len = int(seq_lens.max().item())
+        if max_seq_len <= 0:
+            raise RuntimeError("seq_lens must be positive")
+    batch, q_len, hq, _ = query.shape
+    hkv = key_cache.shape[2]
+    ck = 0 if chunk_keys is None else int(chunk_keys)
+    num_splits, pps = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv,
+                                       int(max_seq_len), block_tables.shape[1], ck)
+    return _lib.custom_op()(query, key_cache, value_cache, block_tables, seq_lens,
+                            num_splits, pps)
+
+
+def paged_mtp_attention(query, key_cache, value_cache, block_tables, seq_lens,
+                        page_size: int = PAGE_SIZE, max_seq_len: int = 0,
+                        chunk_keys: Optional[int] = None):
+    """Native entry: automatic split plan, no host sync unless ``max_seq_len < 0``.
+
+    ``max_seq_len`` > 0 promises every ``seq_lens[b] <= max_seq_len``; 0 plans
+    over the whole block-table row.
+    """
+    _check_python_contract("sqa", query, key_cache, value_cache, block_tables, seq_lens, False)
+    if chunk_keys is not None and chunk_keys <= 0:
+        raise ValueError("chunk_keys must be positive")
+    _load()
+    return _run(query, key_cache, value_cache, block_tables, seq_lens, page_size, chunk_keys,
+                int(max_seq_len))
+
+
+def forward_v0(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
+               verbose: bool = False):
+    """Reference ``forward_v0`` (``cuda.py:61-78``); automatic split plan, no host sync."""
+    _check_python_contract("v0", query, key_cache, value_cache, block_tables, seq_lens, False)
+    return load_v0(verbose=verbose).forward(query, key_cache, value_cache, block_tables,
+                                            seq_lens, page_size)
+
+
+def forward_v1(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
+               verbose: bool = False):
+    """Reference ``forward_v1`` (``cuda.py:81-96``); same kernels as v0."""
+    _check_python_contract("v1", query, key_cache, value_cache, block_tables, seq_lens, False)
+    return load_v1(verbose=verbose).forward_v1(query, key_cache, value_cache, block_tables,
+                                               seq_lens, page_size)
+
+
+def forward_v2(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
+               chunk_keys: Optional[int] = 512, verbose: bool = False):
+    """Reference ``forward_v2`` (``cuda.py:120-153``): ``chunk_keys`` KV entries per split."""
+    _check_python_contract("v2", query, key_cache, value_cache, block_tables, seq_lens, False)
+    if chunk_keys is not None and chunk_keys <= 0:
+        raise ValueError("chunk_keys must be positive")
+    return load_v2(verbose=verbose).forward_v2(query, key_cache, value_cache, block_tables,
+                                               seq_lens, page_size, chunk_keys)
+
+
+def forward_v3(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
+               chunk_keys: Optional[int] = 512, max_seq_len: int = 0, verbose: bool = False):
+    """Reference ``forward_v3`` (``cuda.py:177-214``); ``max_seq_len=0`` measures it (sync)."""
+    _check_python_contract("v3", query, key_cache, value_cache, block_tables, seq_lens, True)
+    if chunk_keys is not None and chunk_keys <= 0:
+        raise ValueError("chunk_keys must be positive")
+    return load_v3(verbose=verbose).forward_v3(query, key_cache, value_cache, block_tables,
+                                               seq_lens, page_size, chunk_keys, max_seq_len)
+
+
+def forward_v4(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
+               chunk_keys: Optional[int] = 512, max_seq_len: int = 0, verbose: bool = False):
+    """Reference ``forward_v4`` (``cuda.py:238-273``); same kernels as v3."""
+    _check_python_contract("v4", query, key_cache, value_cache, block_tables, seq_lens, True)
+    if chunk_keys is not None and chunk_keys <= 0:
+        raise ValueError("chunk_keys must be positive")
+    return load_v4(verbose=verbose).forward_v4(query, key_cache, value_cache, block_tables,
+                                               seq_lens, page_size, chunk_keys, max_seq_len)
+
+
+def forward_v5(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
+               chunk_keys: Optional[int] = 512, token_group: int = 2, max_seq_len: int = 0,
+               verbose: bool = False):
+    """Reference ``forward_v5`` (``cuda.py:297-336``); ``token_group`` checked, then unused."""
+    _check_python_contract("v5", query, key_cache, value_cache, block_tables, seq_lens, True)
+    if token_group not in (2, 4):
+        raise ValueError("v5 token_group must be 2 or 4")
+    if chunk_keys is not None and chunk_keys <= 0:
+        raise ValueError("chunk_keys must be positive")
+    return load_v5(verbose=verbose).forward_v5(query, key_cache, value_cache, block_tables,
+                                               seq_lens, page_size, chunk_keys, token_group,
+                                               max_seq_len)
+
+
+__all__ = [
+    "load_v0", "load_v1", "load_v2", "load_v3", "load_v4", "load_v5",
+    "forward_v0", "forward_v1", "forward_v2", "forward_v3", "forward_v4", "forward_v5",
+    "paged_mtp_attention",
+]
