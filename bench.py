@@ -1,0 +1,211 @@
+"""Benchmark of the paged small-q attention op on one MI355X.
+
+One step = one call of the op over one batch (inputs resident in HBM). The
+workload is BASELINE cfg3 (B16, q_len 8, KV 32768, Hq/Hkv 32/8, d 128,
+page 16, 1% of K scaled x4, random page table over a 2x pool): the shape the
+BASELINE target is quoted at (KV = 32K, batch 16) and the largest single-GPU
+config; its 2.15 GB of KV cannot sit in the 256 MB MALL, so the figure is HBM.
+
+Prints ONE JSON line (the driver's contract). ``value`` is KV GB/s of the whole
+call (KV bytes / mean call time); ``roofline`` uses the partial kernel's own
+mean duration from HIP events the library records around it on the launch
+stream; ``cpu_baseline`` times the loop-faithful CPU oracle on a bounded
+sample of the same workload. ``per_q_len`` repeats the timing at q_len 2, 4
+and 16 on the same KV pool.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, AMD published peak
+METRIC = "µs/call + achieved HBM GB/s (% peak), q_len 2/4/8, KV 8K/32K, batch 1/4/16"
+
+
+def _parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU-baseline sample duration")
+    ap.add_argument("--no-per-q", action="store_true", help="skip the q_len 2/4/16 extras")
+    return ap.parse_args()
+
+
+def _events(torch, n):
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    for e in evs:
+        e.record()  # creates the underlying hipEvent_t
+    torch.cuda.synchronize()
+    return evs
+
+
+def time_calls(torch, lib, tensors, plan, steps, warmup):
+    """Time `steps` calls through the C ABI with a preallocated workspace.
+
+    Returns (ms per call over the bracketed region, mean partial-kernel ms,
+    mean merge-kernel ms).
+    """
+    q, k, v, bt, sl = tensors
+    num_splits, pps = plan
+    out = torch.empty_like(q)
+    nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], num_splits)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    stream = torch.cuda.current_stream()
+    handle = stream.cuda_stream
+    for _ in range(warmup):
+        lib.launch(q, k, v, bt, sl, out, ws, num_splits, pps, handle)
+    kev = _events(torch, 3 * steps)
+    start, end = _events(torch, 2)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(steps):
+        lib.launch(q, k, v, bt, sl, out, ws, num_splits, pps, handle,
+                   timing_events=[e.cuda_event for e in kev[3 * i:3 * i + 3]])
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    part = [kev[3 * i].elapsed_time(kev[3 * i + 1]) for i in range(steps)]
+    merge = [kev[3 * i + 1].elapsed_time(kev[3 * i + 2]) for i in range(steps)]
+    return total_ms / steps, statistics.mean(part), statistics.mean(merge), out
+
+
+def cpu_baseline(torch, tensors, case, target_s):
+    """Loop-faithful CPU oracle on whole sequences of the workload until ~target_s."""
+    import oracle
+
+    q, k, v, bt, sl = tensors
+    page = case.page_size
+    done, elapsed, kv_done = 0, 0.0, 0
+    while done < case.batch and (elapsed < target_s or done == 0):
+        b = done
+        n = -(-int(case.seq_lens[b]) // page)
+        ids = bt[b, :n].long()
+        kc = k.index_select(0, ids).float().cpu()
+        vc = v.index_select(0, ids).float().cpu()
+        qc = q[b:b + 1].float().cpu()
+        btc = torch.arange(n, dtype=torch.int32).unsqueeze(0)
+        slc = sl[b:b + 1].cpu()
+        t0 = time.perf_counter()
+        oracle.paged_mtp_attention_reference(qc, kc, vc, btc, slc, page, case.num_kv_heads)
+        elapsed += time.perf_counter() - t0
+        kv_done += int(case.seq_lens[b]) * case.num_kv_heads * case.head_dim * 4
+        done += 1
+    per_seq_s = elapsed / done
+    return {
+        "value": round(kv_done / elapsed / 1e9, 4),
+        "unit": "GB/s (KV bytes / CPU time)",
+        "us_per_call": round(per_seq_s * case.batch * 1e6, 1),
+        "cores": int(torch.get_num_threads()),
+        "kind": "port",
+        "sample": (f"{done} of {case.batch} sequences of the workload (full KV length "
+                   f"{case.seq_lens[0]}, all {case.num_query_heads} heads), fp32 on .float() "
+                   f"copies; us_per_call extrapolates to the whole batch"),
+        "cpu_model": _cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def _cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
+              "multi-GPU path. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from small_q_attention_amd import _lib, inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    lib = _lib.load(build_if_missing=False)
+    case = inputs.baseline_configs()["cfg3"]
+    tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
+    q, k, v, bt, sl = tensors
+    plan = _lib.plan_splits(0, case.batch, case.q_len, case.num_query_heads, case.num_kv_heads,
+                            case.max_seq_len, bt.shape[1], 0)
+    ms, part_ms, merge_ms, out = time_calls(torch, _lib, tensors, plan, args.steps, args.warmup)
+    if not torch.isfinite(out).all():
+        raise SystemExit("non-finite output")
+    kvb = inputs.kv_bytes(case.seq_lens, case.num_kv_heads, case.head_dim)
+    value = kvb / (ms * 1e-3) / 1e9
+    achieved = kvb / (part_ms * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "us_per_call": round(ms * 1e3, 2),
+        "pct_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 in/out, fp32 accumulate",
+        "data": "synthetic: N(0,1) fp16 Q/K/V drawn on the device, seeded",
+        "config": {
+            "workload": "cfg3: B16 q_len8 KV32768 Hq/Hkv32/8 d128 page16, K x4 on 1% of slots, "
+                        "random page table over a 2x pool",
+            "batch": case.batch, "q_len": case.q_len, "kv_len": case.seq_lens[0],
+            "num_splits": plan[0], "pages_per_split": plan[1],
+            "kv_bytes": kvb, "alg_bytes": inputs.alg_bytes(case),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": None,
+            "kernel": "sqa_partial_kernel",
+            "kernel_us": round(part_ms * 1e3, 2),
+            "merge_us": round(merge_ms * 1e3, 2),
+        },
+    }
+    if not args.no_per_q:
+        extra = {}
+        for ql in (2, 4, 16):
+            g = torch.Generator(device="cuda").manual_seed(100 + ql)
+            qx = torch.randn(case.batch, ql, case.num_query_heads, case.head_dim,
+                             generator=g, device="cuda", dtype=torch.float16)
+            planx = _lib.plan_splits(0, case.batch, ql, case.num_query_heads, case.num_kv_heads,
+                                     case.max_seq_len, bt.shape[1], 0)
+            msx, px, mx, _ = time_calls(torch, _lib, (qx, k, v, bt, sl), planx, args.steps,
+                                        args.warmup)
+            extra[f"q{ql}"] = {"us_per_call": round(msx * 1e3, 2),
+                               "kv_GBps": round(kvb / (msx * 1e-3) / 1e9, 1),
+                               "kernel_us": round(px * 1e3, 2),
+                               "kernel_frac": round(kvb / (px * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+        result["per_q_len"] = extra
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, tensors, case, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

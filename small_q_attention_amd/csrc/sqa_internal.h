@@ -37,12 +37,15 @@ struct MergeArgs {
   int max_pages, pages_per_split, num_splits;
 };
 
-// Waves per workgroup of the partial kernel; the waves of one workgroup split
-// the pages of one (sequence, kv head, split) and merge through LDS.
-constexpr int kWaves = 4;
+// Waves per workgroup of the partial kernel. The waves of one workgroup serve
+// different kv heads (and, for 64 rows, the two 32-row halves of a head) of
+// the same (sequence, split), walking the same pages together.
+constexpr int kWgWaves = 8;
 
 // Number of 16-row blocks (1, 2 or 4) for `rows` query rows.
 inline int row_blocks(int rows) { return rows <= 16 ? 1 : (rows <= 32 ? 2 : 4); }
+// Waves per kv head: one up to 32 rows, two (32 rows each) up to 64.
+inline int row_groups(int rows) { return rows <= 32 ? 1 : 2; }
 
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream);
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream);

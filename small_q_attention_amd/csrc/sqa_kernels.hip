@@ -64,14 +64,21 @@ struct WaveState {
   float l[NB];     // partial row sum over this lane's tokens
 };
 
+// Buffer-resource word 3 for gfx9-family raw (untyped, 32-bit) accesses.
+constexpr int kBufferFlags = 0x00020000;
+// Cache-policy operand of the K/V buffer loads: non-temporal (read once).
+constexpr int kStreamAux = 2;
+
 __device__ __forceinline__ int clamp_page(int pid, long long num_pages) {
   return (pid >= 0 && (long long)pid < num_pages) ? pid : 0;
 }
 
+// sm_q: Q fragments in LDS, [nb][kk][lane] (the B-operand layout), so they cost
+// no registers across the page loop.
 template <int NB>
-__device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, const h8 (&qf)[NB][4],
-                                             const int (&vis)[NB], int tok0, int len, bool masked,
-                                             float scale_log2) {
+__device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, const h8* sm_q,
+                                             int lane, const int (&vis)[NB], int tok0, int len,
+                                             bool masked, float scale_log2) {
   // Scores S^T[token][row] for this page.
   f4 s[NB];
 #pragma unroll
@@ -79,8 +86,9 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, co
     s[nb] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      s[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, pg.k[kk]), qf[nb][kk],
-                                                    s[nb], 0, 0, 0);
+      const h8 qf = sm_q[(nb * 4 + kk) * 64 + lane];
+      s[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, pg.k[kk]), qf, s[nb],
+                                                    0, 0, 0);
     }
     s[nb] *= scale_log2;
   }
@@ -149,20 +157,36 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, co
   }
 }
 
-template <int NB, int NW>
-__global__ __launch_bounds__(NW * 64) void sqa_partial_kernel(PartialArgs a) {
+// One workgroup = one (sequence b, split) x kWgWaves waves. Wave w serves kv
+// head kvh_group * (kWgWaves / RG) + w / RG and row block w % RG of it (RG = 2
+// splits 64 rows into two waves of 32). All waves walk the same pages in the
+// same order, so the per-head 256-byte slices of each page are requested
+// together and HBM sees whole pages. Each wave keeps its own softmax state
+// and writes its own partial (or, with a single split, the output).
+// With RG = 1 every K/V byte is read by one wave only, so the loads are
+// non-temporal; with RG = 2 the two waves of a head read the same bytes and
+// the loads keep the default policy so the second read hits in L2.
+template <int NB, int RG, int D>
+__global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs a) {
+  constexpr int kHeadsPerWg = kWgWaves / RG;
+  constexpr int kAux = RG == 1 ? kStreamAux : 0;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g16 = lane >> 4;
   const int l16 = lane & 15;
 
-  // blockIdx.x = ((b * num_splits + split) * hkv + kvh): the kv heads of one
-  // page range are neighbours in dispatch order.
+  // blockIdx.x = (b * num_splits + split) * head_groups + head_group.
+  const int head_groups = (a.hkv + kHeadsPerWg - 1) / kHeadsPerWg;
   int wg = blockIdx.x;
-  const int kvh = wg % a.hkv;
-  wg /= a.hkv;
+  const int hgrp = wg % head_groups;
+  wg /= head_groups;
   const int split = wg % a.num_splits;
   const int b = wg / a.num_splits;
+  const int kvh = hgrp * kHeadsPerWg + wave / RG;
+  const int row0 = (wave % RG) * NB * 16;
+  // Waves past the last kv head (hkv not a multiple of kHeadsPerWg) or past
+  // the last row block idle but stay for the barrier.
+  const bool active = kvh < a.hkv && row0 < a.rows;
 
   int len = a.seq_lens[b];
   len = len < 0 ? 0 : len;
@@ -171,27 +195,27 @@ __global__ __launch_bounds__(NW * 64) void sqa_partial_kernel(PartialArgs a) {
   const int p_begin = split * a.pages_per_split;
   const int p_end = min(p_begin + a.pages_per_split, pages_used);
   const bool single = a.num_splits == 1;
-  if (p_begin >= p_end && !single) return;  // the merge kernel never reads this split
+  if (p_begin >= p_end && !single) return;  // uniform per workgroup; never merged
 
-  // Q fragments (B operand of the score MFMA) and per-row visible length.
-  h8 qf[NB][4];
+  // Q fragments of this wave's rows in LDS, [wave][nb][kk][lane] (B-operand
+  // layout). Each lane stores exactly the fragments it reads back.
+  __shared__ h8 sm_q[kWgWaves * NB * 4 * 64];
+  h8* my_q = sm_q + wave * NB * 4 * 64;
   int vis[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const int r = nb * 16 + l16;
-    if (r < a.rows) {
-      const int qi = r / a.group;
-      const int gg = r - qi * a.group;
-      const _Float16* qp =
-          a.q + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * kHeadDim + 8 * g16;
+    const int r = row0 + nb * 16 + l16;
+    const bool real = active && r < a.rows;
+    const int qi = real ? r / a.group : 0;
+    const int gg = real ? r - qi * a.group : 0;
+    const _Float16* qp =
+        a.q + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * kHeadDim + 8 * g16;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) qf[nb][kk] = *(const h8*)(qp + 32 * kk);
-      vis[nb] = len - a.q_len + 1 + qi;
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) qf[nb][kk] = h8{0, 0, 0, 0, 0, 0, 0, 0};
-      vis[nb] = 0;
+    for (int kk = 0; kk < 4; ++kk) {
+      my_q[(nb * 4 + kk) * 64 + lane] =
+          real ? *(const h8*)(qp + 32 * kk) : h8{0, 0, 0, 0, 0, 0, 0, 0};
     }
+    vis[nb] = real ? len - a.q_len + 1 + qi : 0;
   }
   // Pages whose last token index >= mask_from need the causal/tail mask.
   const int mask_from = len - a.q_len + 1;
@@ -205,106 +229,85 @@ __global__ __launch_bounds__(NW * 64) void sqa_partial_kernel(PartialArgs a) {
     for (int mb = 0; mb < 8; ++mb) st.acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const size_t tok_stride = (size_t)a.hkv * kHeadDim;         // elements between tokens
-  const size_t page_stride = (size_t)kPageSize * tok_stride;   // elements between pages
-  const size_t k_lane = (size_t)l16 * tok_stride + (size_t)kvh * kHeadDim + 8 * g16;
-  const size_t v_lane = (size_t)(4 * g16) * tok_stride + (size_t)kvh * kHeadDim + 8 * l16;
+  // K/V pages are read with buffer loads: the resource (4 SGPRs) is rebuilt per
+  // page at the page's base address and bounded to the page, and the lane
+  // offsets below stay in one VGPR each for the whole loop.
+  const int kvh_c = active ? kvh : 0;
+  const unsigned tok_bytes = (unsigned)a.hkv * kHeadDim * 2;   // bytes between tokens
+  const unsigned page_bytes = kPageSize * tok_bytes;           // bytes between pages
+  const unsigned k_lane = l16 * tok_bytes + kvh_c * kHeadDim * 2 + 16 * g16;
+  const unsigned v_lane = 4 * g16 * tok_bytes + kvh_c * kHeadDim * 2 + 16 * l16;
   const int32_t* bt_row = a.block_tables + (size_t)b * a.max_pages;
+  const int n_pages = active ? (p_end > p_begin ? p_end - p_begin : 0) : 0;
 
-  auto load_page = [&](int p, PageRegs& pg) {
-    const int pid = clamp_page(bt_row[p], a.num_pages);
-    const _Float16* kb = a.k + (size_t)pid * page_stride + k_lane;
-    const _Float16* vb = a.v + (size_t)pid * page_stride + v_lane;
+  // Page id of page p_begin + i (a scalar load), or -1 past the end. The index
+  // is clamped before the read so the block table is never read beyond the
+  // split's pages.
+  auto page_id = [&](int i) -> int {
+    const int ic = i < n_pages ? i : n_pages - 1;
+    const int pid = ic >= 0 ? clamp_page(bt_row[p_begin + ic], a.num_pages) : 0;
+    return i < n_pages ? pid : -1;
+  };
+  // pid < 0 gives a zero-length resource: the loads return zeros without
+  // touching memory, so every slot refill below is unconditional and the
+  // compiler's wait counts stay exact (one page retires per step). K/V are
+  // streamed once, so the loads are non-temporal.
+  auto load_page = [&](int pid, PageRegs& pg) {
+    const size_t off = pid >= 0 ? (size_t)pid * page_bytes : 0;
+    const int nrec = pid >= 0 ? (int)page_bytes : 0;
+    const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const char*)a.k + off), (short)0, nrec, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const char*)a.v + off), (short)0, nrec, kBufferFlags);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) pg.k[kk] = *(const u4*)(kb + 32 * kk);
+    for (int kk = 0; kk < 4; ++kk)
+      pg.k[kk] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * kk, 0, kAux);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) pg.v[e] = *(const u4*)(vb + e * tok_stride);
+    for (int e = 0; e < 4; ++e)
+      pg.v[e] = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane, e * tok_bytes, kAux);
   };
 
-  int p = p_begin + wave;
-  PageRegs cur;
-  if (p < p_end) load_page(p, cur);
-  for (; p < p_end; p += NW) {
-    PageRegs nxt;
-    const int pn = p + NW;
-    if (pn < p_end) load_page(pn, nxt);
-    const bool masked = (p + 1) * kPageSize > mask_from;
-    process_page<NB>(st, cur, qf, vis, p * kPageSize + 4 * g16, len, masked, a.scale_log2);
-    cur = nxt;
+  __syncthreads();  // sm_q written
+
+  // Ring of D pages in flight: page i is processed from slot i % D, which is
+  // then refilled with page i + D.
+  PageRegs ring[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) load_page(page_id(j), ring[j]);
+  int next_pid = page_id(D);
+  for (int i = 0; i < n_pages; i += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int ii = i + j;
+      if (ii < n_pages) {
+        const int p = p_begin + ii;
+        const bool masked = (p + 1) * kPageSize > mask_from;
+        process_page<NB>(st, ring[j], my_q, lane, vis, p * kPageSize + 4 * g16, len, masked,
+                         a.scale_log2);
+      }
+      const int pid = next_pid;
+      next_pid = page_id(ii + D + 1);
+      load_page(pid, ring[j]);
+    }
   }
+  if (!active) return;
 
   // Row sums over the four lane groups.
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) st.l[nb] = xor_sum(st.l[nb]);
 
-  float row_m[NB], row_l[NB];
-  if constexpr (NW == 1) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      row_m[nb] = st.m[nb];
-      row_l[nb] = st.l[nb];
-    }
-  } else {
-    __shared__ float sm_m[NW][NB * 16];
-    __shared__ float sm_l[NW][NB * 16];
-    __shared__ f4 sm_acc[8 * NB][64];
-    if (g16 == 0) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        sm_m[wave][nb * 16 + l16] = st.m[nb];
-        sm_l[wave][nb * 16 + l16] = st.l[nb];
-      }
-    }
-    __syncthreads();
-    float fac[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int r = nb * 16 + l16;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sm_m[w][r]);
-      const float mu = (mx == -INFINITY) ? 0.f : mx;
-      float lt = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) lt += sm_l[w][r] * fast_exp2(sm_m[w][r] - mu);
-      fac[nb] = fast_exp2(st.m[nb] - mu);
-      row_m[nb] = mx;
-      row_l[nb] = lt;
-    }
-    // Deterministic serial sum of the waves' scaled accumulators.
-#pragma unroll
-    for (int w = NW - 1; w >= 0; --w) {
-      if (wave == w) {
-#pragma unroll
-        for (int mb = 0; mb < 8; ++mb) {
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            f4 x = st.acc[mb][nb] * fac[nb];
-            if (w != NW - 1) x += sm_acc[mb * NB + nb][lane];
-            if (w == 0) {
-              st.acc[mb][nb] = x;
-            } else {
-              sm_acc[mb * NB + nb][lane] = x;
-            }
-          }
-        }
-      }
-      if (w > 0) __syncthreads();
-    }
-    if (wave != 0) return;
-  }
-
-  // Wave 0 stores: lane l owns dims 32*g16 + 8*r + mb (r = 0..3, mb = 0..7)
-  // of row 16*nb + l16.
+  // Lane l owns dims 32*g16 + 8*rr + mb (rr = 0..3, mb = 0..7) of row
+  // row0 + 16*nb + l16.
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const int r = nb * 16 + l16;
+    const int r = row0 + nb * 16 + l16;
     if (r >= a.rows) continue;
     const int qi = r / a.group;
     const int gg = r - qi * a.group;
     if (single) {
-      const float inv = row_l[nb] > 0.f ? 1.0f / row_l[nb] : 0.f;
-      _Float16* op = a.out + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * kHeadDim + 32 * g16;
+      const float inv = st.l[nb] > 0.f ? 1.0f / st.l[nb] : 0.f;
+      _Float16* op =
+          a.out + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * kHeadDim + 32 * g16;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         h8 o;
@@ -327,8 +330,8 @@ __global__ __launch_bounds__(NW * 64) void sqa_partial_kernel(PartialArgs a) {
         *(f4*)(op + 8 * rr + 4) = hi;
       }
       if (g16 == 0) {
-        a.part_ml[item * 2 + 0] = row_m[nb];
-        a.part_ml[item * 2 + 1] = row_l[nb];
+        a.part_ml[item * 2 + 0] = st.m[nb];
+        a.part_ml[item * 2 + 1] = st.l[nb];
       }
     }
   }
@@ -337,12 +340,25 @@ __global__ __launch_bounds__(NW * 64) void sqa_partial_kernel(PartialArgs a) {
 // Log-sum-exp merge of split partials (reference: csrc/small_q_attention_ext.cu:339-366):
 // M = max_s m_s; O = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M); splits
 // with l_s <= 0 are skipped and a row with no visible key is written as 0.
-// 32 lanes per output row, 4 dims each; 8 rows per 256-thread block.
+// One wave per output row: lane j first takes split j's (m, l) (64 splits at a
+// time), the wave reduces the max and the weights, then every lane sums its
+// two dims over the splits with all loads of a chunk in flight.
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
 __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
-  const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int total = a.batch * a.q_len * a.hq;
   if (row >= total) return;
-  const int d4 = (threadIdx.x & 31) * 4;
+  const int lane = threadIdx.x & 63;
   const int h = row % a.hq;
   const int qi = (row / a.hq) % a.q_len;
   const int b = row / (a.hq * a.q_len);
@@ -357,41 +373,77 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   n_valid = n_valid < a.num_splits ? n_valid : a.num_splits;
 
   const size_t base = (size_t)(b * a.hkv + kvh) * a.num_splits;
-  float mx = -INFINITY;
-  for (int s = 0; s < n_valid; ++s) mx = fmaxf(mx, a.part_ml[((base + s) * a.rows + r) * 2]);
-  f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+  const size_t split_stride = (size_t)a.rows;  // items between splits of one row
+  float run_m = -INFINITY;  // running max over chunks
   float den = 0.f;
-  if (mx != -INFINITY) {
-    for (int s = 0; s < n_valid; ++s) {
-      const size_t item = (base + s) * a.rows + r;
-      const float ls = a.part_ml[item * 2 + 1];
-      if (ls <= 0.f) continue;
-      const float w = fast_exp2(a.part_ml[item * 2] - mx);
-      den += ls * w;
-      acc += w * *(const f4*)(a.part_o + item * kHeadDim + d4);
+  float acc0 = 0.f, acc1 = 0.f;
+  for (int s0 = 0; s0 < n_valid; s0 += 64) {
+    const int s = s0 + lane;
+    float ms = -INFINITY, ls = 0.f;
+    if (s < n_valid) {
+      const size_t item = (base + s) * split_stride + r;
+      ms = a.part_ml[item * 2];
+      ls = a.part_ml[item * 2 + 1];
+      if (!(ls > 0.f)) ms = -INFINITY;
+    }
+    const float cm = wave_max(ms);
+    const float new_m = fmaxf(run_m, cm);
+    if (new_m == -INFINITY) continue;  // nothing visible yet
+    const float scale_old = fast_exp2(run_m - new_m);
+    const float w = fast_exp2(ms - new_m);  // 0 for empty splits
+    den = den * scale_old + wave_sum(w * ls);
+    acc0 *= scale_old;
+    acc1 *= scale_old;
+    run_m = new_m;
+    const int n_here = min(64, n_valid - s0);
+    const float* po = a.part_o + ((base + s0) * split_stride + r) * kHeadDim + 2 * lane;
+    const size_t po_stride = split_stride * kHeadDim;
+    int j = 0;
+    for (; j + 4 <= n_here; j += 4) {
+      float2 o[4];
+      float wj[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        o[u] = *(const float2*)(po + (size_t)(j + u) * po_stride);
+        wj[u] = __shfl(w, j + u);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc0 += wj[u] * o[u].x;
+        acc1 += wj[u] * o[u].y;
+      }
+    }
+    for (; j < n_here; ++j) {
+      const float2 o = *(const float2*)(po + (size_t)j * po_stride);
+      const float wj = __shfl(w, j);
+      acc0 += wj * o.x;
+      acc1 += wj * o.y;
     }
   }
   const float inv = den > 0.f ? 1.0f / den : 0.f;
-  h4 o;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = (_Float16)(acc[i] * inv);
-  *(h4*)(a.out + (size_t)row * kHeadDim + d4) = o;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  h2 o;
+  o[0] = (_Float16)(acc0 * inv);
+  o[1] = (_Float16)(acc1 * inv);
+  *(h2*)(a.out + (size_t)row * kHeadDim + 2 * lane) = o;
 }
 
 }  // namespace
 
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)(a.batch * a.hkv * a.num_splits));
-  const dim3 block(kWaves * 64);
+  const int heads_per_wg = kWgWaves / row_groups(a.rows);
+  const int head_groups = (a.hkv + heads_per_wg - 1) / heads_per_wg;
+  const dim3 grid((unsigned)(a.batch * a.num_splits * head_groups));
+  const dim3 block(kWgWaves * 64);
   switch (row_blocks(a.rows)) {
     case 1:
-      hipLaunchKernelGGL((sqa_partial_kernel<1, kWaves>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((sqa_partial_kernel<1, 1, 3>), grid, block, 0, stream, a);
       break;
     case 2:
-      hipLaunchKernelGGL((sqa_partial_kernel<2, kWaves>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((sqa_partial_kernel<2, 1, 3>), grid, block, 0, stream, a);
       break;
     default:
-      hipLaunchKernelGGL((sqa_partial_kernel<4, kWaves>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((sqa_partial_kernel<2, 2, 3>), grid, block, 0, stream, a);
       break;
   }
   return hipGetLastError();
@@ -399,7 +451,7 @@ hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
 
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream) {
   const int total = a.batch * a.q_len * a.hq;
-  const dim3 grid((unsigned)((total + 7) / 8));
+  const dim3 grid((unsigned)((total + 3) / 4));
   hipLaunchKernelGGL(sqa_merge_kernel, grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }
