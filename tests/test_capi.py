@@ -1,0 +1,111 @@
+"""CPU checks of the C ABI (``include/sqa.h`` / ``libsqa.so``): no kernel launches.
+
+The library must load, export every function the header declares, and reject
+bad arguments with the documented status codes before touching the GPU.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from small_q_attention_amd import _lib, build
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "sqa.h"
+
+SQA_OK, SQA_ERR_INVALID, SQA_ERR_UNSUPPORTED, SQA_ERR_WORKSPACE = 0, 1, 2, 3
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    body = text[text.index('extern "C" {'):]
+    return sorted(set(re.findall(r"\b(sqa_[a-z0-9_]+)\s*\(", body)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if build.is_stale():
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_the_bound_functions():
+    assert declared_functions() == sorted(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(str(_lib.library_path()))
+    for name in declared_functions():
+        assert hasattr(raw, name), name
+
+
+def test_version_and_empty_error(lib):
+    assert lib.sqa_version().decode().startswith("sqa ")
+    assert isinstance(lib.sqa_last_error(), bytes)
+
+
+def test_workspace_bytes(lib):
+    # rows = q_len * group; items = B * Hkv * splits * rows; 130 floats each.
+    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 1) == 0
+    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 16) == 16 * 8 * 16 * 32 * 130 * 4
+    assert lib.sqa_workspace_bytes(1, 2, 32, 8, 3) == 1 * 8 * 3 * 8 * 130 * 4
+    assert lib.sqa_workspace_bytes(0, 2, 32, 8, 3) == 0
+
+
+def _plan(lib, **kw):
+    args = dict(device=0, batch=4, q_len=4, hq=32, hkv=8, max_seq_len=8192, max_pages=512,
+                chunk_keys=512)
+    args.update(kw)
+    ns, pps = ctypes.c_int(-7), ctypes.c_int(-7)
+    rc = lib.sqa_plan_splits(args["device"], args["batch"], args["q_len"], args["hq"], args["hkv"],
+                             args["max_seq_len"], args["max_pages"], args["chunk_keys"],
+                             ctypes.byref(ns), ctypes.byref(pps))
+    return rc, ns.value, pps.value
+
+
+def test_plan_with_explicit_chunk_keys(lib):
+    # Reference meaning (csrc/small_q_attention_ext.cu:1177): ceil(longest / chunk) chunks.
+    assert _plan(lib) == (SQA_OK, 16, 32)
+    assert _plan(lib, chunk_keys=128, max_seq_len=33, max_pages=3) == (SQA_OK, 1, 3)
+    assert _plan(lib, chunk_keys=1 << 20, max_seq_len=8192) == (SQA_OK, 1, 512)
+    assert _plan(lib, chunk_keys=100, max_seq_len=1000, max_pages=63) == (SQA_OK, 9, 7)
+    # Unknown max_seq_len: the plan covers the whole block-table row.
+    assert _plan(lib, chunk_keys=512, max_seq_len=0, max_pages=100) == (SQA_OK, 4, 32)
+
+
+def test_plan_rejects_bad_arguments(lib):
+    assert _plan(lib, batch=0)[0] == SQA_ERR_INVALID
+    assert _plan(lib, chunk_keys=-1)[0] == SQA_ERR_INVALID
+    assert _plan(lib, max_pages=0)[0] == SQA_ERR_INVALID
+    rc = lib.sqa_plan_splits(0, 1, 2, 32, 8, 16, 1, 16, None, None)
+    assert rc == SQA_ERR_INVALID
+
+
+def _call(lib, **kw):
+    args = dict(q=1, k=1, v=1, bt=1, sl=1, out=1, ws=None, ws_bytes=0, batch=1, q_len=2, hq=32,
+                hkv=8, dim=128, num_pages=4, page=16, max_pages=2, splits=1, pps=2)
+    args.update(kw)
+    return lib.sqa_paged_mtp_attention(
+        args["q"], args["k"], args["v"], args["bt"], args["sl"], args["out"], args["ws"],
+        args["ws_bytes"], args["batch"], args["q_len"], args["hq"], args["hkv"], args["dim"],
+        args["num_pages"], args["page"], args["max_pages"], args["splits"], args["pps"], None, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(q=None), SQA_ERR_INVALID, "null"),
+    (dict(batch=0), SQA_ERR_INVALID, "positive"),
+    (dict(num_pages=0), SQA_ERR_INVALID, "empty"),
+    (dict(hkv=5), SQA_ERR_INVALID, "divisible"),
+    (dict(dim=64), SQA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(page=32), SQA_ERR_UNSUPPORTED, "page_size"),
+    (dict(q_len=32), SQA_ERR_UNSUPPORTED, "exceeds"),
+    (dict(splits=0), SQA_ERR_INVALID, "positive"),
+    (dict(splits=2, ws=None), SQA_ERR_WORKSPACE, "workspace"),
+    (dict(splits=2, ws=1, ws_bytes=100), SQA_ERR_WORKSPACE, "workspace"),
+])
+def test_launch_rejects_bad_arguments_without_a_gpu(lib, kw, code, msg):
+    # Validation runs before any HIP call, so these pointers are never touched.
+    assert _call(lib, **kw) == code
+    assert msg in lib.sqa_last_error().decode()

@@ -1,0 +1,97 @@
+"""GPU parity at the BASELINE configurations' full sizes and over the 36-case matrix.
+
+cfg1 (B1 q2 L1024) and cfg2 (B4 q4 L8192) are checked whole against the float64
+C oracle. cfg3 (B16 q8 L32768, K x4 on 1% of slots), cfg5 (ragged B16 q8,
+L ~ U[1024, 32768]) and every matrix case are checked whole against a torch
+float32 reference on the GPU and, on sampled sequences, against the float64
+C oracle; at full size they also get size-independent properties (the output
+does not depend on where pages sit in the pool; split plans agree; rows are
+convex combinations of V).
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_c64
+from small_q_attention_amd import cuda as sqa, inputs
+from tests._helpers import assert_parity, compact_sequences, torch_fp32_reference
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    sys.__stderr__.write(f"\n[gpu-test] {request.node.nodeid}\n")
+    sys.__stderr__.flush()
+
+
+def _c_oracle_on(tensors, batches):
+    sub = compact_sequences(*tensors, batches=batches)
+    return attention_c64(*sub, 16, 8)
+
+
+def test_cfg1_cpu_reference_shape():
+    case = inputs.baseline_configs()["cfg1"]
+    tensors = tuple(t.cuda() for t in inputs.make_inputs(case))
+    ref = attention_c64(*(t.cpu() for t in tensors), 16, 8)
+    assert_parity(sqa.forward_v0(*tensors, 16), ref, label="cfg1 v0")
+    assert_parity(sqa.forward_v3(*tensors, 16, 512, 1024), ref, label="cfg1 v3")
+
+
+def test_cfg2_single_split_contract():
+    case = inputs.baseline_configs()["cfg2"]
+    tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
+    ref = attention_c64(*(t.cpu() for t in tensors), 16, 8)
+    assert_parity(sqa.forward_v0(*tensors, 16), ref, label="cfg2 v0 (auto plan)")
+    assert_parity(sqa.forward_v3(*tensors, 16, 1 << 20, 8192), ref, label="cfg2 single split")
+
+
+@pytest.mark.parametrize("name", ["cfg3", "cfg5"])
+def test_full_size_configs(name):
+    case = inputs.baseline_configs()[name]
+    tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
+    q, k, v, bt, sl = tensors
+    out = sqa.paged_mtp_attention(*tensors, 16, case.max_seq_len)
+    torch.cuda.synchronize()
+    ref32 = torch_fp32_reference(*tensors, 16, 8)
+    assert_parity(out, ref32, label=f"{name} vs torch fp32")
+    sample = [0, case.batch - 1]
+    assert_parity(out[sample], _c_oracle_on(tensors, sample), label=f"{name} vs C oracle")
+    # Convexity: every output element lies within the range of V over its head.
+    vmax = v.float().abs().max().item()
+    assert out.float().abs().max().item() <= vmax * (1 + 1e-3)
+    # Physical placement: permuting the pool and the table changes nothing, bit for bit.
+    g = torch.Generator(device="cuda").manual_seed(7)
+    perm = torch.randperm(k.shape[0], device="cuda", generator=g)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel(), device="cuda")
+    bt2 = inv[bt.long()].to(torch.int32)
+    k2 = k[perm]
+    v2 = v[perm]
+    out2 = sqa.paged_mtp_attention(q, k2, v2, bt2, sl, 16, case.max_seq_len)
+    assert torch.equal(out, out2)
+    del k2, v2
+    # A different split plan agrees within the bar.
+    out3 = sqa.forward_v3(*tensors, 16, 512, case.max_seq_len)
+    assert (out3.float() - out.float()).abs().max().item() <= 2e-3
+
+
+MATRIX = [(c.q_len, c.seq_lens[0], c.batch) for c in inputs.matrix_cases()]
+
+
+@pytest.mark.parametrize("q_len,kv_len,batch", MATRIX)
+def test_matrix_case(q_len, kv_len, batch):
+    case = inputs.uniform_case(batch, q_len, kv_len, seed=1000 + q_len * 100 + batch)
+    tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
+    out = sqa.paged_mtp_attention(*tensors, 16, kv_len)
+    torch.cuda.synchronize()
+    assert_parity(out, torch_fp32_reference(*tensors, 16, 8), label="vs torch fp32")
+    assert_parity(out[[0]], _c_oracle_on(tensors, [0]), label="vs C oracle")
+    # The reference default plan (chunk 512) agrees as well.
+    if q_len <= 8:
+        out_v3 = sqa.forward_v3(*tensors, 16, 512, kv_len)
+        assert (out_v3.float() - out.float()).abs().max().item() <= 2e-3
+    assert np.isfinite(out.float().cpu().numpy()).all()

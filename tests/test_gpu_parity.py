@@ -1,0 +1,240 @@
+"""GPU parity of the HIP kernels (through the op boundary and the C ABI) with the oracle.
+
+Restates the reference's GPU correctness drivers
+(``/root/reference/scripts/build_and_test_v0.py``..``_v5.py``: kv 33/1024/8192,
+reversed page tables, chunk 128/512/1<<20, explicit and measured max_seq_len)
+with q_len 16 added, and covers what they leave out: ragged batches on a
+scattered 2x pool, rows that see no key, NaN in unused page slots, padding
+block-table entries, the golden fixtures, determinism, streams and graph
+capture. Bar: ``|a - r| <= 2e-3 + 1e-2 |r|`` against the float64 C oracle
+rounded to fp16.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_c64
+from small_q_attention_amd import _lib, cuda as sqa, inputs
+from tests._helpers import assert_parity, parity_stats
+from tests.test_golden import FIXTURES, load_fixture
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    sys.__stderr__.write(f"\n[gpu-test] {request.node.nodeid}\n")
+    sys.__stderr__.flush()
+
+
+def _to_gpu(tensors):
+    return tuple(t.cuda() for t in tensors)
+
+
+def _oracle(tensors, page=16, hkv=8):
+    q, k, v, bt, sl = (t.cpu() for t in tensors)
+    return attention_c64(q, k, v, bt, sl, page, hkv)
+
+
+def _variants(kv_len):
+    """(label, callable) pairs covering every forward_vN and chunking the reference drivers use."""
+    out = [
+        ("v0", lambda *t: sqa.forward_v0(*t, 16)),
+        ("v1", lambda *t: sqa.forward_v1(*t, 16, 512)),  # positional 512 lands in verbose
+        ("auto", lambda *t: sqa.paged_mtp_attention(*t, 16, kv_len)),
+        ("auto_nosync", lambda *t: sqa.paged_mtp_attention(*t, 16)),
+    ]
+    for ck in (128, 512, 1 << 20):
+        out.append((f"v2_c{ck}", lambda *t, ck=ck: sqa.forward_v2(*t, 16, ck)))
+    for ck in (128, 512):
+        out.append((f"v3_c{ck}", lambda *t, ck=ck: sqa.forward_v3(*t, 16, ck, kv_len)))
+        out.append((f"v3_c{ck}_autolen", lambda *t, ck=ck: sqa.forward_v3(*t, 16, ck, 0)))
+        out.append((f"v4_c{ck}", lambda *t, ck=ck: sqa.forward_v4(*t, 16, ck, kv_len)))
+    for tg in (2, 4):
+        out.append((f"v5_tg{tg}", lambda *t, tg=tg: sqa.forward_v5(
+            *t, 16, chunk_keys=512, token_group=tg, max_seq_len=kv_len)))
+    return out
+
+
+@pytest.mark.parametrize("q_len", [2, 4, 8, 16])
+@pytest.mark.parametrize("kv_len", [33, 1024, 8192])
+def test_reference_driver_cases(q_len, kv_len):
+    """build_and_test_v0..v5: B=1, reversed pages, every variant and chunking."""
+    case = inputs.uniform_case(1, q_len, kv_len, page_mode="shared", seed=99 + q_len + kv_len)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    ref = _oracle(tensors)
+    outs = {}
+    for label, fwd in _variants(kv_len):
+        outs[label] = fwd(*tensors)
+        torch.cuda.synchronize()
+        assert_parity(outs[label], ref, label=f"{label} q{q_len} kv{kv_len}")
+    # Every variant runs the same kernels; different split plans agree closely.
+    base = outs["v0"].float()
+    for label, o in outs.items():
+        assert (o.float() - base).abs().max().item() <= 2e-3, label
+
+
+@pytest.mark.parametrize("q_len", [2, 4, 8])
+@pytest.mark.parametrize("kv_len", [33, 1024])
+def test_reference_v5_unique_pages(q_len, kv_len):
+    """build_and_test_v5: batch 2, 'unique' per-request page ranges."""
+    case = inputs.uniform_case(2, q_len, kv_len, page_mode="unique", seed=5000 + q_len * 17 + kv_len)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    ref = _oracle(tensors)
+    for tg in ((2,) if q_len == 2 else (2, 4)):
+        out = sqa.forward_v5(*tensors, 16, chunk_keys=512, token_group=tg, max_seq_len=kv_len)
+        assert_parity(out, ref, label=f"v5 tg{tg}")
+
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_golden_fixtures(name):
+    case, tensors, expected, _ = load_fixture(name)
+    tensors = _to_gpu(tensors)
+    out = sqa.paged_mtp_attention(*tensors, 16, max(case.seq_lens))
+    assert_parity(out, expected.astype(np.float64), label=name)
+    out2 = sqa.forward_v2(*tensors, 16, 16)  # one page per split: many splits
+    assert_parity(out2, expected.astype(np.float64), label=name + " many splits")
+
+
+@pytest.mark.parametrize("q_len", [2, 4, 8, 16])
+def test_ragged_batch_on_scattered_pool(q_len):
+    lens = [1, q_len, q_len + 1, 16, 17, 31, 300, 1000]
+    case = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=300 + q_len)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    ref = _oracle(tensors)
+    for ck in (None, 16, 64, 512):
+        out = sqa.paged_mtp_attention(*tensors, 16, 1000, chunk_keys=ck)
+        st = assert_parity(out, ref, label=f"q{q_len} ck{ck}")
+        assert st["max_abs_vs_f64_oracle"] < 2e-3
+
+
+def test_rows_without_visible_keys_are_zero():
+    """seq_len < q_len: rows qi < q_len - seq_len see nothing and are written as 0
+    (reference v2-v5 merge, csrc/small_q_attention_ext.cu:365); seq_len 0 gives 0."""
+    case = inputs.Case(batch=3, q_len=8, seq_lens=[3, 0, 8], seed=11)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    for ck in (None, 16):
+        out = sqa.paged_mtp_attention(*tensors, 16, 8, chunk_keys=ck).float().cpu()
+        assert torch.all(out[0, :5] == 0) and torch.all(out[0, 5:].abs().sum(-1) > 0)
+        assert torch.all(out[1] == 0)
+        assert_parity(out.half(), _oracle(tensors), label=f"ck{ck}")
+
+
+def test_garbage_outside_the_sequence_is_never_used():
+    """NaN in the unused slots of last pages and in the page padding entries point to."""
+    case = inputs.Case(batch=3, q_len=4, seq_lens=[20, 33, 47], seed=12)
+    q, k, v, bt, sl = inputs.make_inputs(case)
+    ref = attention_c64(q, k, v, bt, sl, 16, 8)
+    k, v = k.clone(), v.clone()
+    nan_page = k.shape[0]
+    k = torch.cat([k, torch.full_like(k[:1], float("nan"))])
+    v = torch.cat([v, torch.full_like(v[:1], float("nan"))])
+    bt = torch.cat([bt, torch.zeros(3, 4, dtype=torch.int32)], 1)
+    for b, n in enumerate(sl.tolist()):
+        pages = -(-n // 16)
+        bt[b, pages:] = nan_page
+        last = int(bt[b, pages - 1])
+        k[last, n % 16 or 16:] = float("nan")
+        v[last, n % 16 or 16:] = float("nan")
+    tensors = _to_gpu((q, k, v, bt, sl))
+    for ck in (None, 16):
+        out = sqa.paged_mtp_attention(*tensors, 16, 0, chunk_keys=ck)
+        assert_parity(out, ref, label=f"ck{ck}")
+
+
+def test_outliers_and_multi_page_drafts():
+    for q_len, lens in ((16, [17, 31, 32, 33]), (8, [9, 15, 16, 17])):
+        case = inputs.Case(batch=4, q_len=q_len, seq_lens=lens, seed=13 + q_len,
+                           k_outlier_frac=0.2, k_outlier_scale=4.0)
+        tensors = _to_gpu(inputs.make_inputs(case))
+        assert_parity(sqa.paged_mtp_attention(*tensors, 16, max(lens)), _oracle(tensors),
+                      label=f"q{q_len}")
+
+
+def test_deterministic_and_split_plans_agree():
+    case = inputs.Case(batch=2, q_len=8, seq_lens=[4000, 2500], seed=14)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    a = sqa.paged_mtp_attention(*tensors, 16, 4000)
+    b = sqa.paged_mtp_attention(*tensors, 16, 4000)
+    assert torch.equal(a, b)
+    single = sqa.forward_v3(*tensors, 16, 1 << 20, 4000)
+    many = sqa.forward_v3(*tensors, 16, 16, 4000)
+    assert (single.float() - many.float()).abs().max().item() <= 1e-3
+    ref = _oracle(tensors)
+    for o in (a, single, many):
+        assert_parity(o, ref)
+
+
+def test_runs_on_the_callers_stream():
+    case = inputs.Case(batch=2, q_len=4, seq_lens=[700, 900], seed=15)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    ref = _oracle(tensors)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out = sqa.paged_mtp_attention(*tensors, 16, 900)
+    side.synchronize()
+    assert_parity(out, ref)
+
+
+def test_graph_capture_and_replay():
+    """The op has no host sync and no allocation outside torch's allocator, so it captures.
+
+    Replays several times with eager work in between; every replay must equal the
+    eager result bit for bit.
+    """
+    case = inputs.Case(batch=2, q_len=8, seq_lens=[3000, 1200], seed=16)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    eager = sqa.paged_mtp_attention(*tensors, 16, 3000)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            sqa.paged_mtp_attention(*tensors, 16, 3000)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = sqa.paged_mtp_attention(*tensors, 16, 3000)
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager), f"replay {i}"
+        junk = torch.randn(1 << 20, device="cuda").sum()  # eager work between replays
+        torch.cuda.synchronize()
+        del junk
+
+
+def test_c_abi_direct_with_caller_workspace():
+    """sqa_paged_mtp_attention through ctypes with a caller-owned workspace and events."""
+    case = inputs.Case(batch=3, q_len=4, seq_lens=[500, 64, 1500], seed=17)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    q, k, v, bt, sl = tensors
+    ns, pps = _lib.plan_splits(0, 3, 4, 32, 8, 1500, bt.shape[1], 256)
+    assert ns > 1
+    ws = torch.empty(_lib.workspace_bytes(3, 4, 32, 8, ns), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(q)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    for e in evs:
+        e.record()
+    _lib.launch(q, k, v, bt, sl, out, ws, ns, pps, torch.cuda.current_stream().cuda_stream,
+                timing_events=[e.cuda_event for e in evs])
+    torch.cuda.synchronize()
+    assert evs[0].elapsed_time(evs[1]) > 0
+    assert_parity(out, _oracle(tensors))
+    small = torch.empty(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError, match="workspace"):
+        _lib.launch(q, k, v, bt, sl, out, small, ns, pps, 0)
+
+
+def test_parity_stats_flags_a_planted_mistake():
+    """The checker itself: an oracle off by one visible key fails the bar."""
+    case = inputs.Case(batch=1, q_len=4, seq_lens=[40], seed=18)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    out = sqa.paged_mtp_attention(*tensors, 16, 40)
+    q, k, v, bt, sl = (t.cpu() for t in tensors)
+    wrong = attention_c64(q, k, v, bt, sl - 1, 16, 8)  # every row sees one key less
+    assert not parity_stats(out, wrong)["ok"]
