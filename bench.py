@@ -28,6 +28,20 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, AMD published peak
+# rocprofv3 FETCH_SIZE + WRITE_SIZE summary of the partial kernel on this workload
+# (calibrated against a plain 1 GiB copy); regenerated with the kernel.
+PROFILE = ROOT / "profiles" / "sqa_partial_kernel_cfg3_b16_q8_kv32768.txt"
+
+
+def _profiled_traffic():
+    """HBM bytes per partial-kernel launch from the committed counter summary, or None."""
+    try:
+        for line in PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 METRIC = "µs/call + achieved HBM GB/s (% peak), q_len 2/4/8, KV 8K/32K, batch 1/4/16"
 
 
@@ -40,6 +54,8 @@ def _parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU-baseline sample duration")
     ap.add_argument("--no-per-q", action="store_true", help="skip the q_len 2/4/16 extras")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run 3 plain device copies of this many MiB (counter calibration)")
     return ap.parse_args()
 
 
@@ -142,6 +158,16 @@ def main():
         sys.exit(1)
     torch.cuda.set_device(0)
     lib = _lib.load(build_if_missing=False)
+    if args.copy_probe_mib > 0:
+        # A plain copy kernel of known size: its FETCH_SIZE / WRITE_SIZE counters
+        # calibrate the per-dispatch byte counts of the attention kernels.
+        n = args.copy_probe_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     case = inputs.baseline_configs()["cfg3"]
     tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
     q, k, v, bt, sl = tensors
@@ -181,7 +207,8 @@ def main():
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": None,
+            "traffic": _profiled_traffic(),
+            "traffic_source": str(PROFILE.relative_to(ROOT)),
             "kernel": "sqa_partial_kernel",
             "kernel_us": round(part_ms * 1e3, 2),
             "merge_us": round(merge_ms * 1e3, 2),
