@@ -94,6 +94,7 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
     if (pps < kMinPagesPerSplit) pps = kMinPagesPerSplit;
   }
   if (pps > pages) pps = pages;
+  if (pps > sqa::kMaxSplitPages) pps = sqa::kMaxSplitPages;
   if (pps < 1) pps = 1;
   long long splits = ceil_div(pages, pps);
   if (splits < 1) splits = 1;
@@ -137,6 +138,9 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
     return fail(SQA_ERR_UNSUPPORTED, "q_len * group = %lld exceeds %d", rows, sqa::kMaxRows);
   if (num_splits <= 0 || pages_per_split <= 0)
     return fail(SQA_ERR_INVALID, "num_splits and pages_per_split must be positive");
+  if (pages_per_split > sqa::kMaxSplitPages)
+    return fail(SQA_ERR_INVALID, "pages_per_split %d exceeds %d", pages_per_split,
+                sqa::kMaxSplitPages);
   // A plan covering fewer than max_pages pages (built from a known
   // max_seq_len) processes only the first num_splits * pages_per_split pages of
   // each sequence, as the reference launchers do with their max_seq_len.

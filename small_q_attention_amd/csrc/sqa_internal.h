@@ -10,6 +10,7 @@ namespace sqa {
 constexpr int kHeadDim = 128;   // contract: head_dim 128
 constexpr int kPageSize = 16;   // contract: 16-token pages
 constexpr int kMaxRows = 64;    // q_len * (Hq / Hkv) rows one work item holds
+constexpr int kMaxSplitPages = 2048;  // pages one split may own (LDS page-id table)
 
 // Everything the split-KV partial kernel needs. Element counts, not bytes.
 struct PartialArgs {

@@ -46,6 +46,12 @@ __device__ __forceinline__ float xor_max(float x) {
   return fmaxf(x, __shfl_xor(x, 32));
 }
 
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
 __device__ __forceinline__ float xor_sum(float x) {
   x += __shfl_xor(x, 16);
   return x + __shfl_xor(x, 32);
@@ -60,7 +66,7 @@ struct PageRegs {
 template <int NB>
 struct WaveState {
   f4 acc[8][NB];   // O^T blocks: lane l holds dims 32*(l/16)+8*r+mb of row 16*nb+l%16
-  float m[NB];     // running row max (log2 units), identical in the 4 lane groups
+  float m[NB];     // reference max (log2 units, within kMaxLag of the true row max), same in all 4 lane groups
   float l[NB];     // partial row sum over this lane's tokens
 };
 
@@ -68,18 +74,39 @@ struct WaveState {
 constexpr int kBufferFlags = 0x00020000;
 // Cache-policy operand of the K/V buffer loads: non-temporal (read once).
 constexpr int kStreamAux = 2;
+// Padding of the LDS page-id table beyond the split's last page: covers the
+// ring's look-ahead (at most 2 * D + 1 entries past the end).
+constexpr int kIdPad = 16;
 
 __device__ __forceinline__ int clamp_page(int pid, long long num_pages) {
   return (pid >= 0 && (long long)pid < num_pages) ? pid : 0;
 }
 
-// sm_q: Q fragments in LDS, [nb][kk][lane] (the B-operand layout), so they cost
-// no registers across the page loop.
+// The running row max may trail the true max by up to this many log2 units
+// (probabilities up to 2^8 = 256, still exact to fp16 precision in P and far
+// from any fp32 range limit in the sums). Rows only pay for the cross-lane max
+// and the accumulator rescale when a new score exceeds the running max by
+// more than this, which after the first page is rare.
+constexpr float kMaxLag = 8.0f;
+
+__device__ __forceinline__ float max4(f4 v) { return fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])); }
+
+// Bytes {a.lo16, b.lo16} and {a.hi16, b.hi16} of two dwords (v_perm_b32).
+__device__ __forceinline__ unsigned pack_lo(unsigned a, unsigned b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ unsigned pack_hi(unsigned a, unsigned b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// One 16-token page for one wave. sm_q: Q fragments in LDS, [nb][kk][lane]
+// (the B-operand layout). c = head_dim^-1/2 * log2(e); scores stay raw until
+// the exponent, where the scale and the running max meet in one FMA.
 template <int NB>
 __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, const h8* sm_q,
                                              int lane, const int (&vis)[NB], int tok0, int len,
-                                             bool masked, float scale_log2) {
-  // Scores S^T[token][row] for this page.
+                                             bool masked, float c) {
+  // Raw scores S^T[token][row] = K . Q^T for this page.
   f4 s[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -90,7 +117,6 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, co
       s[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, pg.k[kk]), qf, s[nb],
                                                     0, 0, 0);
     }
-    s[nb] *= scale_log2;
   }
   if (masked) {
     // tok0 = absolute index of this lane's first token (4 consecutive tokens).
@@ -109,46 +135,53 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, co
     }
   }
 
-  h4 ph[NB];
-  bool rescale = false;
-  float alpha[NB];
+  // Lane-local max (4 tokens of one row); the row max is only reduced across
+  // the four 16-lane groups when some lane runs ahead of its running max.
+  float lm[NB];
+  bool grow = false;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    float pm = fmaxf(fmaxf(s[nb][0], s[nb][1]), fmaxf(s[nb][2], s[nb][3]));
-    pm = xor_max(pm);
-    const float mn = fmaxf(st.m[nb], pm);
-    const float mu = (mn == -INFINITY) ? 0.f : mn;
-    alpha[nb] = fast_exp2(st.m[nb] - mu);
-    rescale |= (alpha[nb] != 1.0f);
-    st.m[nb] = mn;
-    float lsum = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const _Float16 p = (_Float16)fast_exp2(s[nb][e] - mu);
-      ph[nb][e] = p;
-      lsum += (float)p;
-    }
-    st.l[nb] = st.l[nb] * alpha[nb] + lsum;
+    lm[nb] = max4(s[nb]) * c;
+    grow |= lm[nb] > st.m[nb] + kMaxLag;
   }
-  if (__any(rescale)) {
+  if (__any(grow)) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
+      const float mn = fmaxf(st.m[nb], xor_max(lm[nb]));
+      const float alpha = fast_exp2(st.m[nb] - (mn == -INFINITY ? 0.f : mn));
+      st.m[nb] = mn;
+      st.l[nb] *= alpha;
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) st.acc[mb][nb] *= alpha[nb];
+      for (int mb = 0; mb < 8; ++mb) st.acc[mb][nb] *= alpha;
     }
   }
 
-  // O^T += V^T . P^T, one 16x16x16 MFMA per (dim block, row block).
+  // P = 2^(c*s - m), rounded once to fp16; the row sum is taken over the
+  // rounded values (v_dot2 against ones) so O is an exact convex combination.
+  h4 ph[NB];
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const float mu = st.m[nb] == -INFINITY ? 0.f : st.m[nb];
+    h2 lo, hi;
+    lo[0] = (_Float16)fast_exp2(fmaf(s[nb][0], c, -mu));
+    lo[1] = (_Float16)fast_exp2(fmaf(s[nb][1], c, -mu));
+    hi[0] = (_Float16)fast_exp2(fmaf(s[nb][2], c, -mu));
+    hi[1] = (_Float16)fast_exp2(fmaf(s[nb][3], c, -mu));
+    st.l[nb] = __builtin_amdgcn_fdot2(hi, ones, __builtin_amdgcn_fdot2(lo, ones, st.l[nb], false),
+                                      false);
+    ph[nb] = h4{lo[0], lo[1], hi[0], hi[1]};
+  }
+
+  // O^T += V^T . P^T, one 16x16x16 MFMA per (dim block, row block). Dim block
+  // mb takes half mb%2 of dword mb/2 from the four token rows this lane holds.
 #pragma unroll
   for (int mb = 0; mb < 8; ++mb) {
     const int j = mb >> 1;
     const unsigned w0 = pg.v[0][j], w1 = pg.v[1][j], w2 = pg.v[2][j], w3 = pg.v[3][j];
-    u2 av;
-    if ((mb & 1) == 0) {
-      av = u2{(w0 & 0xffffu) | (w1 << 16), (w2 & 0xffffu) | (w3 << 16)};
-    } else {
-      av = u2{(w0 >> 16) | (w1 & 0xffff0000u), (w2 >> 16) | (w3 & 0xffff0000u)};
-    }
+    const u2 av = (mb & 1) == 0 ? u2{pack_lo(w0, w1), pack_lo(w2, w3)}
+                                : u2{pack_hi(w0, w1), pack_hi(w2, w3)};
     const h4 a = __builtin_bit_cast(h4, av);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -188,45 +221,56 @@ __global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs 
   // the last row block idle but stay for the barrier.
   const bool active = kvh < a.hkv && row0 < a.rows;
 
+  const int p_begin = split * a.pages_per_split;
+  const int32_t* bt_row = a.block_tables + (size_t)b * a.max_pages;
+
+  // Start-up is two memory round trips. First (scalar, together): the
+  // sequence length and the ids of the split's first D pages (index clamped
+  // into the block-table row; ids past the sequence are never used).
+  int first_id[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) first_id[j] = bt_row[min(p_begin + j, a.max_pages - 1)];
   int len = a.seq_lens[b];
   len = len < 0 ? 0 : len;
   int pages_used = (len + kPageSize - 1) / kPageSize;
   pages_used = pages_used < a.max_pages ? pages_used : a.max_pages;
-  const int p_begin = split * a.pages_per_split;
   const int p_end = min(p_begin + a.pages_per_split, pages_used);
   const bool single = a.num_splits == 1;
   if (p_begin >= p_end && !single) return;  // uniform per workgroup; never merged
+  const int n_split = p_end > p_begin ? p_end - p_begin : 0;
+  const int n_pages = active ? n_split : 0;
 
-  // Q fragments of this wave's rows in LDS, [wave][nb][kk][lane] (B-operand
-  // layout). Each lane stores exactly the fragments it reads back.
-  __shared__ h8 sm_q[kWgWaves * NB * 4 * 64];
-  h8* my_q = sm_q + wave * NB * 4 * 64;
+  // Second: Q fragments, the rest of the split's page ids and the first D
+  // pages, all in flight at once (Q and ids first, so waiting for them leaves
+  // the page loads outstanding).
+  h8 qreg[NB][4];
   int vis[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
+    // Loads are unconditional from an in-bounds address (padding rows and idle
+    // waves read row 0 of kv head 0) and the value is selected afterwards, so
+    // no lane-divergent branch splits the load stream.
     const int r = row0 + nb * 16 + l16;
     const bool real = active && r < a.rows;
     const int qi = real ? r / a.group : 0;
     const int gg = real ? r - qi * a.group : 0;
-    const _Float16* qp =
-        a.q + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * kHeadDim + 8 * g16;
+    const int hh = real ? kvh * a.group + gg : 0;
+    const _Float16* qp = a.q + ((size_t)(b * a.q_len + qi) * a.hq + hh) * kHeadDim + 8 * g16;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      my_q[(nb * 4 + kk) * 64 + lane] =
-          real ? *(const h8*)(qp + 32 * kk) : h8{0, 0, 0, 0, 0, 0, 0, 0};
+      const h8 x = *(const h8*)(qp + 32 * kk);
+      qreg[nb][kk] = real ? x : h8{0, 0, 0, 0, 0, 0, 0, 0};
     }
     vis[nb] = real ? len - a.q_len + 1 + qi : 0;
   }
-  // Pages whose last token index >= mask_from need the causal/tail mask.
-  const int mask_from = len - a.q_len + 1;
-
-  WaveState<NB> st;
+  constexpr int kIdSlots = (kMaxSplitPages + kIdPad + kWgWaves * 64 - 1) / (kWgWaves * 64);
+  int idreg[kIdSlots];
+  const int last_id = n_split > 0 ? n_split - 1 : 0;  // p_begin + last_id < max_pages
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    st.m[nb] = -INFINITY;
-    st.l[nb] = 0.f;
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb) st.acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < kIdSlots; ++k) {
+    const int i = threadIdx.x + k * kWgWaves * 64;
+    const int x = bt_row[p_begin + min(i, last_id)];
+    idreg[k] = i < n_split ? x : -1;
   }
 
   // K/V pages are read with buffer loads: the resource (4 SGPRs) is rebuilt per
@@ -237,17 +281,6 @@ __global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs 
   const unsigned page_bytes = kPageSize * tok_bytes;           // bytes between pages
   const unsigned k_lane = l16 * tok_bytes + kvh_c * kHeadDim * 2 + 16 * g16;
   const unsigned v_lane = 4 * g16 * tok_bytes + kvh_c * kHeadDim * 2 + 16 * l16;
-  const int32_t* bt_row = a.block_tables + (size_t)b * a.max_pages;
-  const int n_pages = active ? (p_end > p_begin ? p_end - p_begin : 0) : 0;
-
-  // Page id of page p_begin + i (a scalar load), or -1 past the end. The index
-  // is clamped before the read so the block table is never read beyond the
-  // split's pages.
-  auto page_id = [&](int i) -> int {
-    const int ic = i < n_pages ? i : n_pages - 1;
-    const int pid = ic >= 0 ? clamp_page(bt_row[p_begin + ic], a.num_pages) : 0;
-    return i < n_pages ? pid : -1;
-  };
   // pid < 0 gives a zero-length resource: the loads return zeros without
   // touching memory, so every slot refill below is unconditional and the
   // compiler's wait counts stay exact (one page retires per step). K/V are
@@ -266,14 +299,47 @@ __global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs 
     for (int e = 0; e < 4; ++e)
       pg.v[e] = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane, e * tok_bytes, kAux);
   };
-
-  __syncthreads();  // sm_q written
-
   // Ring of D pages in flight: page i is processed from slot i % D, which is
   // then refilled with page i + D.
   PageRegs ring[D];
 #pragma unroll
-  for (int j = 0; j < D; ++j) load_page(page_id(j), ring[j]);
+  for (int j = 0; j < D; ++j) {
+    load_page(j < n_pages ? clamp_page(first_id[j], a.num_pages) : -1, ring[j]);
+  }
+
+  // LDS: the Q fragments of this wave's rows, [wave][nb][kk][lane] (the
+  // B-operand layout; each lane stores exactly the fragments it reads back),
+  // and the split's page ids: ids of [p_begin, p_end) clamped into the pool,
+  // then -1 for the ring's look-ahead. Waves read ids back a step ahead of
+  // use, so no page waits on a block-table load from memory.
+  __shared__ h8 sm_q[kWgWaves * NB * 4 * 64];
+  __shared__ int sm_ids[kIdSlots * kWgWaves * 64];
+  h8* my_q = sm_q + wave * NB * 4 * 64;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) my_q[(nb * 4 + kk) * 64 + lane] = qreg[nb][kk];
+  }
+#pragma unroll
+  for (int k = 0; k < kIdSlots; ++k) {
+    const int i = threadIdx.x + k * kWgWaves * 64;
+    sm_ids[i] = idreg[k] >= 0 ? clamp_page(idreg[k], a.num_pages) : -1;
+  }
+  auto page_id = [&](int i) -> int { return active ? sm_ids[i] : -1; };
+  // Pages whose last token index >= mask_from need the causal/tail mask.
+  const int mask_from = len - a.q_len + 1;
+
+  WaveState<NB> st;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    st.m[nb] = -INFINITY;
+    st.l[nb] = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) st.acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  __syncthreads();  // sm_q and sm_ids written
+
   int next_pid = page_id(D);
   for (int i = 0; i < n_pages; i += D) {
 #pragma unroll
@@ -340,28 +406,26 @@ __global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs 
 // Log-sum-exp merge of split partials (reference: csrc/small_q_attention_ext.cu:339-366):
 // M = max_s m_s; O = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M); splits
 // with l_s <= 0 are skipped and a row with no visible key is written as 0.
-// One wave per output row: lane j first takes split j's (m, l) (64 splits at a
-// time), the wave reduces the max and the weights, then every lane sums its
-// two dims over the splits with all loads of a chunk in flight.
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
+// A 256-thread workgroup merges 4 / G output rows; each row gets G waves and
+// wave g of a row sums dims 2*lane, +1 over the splits s = g (mod G) with
+// eight loads in flight. G = 1 (a wave per row) suits a few splits per row,
+// G = 4 spreads many splits over the workgroup; the G partial sums and the
+// global max meet in LDS.
+template <int G>
 __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  constexpr int kRowsPerWg = 4 / G;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wv = t >> 6;
+  const int slot = wv / G;  // row slot of this wave inside the workgroup
+  const int grp = wv % G;   // split group of this wave
+  const int row = blockIdx.x * kRowsPerWg + slot;
   const int total = a.batch * a.q_len * a.hq;
-  if (row >= total) return;
-  const int lane = threadIdx.x & 63;
-  const int h = row % a.hq;
-  const int qi = (row / a.hq) % a.q_len;
-  const int b = row / (a.hq * a.q_len);
+  const bool live = row < total;  // uniform per wave; every wave reaches the barriers
+  const int rowc = live ? row : 0;
+  const int h = rowc % a.hq;
+  const int qi = (rowc / a.hq) % a.q_len;
+  const int b = rowc / (a.hq * a.q_len);
   const int kvh = h / a.group;
   const int r = qi * a.group + (h - kvh * a.group);
 
@@ -371,55 +435,78 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   pages_used = pages_used < a.max_pages ? pages_used : a.max_pages;
   int n_valid = (pages_used + a.pages_per_split - 1) / a.pages_per_split;
   n_valid = n_valid < a.num_splits ? n_valid : a.num_splits;
+  if (!live) n_valid = 0;
 
   const size_t base = (size_t)(b * a.hkv + kvh) * a.num_splits;
-  const size_t split_stride = (size_t)a.rows;  // items between splits of one row
-  float run_m = -INFINITY;  // running max over chunks
-  float den = 0.f;
-  float acc0 = 0.f, acc1 = 0.f;
-  for (int s0 = 0; s0 < n_valid; s0 += 64) {
-    const int s = s0 + lane;
-    float ms = -INFINITY, ls = 0.f;
-    if (s < n_valid) {
-      const size_t item = (base + s) * split_stride + r;
-      ms = a.part_ml[item * 2];
-      ls = a.part_ml[item * 2 + 1];
-      if (!(ls > 0.f)) ms = -INFINITY;
-    }
-    const float cm = wave_max(ms);
-    const float new_m = fmaxf(run_m, cm);
-    if (new_m == -INFINITY) continue;  // nothing visible yet
-    const float scale_old = fast_exp2(run_m - new_m);
-    const float w = fast_exp2(ms - new_m);  // 0 for empty splits
-    den = den * scale_old + wave_sum(w * ls);
-    acc0 *= scale_old;
-    acc1 *= scale_old;
-    run_m = new_m;
-    const int n_here = min(64, n_valid - s0);
-    const float* po = a.part_o + ((base + s0) * split_stride + r) * kHeadDim + 2 * lane;
-    const size_t po_stride = split_stride * kHeadDim;
-    int j = 0;
-    for (; j + 4 <= n_here; j += 4) {
-      float2 o[4];
-      float wj[4];
+  const size_t stride = (size_t)a.rows;  // items between consecutive splits of this row
+  const float* ml = a.part_ml + (base * stride + r) * 2;
+  const float* po = a.part_o + (base * stride + r) * kHeadDim + 2 * lane;
+
+  __shared__ float sm_red[4];
+  __shared__ float sm_acc[4][2 * 64 + 1];
+
+  // 1. M over the splits that hold a positive sum.
+  float mx = -INFINITY;
+  for (int s = grp * 64 + lane; s < n_valid; s += G * 64) {
+    const float ls = ml[(size_t)s * stride * 2 + 1];
+    if (ls > 0.f) mx = fmaxf(mx, ml[(size_t)s * stride * 2]);
+  }
+  mx = wave_max(mx);
+  if (G > 1) {
+    if (lane == 0) sm_red[wv] = mx;
+    __syncthreads();
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        o[u] = *(const float2*)(po + (size_t)(j + u) * po_stride);
-        wj[u] = __shfl(w, j + u);
+    for (int g = 0; g < G; ++g) mx = fmaxf(mx, sm_red[slot * G + g]);
+  }
+
+  // 2. Weighted sums over this wave's splits.
+  float acc0 = 0.f, acc1 = 0.f, den = 0.f;
+  if (mx != -INFINITY) {
+    constexpr int kUnroll = 8;
+    int s = grp;
+    for (; s + (kUnroll - 1) * G < n_valid; s += kUnroll * G) {
+      float2 o[kUnroll];
+      float m[kUnroll], l[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const size_t it = (size_t)(s + u * G) * stride;
+        o[u] = *(const float2*)(po + it * kHeadDim);
+        m[u] = ml[it * 2];
+        l[u] = ml[it * 2 + 1];
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        acc0 += wj[u] * o[u].x;
-        acc1 += wj[u] * o[u].y;
+      for (int u = 0; u < kUnroll; ++u) {
+        const float w = l[u] > 0.f ? fast_exp2(m[u] - mx) : 0.f;
+        den += w * l[u];
+        acc0 += w * o[u].x;
+        acc1 += w * o[u].y;
       }
     }
-    for (; j < n_here; ++j) {
-      const float2 o = *(const float2*)(po + (size_t)j * po_stride);
-      const float wj = __shfl(w, j);
-      acc0 += wj * o.x;
-      acc1 += wj * o.y;
+    for (; s < n_valid; s += G) {
+      const size_t it = (size_t)s * stride;
+      const float l = ml[it * 2 + 1];
+      const float w = l > 0.f ? fast_exp2(ml[it * 2] - mx) : 0.f;
+      const float2 o = *(const float2*)(po + it * kHeadDim);
+      den += w * l;
+      acc0 += w * o.x;
+      acc1 += w * o.y;
     }
   }
+  if (G > 1) {
+    sm_acc[wv][2 * lane] = acc0;
+    sm_acc[wv][2 * lane + 1] = acc1;
+    if (lane == 0) sm_acc[wv][128] = den;
+    __syncthreads();
+    if (grp != 0) return;
+    acc0 = acc1 = den = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      den += sm_acc[slot * G + g][128];
+      acc0 += sm_acc[slot * G + g][2 * lane];
+      acc1 += sm_acc[slot * G + g][2 * lane + 1];
+    }
+  }
+  if (!live) return;
   const float inv = den > 0.f ? 1.0f / den : 0.f;
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   h2 o;
@@ -451,8 +538,13 @@ hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
 
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream) {
   const int total = a.batch * a.q_len * a.hq;
-  const dim3 grid((unsigned)((total + 3) / 4));
-  hipLaunchKernelGGL(sqa_merge_kernel, grid, dim3(256), 0, stream, a);
+  // A wave per row while the splits per row fit one pass of eight loads per
+  // lane group; four waves per row beyond that.
+  if (a.num_splits <= 32) {
+    hipLaunchKernelGGL(sqa_merge_kernel<1>, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL(sqa_merge_kernel<4>, dim3((unsigned)total), dim3(256), 0, stream, a);
+  }
   return hipGetLastError();
 }
 

@@ -70,7 +70,8 @@ def _resolve(variant, case, chunk_keys):
     if variant == "v5":
         return (lambda *a, **k: sqa.forward_v5(*a, chunk_keys=ck, token_group=case["token_group"],
                                                 max_seq_len=kv, **k)), ck
-    return (lambda *a, **k: sqa.paged_mtp_attention(*a, max_seq_len=kv, chunk_keys=ck)), ck
+    # "auto": the native entry with the automatic (CU-count) plan.
+    return (lambda *a, **k: sqa.paged_mtp_attention(*a, max_seq_len=kv)), None
 
 
 def _events(torch, n):
@@ -149,7 +150,8 @@ def main(argv=None):
     ap.add_argument("--variants", nargs="+", default=["v3"],
                     choices=("v0", "v1", "v2", "v3", "v4", "v5", "auto"))
     ap.add_argument("--chunk-keys", default="512",
-                    help="KV entries per split for v2-v5, or 'auto' (CU-count plan)")
+                    help="KV entries per split for v2-v5, or 'auto' (CU-count plan); "
+                         "variant 'auto' always uses the CU-count plan")
     ap.add_argument("--token-group", type=int, choices=(2, 4), default=2)
     ap.add_argument("--page-mode", choices=("shared", "unique", "random"), default="random")
     ap.add_argument("--q-lens", nargs="+", type=int, default=[2, 4, 8])

@@ -73,6 +73,8 @@ def test_plan_with_explicit_chunk_keys(lib):
     assert _plan(lib, chunk_keys=100, max_seq_len=1000, max_pages=63) == (SQA_OK, 9, 7)
     # Unknown max_seq_len: the plan covers the whole block-table row.
     assert _plan(lib, chunk_keys=512, max_seq_len=0, max_pages=100) == (SQA_OK, 4, 32)
+    # A split owns at most 2048 pages (the kernel's LDS page-id table).
+    assert _plan(lib, chunk_keys=1 << 20, max_seq_len=65536, max_pages=4096) == (SQA_OK, 2, 2048)
 
 
 def test_plan_rejects_bad_arguments(lib):
@@ -102,6 +104,7 @@ def _call(lib, **kw):
     (dict(page=32), SQA_ERR_UNSUPPORTED, "page_size"),
     (dict(q_len=32), SQA_ERR_UNSUPPORTED, "exceeds"),
     (dict(splits=0), SQA_ERR_INVALID, "positive"),
+    (dict(pps=2049), SQA_ERR_INVALID, "exceeds"),
     (dict(splits=2, ws=None), SQA_ERR_WORKSPACE, "workspace"),
     (dict(splits=2, ws=1, ws_bytes=100), SQA_ERR_WORKSPACE, "workspace"),
 ])
