@@ -32,10 +32,7 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(SQA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Target workgroups per compute unit for the automatic plan (one 8-wave
-// workgroup fills a CU at two waves per SIMD), and the fewest pages one split
-// may own.
-constexpr int kWgPerCu = 1;
+// The fewest pages one split of the automatic plan may own.
 constexpr int kMinPagesPerSplit = 4;
 
 std::mutex g_cu_mutex;
@@ -85,10 +82,10 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
   } else {
     int cus = sqa_device_cu_count(device);
     if (cus <= 0) return SQA_ERR_HIP;
-    const int rows = q_len * (num_query_heads / num_kv_heads);
-    const int heads_per_wg = sqa::kWgWaves / sqa::row_groups(rows);
-    const long long items = (long long)batch * ((num_kv_heads + heads_per_wg - 1) / heads_per_wg);
-    const long long target = (long long)cus * kWgPerCu;
+    // One wave of resident workgroups over the whole chip.
+    const sqa::LaunchShape sh = sqa::launch_shape(q_len * (num_query_heads / num_kv_heads));
+    const long long items = (long long)batch * ((num_kv_heads + sh.heads - 1) / sh.heads);
+    const long long target = (long long)cus * sh.wg_per_cu;
     const long long splits = ceil_div(target, items);
     pps = ceil_div(pages, splits);
     if (pps < kMinPagesPerSplit) pps = kMinPagesPerSplit;

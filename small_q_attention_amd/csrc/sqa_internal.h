@@ -38,15 +38,28 @@ struct MergeArgs {
   int max_pages, pages_per_split, num_splits;
 };
 
-// Waves per workgroup of the partial kernel. The waves of one workgroup serve
-// different kv heads (and, for 64 rows, the two 32-row halves of a head) of
-// the same (sequence, split), walking the same pages together.
-constexpr int kWgWaves = 8;
+// Launch shape of the partial kernel for a given number of query rows per kv
+// head. A workgroup serves `heads` kv heads of one (sequence, split), one wave
+// per head holding all of its rows; all waves walk the same pages, so the
+// heads' slices of a page are read together (>= 4 heads keeps HBM accesses at
+// >= 1 KiB contiguous). `wg_per_cu` workgroups are resident per CU (register
+// file), which sets the split count of the automatic plan.
+struct LaunchShape {
+  int row_blocks;  // 16-row blocks per wave (1, 2 or 4)
+  int heads;       // kv heads per workgroup (one wave each)
+  int wg_per_cu;   // resident workgroups per CU
+};
 
-// Number of 16-row blocks (1, 2 or 4) for `rows` query rows.
-inline int row_blocks(int rows) { return rows <= 16 ? 1 : (rows <= 32 ? 2 : 4); }
-// Waves per kv head: one up to 32 rows, two (32 rows each) up to 64.
-inline int row_groups(int rows) { return rows <= 32 ? 1 : 2; }
+inline LaunchShape launch_shape(int rows) {
+  // Two 4-wave workgroups per CU (2 waves per SIMD) measured best up to 32
+  // rows: a third (possible at <= 16 rows, 165 VGPRs) adds page streams per
+  // CU and lowers bandwidth. 64 rows take the whole 512-entry register file
+  // (1 wave per SIMD), which beat splitting a head's rows over two waves that
+  // each read its pages.
+  if (rows <= 16) return {1, 4, 2};
+  if (rows <= 32) return {2, 4, 2};
+  return {4, 4, 1};
+}
 
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream);
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream);

@@ -190,36 +190,33 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, co
   }
 }
 
-// One workgroup = one (sequence b, split) x kWgWaves waves. Wave w serves kv
-// head kvh_group * (kWgWaves / RG) + w / RG and row block w % RG of it (RG = 2
-// splits 64 rows into two waves of 32). All waves walk the same pages in the
-// same order, so the per-head 256-byte slices of each page are requested
-// together and HBM sees whole pages. Each wave keeps its own softmax state
-// and writes its own partial (or, with a single split, the output).
-// With RG = 1 every K/V byte is read by one wave only, so the loads are
-// non-temporal; with RG = 2 the two waves of a head read the same bytes and
-// the loads keep the default policy so the second read hits in L2.
-template <int NB, int RG, int D>
-__global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs a) {
-  constexpr int kHeadsPerWg = kWgWaves / RG;
-  constexpr int kAux = RG == 1 ? kStreamAux : 0;
+// One workgroup = one (sequence b, split) x WW waves; wave w serves kv head
+// head_group * WW + w with all of its rows (NB blocks of 16); WPE = waves per
+// SIMD the register budget allows. All waves walk the same pages in the same
+// order, so the heads' 256-byte slices of each page are requested together and
+// HBM sees whole 1 KiB (4 heads) runs; the two head groups of a page range are
+// dispatch neighbours. Each wave keeps its own softmax state and writes its
+// own partial (or, with a single split, the output). Every K/V byte is read by
+// one wave only, so the loads are non-temporal.
+template <int NB, int D, int WW, int WPE>
+__global__ __launch_bounds__(WW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
+void sqa_partial_kernel(PartialArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g16 = lane >> 4;
   const int l16 = lane & 15;
 
   // blockIdx.x = (b * num_splits + split) * head_groups + head_group.
-  const int head_groups = (a.hkv + kHeadsPerWg - 1) / kHeadsPerWg;
+  const int head_groups = (a.hkv + WW - 1) / WW;
   int wg = blockIdx.x;
   const int hgrp = wg % head_groups;
   wg /= head_groups;
   const int split = wg % a.num_splits;
   const int b = wg / a.num_splits;
-  const int kvh = hgrp * kHeadsPerWg + wave / RG;
-  const int row0 = (wave % RG) * NB * 16;
-  // Waves past the last kv head (hkv not a multiple of kHeadsPerWg) or past
-  // the last row block idle but stay for the barrier.
-  const bool active = kvh < a.hkv && row0 < a.rows;
+  const int kvh = hgrp * WW + wave;
+  // Waves past the last kv head (hkv not a multiple of WW) idle but stay for
+  // the barrier.
+  const bool active = kvh < a.hkv;
 
   const int p_begin = split * a.pages_per_split;
   const int32_t* bt_row = a.block_tables + (size_t)b * a.max_pages;
@@ -250,7 +247,7 @@ __global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs 
     // Loads are unconditional from an in-bounds address (padding rows and idle
     // waves read row 0 of kv head 0) and the value is selected afterwards, so
     // no lane-divergent branch splits the load stream.
-    const int r = row0 + nb * 16 + l16;
+    const int r = nb * 16 + l16;
     const bool real = active && r < a.rows;
     const int qi = real ? r / a.group : 0;
     const int gg = real ? r - qi * a.group : 0;
@@ -263,12 +260,12 @@ __global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs 
     }
     vis[nb] = real ? len - a.q_len + 1 + qi : 0;
   }
-  constexpr int kIdSlots = (kMaxSplitPages + kIdPad + kWgWaves * 64 - 1) / (kWgWaves * 64);
+  constexpr int kIdSlots = (kMaxSplitPages + kIdPad + WW * 64 - 1) / (WW * 64);
   int idreg[kIdSlots];
   const int last_id = n_split > 0 ? n_split - 1 : 0;  // p_begin + last_id < max_pages
 #pragma unroll
   for (int k = 0; k < kIdSlots; ++k) {
-    const int i = threadIdx.x + k * kWgWaves * 64;
+    const int i = threadIdx.x + k * WW * 64;
     const int x = bt_row[p_begin + min(i, last_id)];
     idreg[k] = i < n_split ? x : -1;
   }
@@ -294,10 +291,10 @@ __global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs 
         (void*)((const char*)a.v + off), (short)0, nrec, kBufferFlags);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      pg.k[kk] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * kk, 0, kAux);
+      pg.k[kk] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * kk, 0, kStreamAux);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      pg.v[e] = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane, e * tok_bytes, kAux);
+      pg.v[e] = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane, e * tok_bytes, kStreamAux);
   };
   // Ring of D pages in flight: page i is processed from slot i % D, which is
   // then refilled with page i + D.
@@ -312,8 +309,8 @@ __global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs 
   // and the split's page ids: ids of [p_begin, p_end) clamped into the pool,
   // then -1 for the ring's look-ahead. Waves read ids back a step ahead of
   // use, so no page waits on a block-table load from memory.
-  __shared__ h8 sm_q[kWgWaves * NB * 4 * 64];
-  __shared__ int sm_ids[kIdSlots * kWgWaves * 64];
+  __shared__ h8 sm_q[WW * NB * 4 * 64];
+  __shared__ int sm_ids[kIdSlots * WW * 64];
   h8* my_q = sm_q + wave * NB * 4 * 64;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -322,7 +319,7 @@ __global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs 
   }
 #pragma unroll
   for (int k = 0; k < kIdSlots; ++k) {
-    const int i = threadIdx.x + k * kWgWaves * 64;
+    const int i = threadIdx.x + k * WW * 64;
     sm_ids[i] = idreg[k] >= 0 ? clamp_page(idreg[k], a.num_pages) : -1;
   }
   auto page_id = [&](int i) -> int { return active ? sm_ids[i] : -1; };
@@ -363,10 +360,10 @@ __global__ __launch_bounds__(kWgWaves * 64) void sqa_partial_kernel(PartialArgs 
   for (int nb = 0; nb < NB; ++nb) st.l[nb] = xor_sum(st.l[nb]);
 
   // Lane l owns dims 32*g16 + 8*rr + mb (rr = 0..3, mb = 0..7) of row
-  // row0 + 16*nb + l16.
+  // 16*nb + l16.
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const int r = row0 + nb * 16 + l16;
+    const int r = nb * 16 + l16;
     if (r >= a.rows) continue;
     const int qi = r / a.group;
     const int gg = r - qi * a.group;
@@ -518,20 +515,16 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
 }  // namespace
 
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
-  const int heads_per_wg = kWgWaves / row_groups(a.rows);
-  const int head_groups = (a.hkv + heads_per_wg - 1) / heads_per_wg;
+  const LaunchShape sh = launch_shape(a.rows);
+  const int head_groups = (a.hkv + sh.heads - 1) / sh.heads;
   const dim3 grid((unsigned)(a.batch * a.num_splits * head_groups));
-  const dim3 block(kWgWaves * 64);
-  switch (row_blocks(a.rows)) {
-    case 1:
-      hipLaunchKernelGGL((sqa_partial_kernel<1, 1, 3>), grid, block, 0, stream, a);
-      break;
-    case 2:
-      hipLaunchKernelGGL((sqa_partial_kernel<2, 1, 3>), grid, block, 0, stream, a);
-      break;
-    default:
-      hipLaunchKernelGGL((sqa_partial_kernel<2, 2, 3>), grid, block, 0, stream, a);
-      break;
+  const dim3 block(sh.heads * 64);
+  if (sh.row_blocks == 1) {
+    hipLaunchKernelGGL((sqa_partial_kernel<1, 3, 4, 2>), grid, block, 0, stream, a);
+  } else if (sh.row_blocks == 2) {
+    hipLaunchKernelGGL((sqa_partial_kernel<2, 3, 4, 2>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((sqa_partial_kernel<4, 3, 4, 1>), grid, block, 0, stream, a);
   }
   return hipGetLastError();
 }
