@@ -78,7 +78,7 @@ def time_calls(torch, lib, tensors, plan, steps, warmup):
     q, k, v, bt, sl = tensors
     num_splits, pps = plan
     out = torch.empty_like(q)
-    nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], num_splits)
+    nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], num_splits, pps)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     stream = torch.cuda.current_stream()
     handle = stream.cuda_stream
@@ -104,7 +104,7 @@ def _ramp_clocks(torch, lib, tensors, plan, seconds=0.25):
     warmup steps (the first calls of a process otherwise run up to ~10% slow)."""
     q, k, v, bt, sl = tensors
     out = torch.empty_like(q)
-    nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], plan[0])
+    nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], plan[0], plan[1])
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     handle = torch.cuda.current_stream().cuda_stream
     t0 = time.perf_counter()
@@ -249,6 +249,28 @@ def main():
                                "kernel_us": round(px * 1e3, 2),
                                "kernel_frac": round(kvb / (px * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
         result["per_q_len"] = extra
+    if not args.no_per_q:
+        # The other single-GPU BASELINE configs, same timing (extra fields only).
+        others = {}
+        del tensors, q, k, v, bt, sl, out
+        torch.cuda.empty_cache()
+        for name in ("cfg2", "cfg5"):
+            c = inputs.baseline_configs()[name]
+            t = inputs.make_inputs(c, device="cuda", gen_device="cuda")
+            pl = _lib.plan_splits(0, c.batch, c.q_len, c.num_query_heads, c.num_kv_heads,
+                                  c.max_seq_len, t[3].shape[1], 0)
+            _ramp_clocks(torch, _lib, t, pl, seconds=0.1)
+            msx, px, mx, _ = time_calls(torch, _lib, t, pl, args.steps, args.warmup)
+            kb = inputs.kv_bytes(c.seq_lens, c.num_kv_heads, c.head_dim)
+            others[name] = {"batch": c.batch, "q_len": c.q_len, "kv_lens": "ragged" if name == "cfg5"
+                            else c.seq_lens[0], "kv_bytes": kb, "us_per_call": round(msx * 1e3, 2),
+                            "kernel_us": round(px * 1e3, 2), "merge_us": round(mx * 1e3, 2),
+                            "kernel_frac": round(kb / (px * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                            "num_splits": pl[0], "pages_per_split": pl[1]}
+            del t
+            torch.cuda.empty_cache()
+        result["other_configs"] = others
+        tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, tensors, case, args.cpu_seconds)
     print(json.dumps(result), flush=True)

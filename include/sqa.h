@@ -37,30 +37,40 @@ extern "C" {
  * Chooses the split-KV decomposition.
  * Replaces the reference chunking policy (csrc/small_q_attention_ext.cu:1096-1099,
  * :1171-1178; default chunk_keys=512 at src/small_q_attention/cuda.py:127).
- *   chunk_keys > 0: each split owns ceil(chunk_keys / 16) pages (reference meaning).
- *   chunk_keys == 0: automatic, from the device's compute-unit count.
- * max_seq_len <= 0 means "unknown": the plan covers max_pages * 16 tokens.
- * Writes *num_splits >= 1 and *pages_per_split >= 1.
+ *   chunk_keys > 0: each split owns ceil(chunk_keys / 16) pages (reference meaning);
+ *     sequence b's splits are b * num_splits + s, split s covering pages
+ *     [s * pages_per_split, (s + 1) * pages_per_split).
+ *   chunk_keys == 0: automatic, sized from the device's compute-unit count.
+ *     For 2 <= batch <= 256 this is the balanced plan, *pages_per_split = 0:
+ *     *num_splits work-item slots are shared by the whole batch and the kernel
+ *     sizes the splits on the device from the sum of seq_lens, so ragged
+ *     batches spread evenly over the chip without a host sync. Otherwise a
+ *     fixed plan as above.
+ * max_seq_len <= 0 means "unknown": a fixed plan covers max_pages * 16 tokens.
+ * Writes *num_splits >= 1 and *pages_per_split >= 0.
  */
 int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int num_kv_heads,
                     int max_seq_len, int max_pages, int chunk_keys, int* num_splits,
                     int* pages_per_split);
 
 /*
- * Device workspace bytes sqa_paged_mtp_attention needs for num_splits splits
- * (0 when num_splits == 1). Replaces the per-call torch::empty of the partial
- * buffers in the reference launchers (csrc/small_q_attention_ext.cu:1102-1104).
+ * Device workspace bytes sqa_paged_mtp_attention needs for a plan from
+ * sqa_plan_splits (0 for a fixed plan with num_splits == 1). Replaces the
+ * per-call torch::empty of the partial buffers in the reference launchers
+ * (csrc/small_q_attention_ext.cu:1102-1104).
  */
 size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv_heads,
-                           int num_splits);
+                           int num_splits, int pages_per_split);
 
 /*
  * Runs the op asynchronously on `stream` (a hipStream_t; NULL = default stream).
  * Replaces the launchers small_q_attention_v0..v5 and their pybind entries
  * forward, forward_v1..forward_v5 (csrc/small_q_attention_ext.cu:969-1378,
- * :1380-1390). num_splits/pages_per_split come from sqa_plan_splits.
- * `workspace` must hold sqa_workspace_bytes(...) bytes (may be NULL when
- * num_splits == 1). Allocates nothing and never synchronises.
+ * :1380-1390). num_splits/pages_per_split come from sqa_plan_splits
+ * (pages_per_split 0: balanced plan, batch <= 256 and num_splits >= batch +
+ * max(1, ceil(batch * max_pages / 2048))). `workspace` must hold
+ * sqa_workspace_bytes(...) bytes (may be NULL when that is 0). Allocates
+ * nothing and never synchronises.
  * `timing_events`: NULL, or an array of 3 hipEvent_t recorded on `stream`
  * before the partial kernel, between the two kernels and after the merge
  * kernel (used by the benchmark to time the partial kernel alone).

@@ -22,7 +22,7 @@ _C = ctypes
 _SIGNATURES = [
     ("sqa_plan_splits", _C.c_int,
      [_C.c_int] * 8 + [_C.POINTER(_C.c_int), _C.POINTER(_C.c_int)]),
-    ("sqa_workspace_bytes", _C.c_size_t, [_C.c_int] * 5),
+    ("sqa_workspace_bytes", _C.c_size_t, [_C.c_int] * 6),
     ("sqa_paged_mtp_attention", _C.c_int,
      [_C.c_void_p] * 7 + [_C.c_size_t] + [_C.c_int] * 5 + [_C.c_int64] + [_C.c_int] * 4
      + [_C.c_void_p, _C.c_void_p]),
@@ -76,8 +76,10 @@ def plan_splits(device_index: int, batch: int, q_len: int, num_query_heads: int,
 
 
 def workspace_bytes(batch: int, q_len: int, num_query_heads: int, num_kv_heads: int,
-                    num_splits: int) -> int:
-    return int(load().sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, num_splits))
+                    num_splits: int, pages_per_split: int) -> int:
+    """Workspace of a plan from :func:`plan_splits` (``pages_per_split`` 0 = balanced)."""
+    return int(load().sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, num_splits,
+                                          pages_per_split))
 
 
 def launch(query, key_cache, value_cache, block_tables, seq_lens, output, workspace,

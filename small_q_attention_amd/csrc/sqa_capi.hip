@@ -32,9 +32,6 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(SQA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// The fewest pages one split of the automatic plan may own.
-constexpr int kMinPagesPerSplit = 4;
-
 std::mutex g_cu_mutex;
 std::vector<int> g_cu_count;  // cached per device
 
@@ -84,11 +81,25 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
     if (cus <= 0) return SQA_ERR_HIP;
     // One wave of resident workgroups over the whole chip.
     const sqa::LaunchShape sh = sqa::launch_shape(q_len * (num_query_heads / num_kv_heads));
-    const long long items = (long long)batch * ((num_kv_heads + sh.heads - 1) / sh.heads);
-    const long long target = (long long)cus * sh.wg_per_cu;
-    const long long splits = ceil_div(target, items);
+    const long long head_groups = (num_kv_heads + sh.heads - 1) / sh.heads;
+    const long long slots_target = ceil_div((long long)cus * sh.wg_per_cu, head_groups);
+    if (batch > 1 && batch <= sqa::kMaxBalancedBatch) {
+      // Balanced plan: the kernel sizes splits from the batch's total pages,
+      // so ragged batches keep every workgroup equally busy. The slot count
+      // leaves one spare slot per sequence (rounding up each sequence's last
+      // split) and keeps a split within kMaxSplitPages pages.
+      long long target = slots_target;
+      const long long cap = ceil_div((long long)batch * max_pages, sqa::kMaxSplitPages);
+      if (target < cap) target = cap;
+      if ((target + batch) * num_kv_heads > 0x7fffffffLL)
+        return fail(SQA_ERR_INVALID, "grid too large");
+      *num_splits = (int)(target + batch);
+      *pages_per_split = 0;
+      return SQA_OK;
+    }
+    const long long splits = ceil_div(slots_target, batch);
     pps = ceil_div(pages, splits);
-    if (pps < kMinPagesPerSplit) pps = kMinPagesPerSplit;
+    if (pps < sqa::kMinSplitPages) pps = sqa::kMinSplitPages;
   }
   if (pps > pages) pps = pages;
   if (pps > sqa::kMaxSplitPages) pps = sqa::kMaxSplitPages;
@@ -103,12 +114,17 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
 }
 
 size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv_heads,
-                           int num_splits) {
-  if (num_splits <= 1 || batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_query_heads <= 0)
+                           int num_splits, int pages_per_split) {
+  if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_query_heads <= 0 || num_splits <= 0 ||
+      pages_per_split < 0)
     return 0;
+  const bool balanced = sqa::is_balanced(pages_per_split);
+  if (!balanced && num_splits == 1) return 0;
   const size_t rows = (size_t)q_len * (num_query_heads / num_kv_heads);
-  const size_t items = (size_t)batch * num_kv_heads * num_splits * rows;
-  return items * (sqa::kHeadDim + 2) * sizeof(float);
+  const size_t items = (size_t)sqa::plan_slots(batch, num_splits, pages_per_split) * num_kv_heads * rows;
+  size_t bytes = items * (sqa::kHeadDim + 2) * sizeof(float);
+  if (balanced) bytes += (size_t)batch * sizeof(sqa::SeqSplits);
+  return bytes;
 }
 
 int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void* value_cache,
@@ -133,17 +149,31 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
   const long long rows = (long long)q_len * group;
   if (rows > sqa::kMaxRows)
     return fail(SQA_ERR_UNSUPPORTED, "q_len * group = %lld exceeds %d", rows, sqa::kMaxRows);
-  if (num_splits <= 0 || pages_per_split <= 0)
-    return fail(SQA_ERR_INVALID, "num_splits and pages_per_split must be positive");
+  if (num_splits <= 0 || pages_per_split < 0)
+    return fail(SQA_ERR_INVALID, "num_splits must be positive and pages_per_split non-negative");
   if (pages_per_split > sqa::kMaxSplitPages)
     return fail(SQA_ERR_INVALID, "pages_per_split %d exceeds %d", pages_per_split,
                 sqa::kMaxSplitPages);
-  // A plan covering fewer than max_pages pages (built from a known
+  const bool balanced = sqa::is_balanced(pages_per_split);
+  if (balanced) {
+    // pages_per_split == 0 selects the balanced plan (sqa_plan_splits).
+    if (batch > sqa::kMaxBalancedBatch)
+      return fail(SQA_ERR_INVALID, "balanced plan (pages_per_split 0) needs batch <= %d, got %d",
+                  sqa::kMaxBalancedBatch, batch);
+    const long long cap = ceil_div((long long)batch * max_pages, sqa::kMaxSplitPages);
+    if ((long long)num_splits - batch < (cap > 1 ? cap : 1))
+      return fail(SQA_ERR_INVALID,
+                  "balanced plan needs num_splits >= batch + %lld (batch %d), got %d",
+                  cap > 1 ? cap : 1, batch, num_splits);
+  }
+  // A fixed plan covering fewer than max_pages pages (built from a known
   // max_seq_len) processes only the first num_splits * pages_per_split pages of
-  // each sequence, as the reference launchers do with their max_seq_len.
-  if ((long long)batch * num_kv_heads * num_splits > 0x7fffffffLL)
+  // each sequence, as the reference launchers do with their max_seq_len. The
+  // balanced plan processes every page up to seq_lens (clamped to max_pages).
+  if (sqa::plan_slots(batch, num_splits, pages_per_split) * num_kv_heads > 0x7fffffffLL)
     return fail(SQA_ERR_INVALID, "grid too large");
-  const size_t need = sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, num_splits);
+  const size_t need = sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, num_splits,
+                                          pages_per_split);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(SQA_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
                 workspace ? workspace_bytes : (size_t)0);
@@ -158,9 +188,12 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
   pa.block_tables = block_tables;
   pa.seq_lens = seq_lens;
   pa.out = (_Float16*)output;
-  const size_t items = (size_t)batch * num_kv_heads * num_splits * rows;
-  pa.part_o = num_splits > 1 ? (float*)workspace : nullptr;
-  pa.part_ml = num_splits > 1 ? (float*)workspace + items * sqa::kHeadDim : nullptr;
+  const size_t items =
+      (size_t)sqa::plan_slots(batch, num_splits, pages_per_split) * num_kv_heads * rows;
+  const bool merged = balanced || num_splits > 1;
+  pa.part_o = merged ? (float*)workspace : nullptr;
+  pa.part_ml = merged ? (float*)workspace + items * sqa::kHeadDim : nullptr;
+  pa.seq_splits = balanced ? (sqa::SeqSplits*)(pa.part_ml + items * 2) : nullptr;
   pa.num_pages = num_pages;
   pa.batch = batch;
   pa.q_len = q_len;
@@ -177,10 +210,11 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
   if ((e = sqa::launch_partial(pa, s)) != hipSuccess) return hip_fail(e, "partial kernel launch");
   if (ev && (e = hipEventRecord(ev[1], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-  if (num_splits > 1) {
+  if (merged) {
     sqa::MergeArgs ma;
     ma.part_o = pa.part_o;
     ma.part_ml = pa.part_ml;
+    ma.seq_splits = pa.seq_splits;
     ma.seq_lens = seq_lens;
     ma.out = pa.out;
     ma.batch = batch;

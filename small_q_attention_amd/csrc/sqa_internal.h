@@ -11,8 +11,27 @@ constexpr int kHeadDim = 128;   // contract: head_dim 128
 constexpr int kPageSize = 16;   // contract: 16-token pages
 constexpr int kMaxRows = 64;    // q_len * (Hq / Hkv) rows one work item holds
 constexpr int kMaxSplitPages = 2048;  // pages one split may own (LDS page-id table)
+constexpr int kMinSplitPages = 4;     // fewest pages the automatic plans give a split
+constexpr int kMaxBalancedBatch = 256;  // balanced plan: one sequence per thread of a workgroup
+
+// Per-sequence split layout of the balanced plan, written by the partial
+// kernel for the merge kernel: first slot and number of splits.
+struct SeqSplits {
+  int first;
+  int count;
+};
 
 // Everything the split-KV partial kernel needs. Element counts, not bytes.
+//
+// Two split plans. Fixed (pages_per_split > 0): sequence b owns slots
+// b * num_splits + s, split s covering pages [s * pages_per_split, ...).
+// Balanced (pages_per_split == 0, batch <= kMaxBalancedBatch): num_splits is
+// the number of work-item slots; every workgroup derives, from all seq_lens,
+// one split size for the whole batch (total pages / (num_splits - batch),
+// rounded up) and the (sequence, split) of its item, so all items carry the
+// same number of pages whatever the length distribution. Partial slot of
+// (sequence, split) = first slot of the sequence + split; sequences whose
+// pages fit one split are written straight to the output.
 struct PartialArgs {
   const _Float16* q;          // [B, Q, Hq, 128]
   const _Float16* k;          // [num_pages, 16, Hkv, 128]
@@ -20,8 +39,9 @@ struct PartialArgs {
   const int32_t* block_tables;  // [B, max_pages]
   const int32_t* seq_lens;      // [B]
   _Float16* out;              // [B, Q, Hq, 128]; written directly when num_splits == 1
-  float* part_o;              // [B, Hkv, num_splits, rows, 128] unnormalised sums
-  float* part_ml;             // [B, Hkv, num_splits, rows, 2] (max in log2 units, sum)
+  float* part_o;              // [slots, Hkv, rows, 128] unnormalised sums
+  float* part_ml;             // [slots, Hkv, rows, 2] (max in log2 units, sum)
+  SeqSplits* seq_splits;      // [B] (balanced plan only)
   long long num_pages;        // pages in the cache pool; ids outside are clamped to 0
   int batch, q_len, hq, hkv, group, rows;
   int max_pages;              // block_tables row length
@@ -29,9 +49,17 @@ struct PartialArgs {
   float scale_log2;           // head_dim^-1/2 * log2(e)
 };
 
+__host__ __device__ inline bool is_balanced(int pages_per_split) { return pages_per_split == 0; }
+
+// Partial slots a plan uses.
+inline long long plan_slots(int batch, int num_splits, int pages_per_split) {
+  return is_balanced(pages_per_split) ? (long long)num_splits : (long long)batch * num_splits;
+}
+
 struct MergeArgs {
   const float* part_o;
   const float* part_ml;
+  const SeqSplits* seq_splits;  // balanced plan only
   const int32_t* seq_lens;
   _Float16* out;
   int batch, q_len, hq, hkv, group, rows;

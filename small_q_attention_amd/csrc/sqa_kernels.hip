@@ -190,6 +190,128 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, co
   }
 }
 
+// Block-wide sum and exclusive scan over NT threads (sm: NT / 64 ints). Both
+// end with a barrier, so sm can be reused right after.
+template <int NT>
+__device__ __forceinline__ int block_sum(int v, int* sm) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  if (lane == 0) sm[wave] = v;
+  __syncthreads();
+  int total = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) total += sm[w];
+  __syncthreads();
+  return total;
+}
+
+template <int NT>
+__device__ __forceinline__ int block_exclusive_scan(int v, int* sm) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) sm[wave] = x;
+  __syncthreads();
+  int off = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) off += w < wave ? sm[w] : 0;
+  __syncthreads();
+  return off + x - v;
+}
+
+// The page range one workgroup owns and where its sequence's result goes.
+struct ItemRange {
+  int b;        // sequence (-1: no work item for this workgroup)
+  int split;    // split index within the sequence
+  int p_begin;  // first page (logical index within the sequence)
+  int p_end;    // one past the last page
+  int len;      // seq_lens[b], clamped to >= 0
+  int n_valid;  // splits of this sequence that own pages
+  int slot0;    // partial slot of split 0 of this sequence
+};
+
+// Fixed plan: sequence b owns slots b * num_splits + s.
+__device__ __forceinline__ ItemRange fixed_item(const PartialArgs& a, int item) {
+  ItemRange r;
+  r.b = item / a.num_splits;
+  r.split = item - r.b * a.num_splits;
+  r.p_begin = r.split * a.pages_per_split;
+  r.len = max(a.seq_lens[r.b], 0);
+  const int pages = min((r.len + kPageSize - 1) / kPageSize, a.max_pages);
+  r.p_end = min(r.p_begin + a.pages_per_split, pages);
+  r.n_valid = min((pages + a.pages_per_split - 1) / a.pages_per_split, a.num_splits);
+  r.slot0 = r.b * a.num_splits;
+  return r;
+}
+
+// Balanced plan (all NT threads call it; batch <= NT). num_splits = T +
+// batch slots, T = the work items one wave of resident workgroups holds.
+// Thread t takes sequence t and the workgroup picks one split size for the
+// batch: the smallest in [ceil(total / T), ceil(total / (T - batch))] (clamped
+// to [kMinSplitPages, kMaxSplitPages]) whose per-sequence split counts sum to
+// at most T (bisection over block sums), so no workgroup waits for a second
+// wave; the lower end alone always fits the T + batch slots. A scan of the
+// split counts then gives each sequence its first slot; the thread whose
+// sequence holds `item` publishes it. Workgroup 0 also stores every sequence's
+// (first slot, split count) for the merge kernel. Every workgroup computes the
+// same plan from the same seq_lens.
+template <int NT>
+__device__ ItemRange balanced_item(const PartialArgs& a, int item, int* sm) {
+  const int t = threadIdx.x;
+  if (t < 6) sm[8 + t] = t == 0 ? -1 : 0;  // defaults: no work item
+  int len = 0, pages = 0;
+  if (t < a.batch) {
+    len = max(a.seq_lens[t], 0);
+    pages = min((len + kPageSize - 1) / kPageSize, a.max_pages);
+  }
+  const int total = block_sum<NT>(pages, sm);
+  const int target = a.num_splits - a.batch;
+  const int lo = min(max((total + target - 1) / target, kMinSplitPages), kMaxSplitPages);
+  int hi = lo;
+  if (target > a.batch)
+    hi = min(max((total + target - a.batch - 1) / (target - a.batch), lo), kMaxSplitPages);
+  int pps = lo;
+  if (hi > lo && block_sum<NT>((pages + lo - 1) / lo, sm) > target) {
+    int l = lo + 1, h = hi;  // uniform bisection: smallest size in (lo, hi] that fits
+    while (l < h) {
+      const int mid = (l + h) >> 1;
+      if (block_sum<NT>((pages + mid - 1) / mid, sm) <= target)
+        h = mid;
+      else
+        l = mid + 1;
+    }
+    pps = h;
+  }
+  const int splits = (pages + pps - 1) / pps;
+  const int first = block_exclusive_scan<NT>(splits, sm);
+  if (t < a.batch) {
+    if (blockIdx.x == 0) a.seq_splits[t] = SeqSplits{first, splits};
+    if (item >= first && item < first + splits) {
+      sm[8] = t;
+      sm[9] = item - first;
+      sm[10] = len;
+      sm[11] = pages;
+      sm[12] = first;
+      sm[13] = splits;
+    }
+  }
+  __syncthreads();
+  ItemRange r;
+  r.b = sm[8];
+  r.split = sm[9];
+  r.len = sm[10];
+  r.p_begin = r.split * pps;
+  r.p_end = min(r.p_begin + pps, sm[11]);
+  r.slot0 = sm[12];
+  r.n_valid = sm[13];
+  return r;
+}
+
 // One workgroup = one (sequence b, split) x WW waves; wave w serves kv head
 // head_group * WW + w with all of its rows (NB blocks of 16); WPE = waves per
 // SIMD the register budget allows. All waves walk the same pages in the same
@@ -206,36 +328,41 @@ void sqa_partial_kernel(PartialArgs a) {
   const int g16 = lane >> 4;
   const int l16 = lane & 15;
 
-  // blockIdx.x = (b * num_splits + split) * head_groups + head_group.
+  // blockIdx.x = item * head_groups + head_group.
   const int head_groups = (a.hkv + WW - 1) / WW;
-  int wg = blockIdx.x;
-  const int hgrp = wg % head_groups;
-  wg /= head_groups;
-  const int split = wg % a.num_splits;
-  const int b = wg / a.num_splits;
+  const int hgrp = blockIdx.x % head_groups;
+  const int item = blockIdx.x / head_groups;
   const int kvh = hgrp * WW + wave;
   // Waves past the last kv head (hkv not a multiple of WW) idle but stay for
   // the barrier.
   const bool active = kvh < a.hkv;
 
-  const int p_begin = split * a.pages_per_split;
+  // Start-up is two memory round trips. First: the work item (fixed plan:
+  // the sequence length, with the ids of the split's first D pages loaded
+  // alongside; balanced plan: all seq_lens and a workgroup scan).
+  __shared__ int sm_plan[16];
+  const bool balanced = is_balanced(a.pages_per_split);
+  const ItemRange it = balanced ? balanced_item<WW * 64>(a, item, sm_plan) : fixed_item(a, item);
+  const bool single = !balanced && a.num_splits == 1;  // no merge kernel follows
+  const int b = max(it.b, 0);
+  const int split = it.split;
+  const int len = it.len;
+  const int p_begin = it.p_begin;
+  const int p_end = it.p_end;
   const int32_t* bt_row = a.block_tables + (size_t)b * a.max_pages;
-
-  // Start-up is two memory round trips. First (scalar, together): the
-  // sequence length and the ids of the split's first D pages (index clamped
-  // into the block-table row; ids past the sequence are never used).
+  // Ids of the split's first D pages (index clamped into the block-table row;
+  // ids past the split are never used), issued before the exits below so the
+  // fixed plan loads them together with the sequence length.
   int first_id[D];
 #pragma unroll
-  for (int j = 0; j < D; ++j) first_id[j] = bt_row[min(p_begin + j, a.max_pages - 1)];
-  int len = a.seq_lens[b];
-  len = len < 0 ? 0 : len;
-  int pages_used = (len + kPageSize - 1) / kPageSize;
-  pages_used = pages_used < a.max_pages ? pages_used : a.max_pages;
-  const int p_end = min(p_begin + a.pages_per_split, pages_used);
-  const bool single = a.num_splits == 1;
-  if (p_begin >= p_end && !single) return;  // uniform per workgroup; never merged
+  for (int j = 0; j < D; ++j) first_id[j] = bt_row[min(max(p_begin + j, 0), a.max_pages - 1)];
+  if (it.b < 0) return;                           // uniform: no work item
+  if (p_begin >= p_end && !single) return;        // uniform; never merged
   const int n_split = p_end > p_begin ? p_end - p_begin : 0;
   const int n_pages = active ? n_split : 0;
+  // A sequence with at most one split is finished here; otherwise this
+  // workgroup leaves a partial for the merge kernel.
+  const bool direct = it.n_valid <= 1;
 
   // Second: Q fragments, the rest of the split's page ids and the first D
   // pages, all in flight at once (Q and ids first, so waiting for them leaves
@@ -367,7 +494,7 @@ void sqa_partial_kernel(PartialArgs a) {
     if (r >= a.rows) continue;
     const int qi = r / a.group;
     const int gg = r - qi * a.group;
-    if (single) {
+    if (direct) {
       const float inv = st.l[nb] > 0.f ? 1.0f / st.l[nb] : 0.f;
       _Float16* op =
           a.out + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * kHeadDim + 32 * g16;
@@ -379,8 +506,8 @@ void sqa_partial_kernel(PartialArgs a) {
         *(h8*)(op + 8 * rr) = o;
       }
     } else {
-      const size_t item = ((size_t)(b * a.hkv + kvh) * a.num_splits + split) * a.rows + r;
-      float* op = a.part_o + item * kHeadDim + 32 * g16;
+      const size_t pitem = ((size_t)(it.slot0 + split) * a.hkv + kvh) * a.rows + r;
+      float* op = a.part_o + pitem * kHeadDim + 32 * g16;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         f4 lo, hi;
@@ -393,8 +520,8 @@ void sqa_partial_kernel(PartialArgs a) {
         *(f4*)(op + 8 * rr + 4) = hi;
       }
       if (g16 == 0) {
-        a.part_ml[item * 2 + 0] = st.m[nb];
-        a.part_ml[item * 2 + 1] = st.l[nb];
+        a.part_ml[pitem * 2 + 0] = st.m[nb];
+        a.part_ml[pitem * 2 + 1] = st.l[nb];
       }
     }
   }
@@ -426,18 +553,25 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   const int kvh = h / a.group;
   const int r = qi * a.group + (h - kvh * a.group);
 
-  int len = a.seq_lens[b];
-  len = len < 0 ? 0 : len;
-  int pages_used = (len + kPageSize - 1) / kPageSize;
-  pages_used = pages_used < a.max_pages ? pages_used : a.max_pages;
-  int n_valid = (pages_used + a.pages_per_split - 1) / a.pages_per_split;
-  n_valid = n_valid < a.num_splits ? n_valid : a.num_splits;
-  if (!live) n_valid = 0;
+  int n_valid, slot0;
+  if (is_balanced(a.pages_per_split)) {
+    const SeqSplits ss = a.seq_splits[b];
+    n_valid = ss.count;
+    slot0 = ss.first;
+  } else {
+    const int len = max(a.seq_lens[b], 0);
+    const int pages = min((len + kPageSize - 1) / kPageSize, a.max_pages);
+    n_valid = min((pages + a.pages_per_split - 1) / a.pages_per_split, a.num_splits);
+    slot0 = b * a.num_splits;
+  }
+  // A sequence with one split was written by the partial kernel.
+  const bool skip = !live || n_valid == 1;
+  if (skip) n_valid = 0;
 
-  const size_t base = (size_t)(b * a.hkv + kvh) * a.num_splits;
-  const size_t stride = (size_t)a.rows;  // items between consecutive splits of this row
-  const float* ml = a.part_ml + (base * stride + r) * 2;
-  const float* po = a.part_o + (base * stride + r) * kHeadDim + 2 * lane;
+  const size_t stride = (size_t)a.hkv * a.rows;  // items between consecutive splits of this row
+  const size_t first = ((size_t)slot0 * a.hkv + kvh) * a.rows + r;
+  const float* ml = a.part_ml + first * 2;
+  const float* po = a.part_o + first * kHeadDim + 2 * lane;
 
   __shared__ float sm_red[4];
   __shared__ float sm_acc[4][2 * 64 + 1];
@@ -503,7 +637,7 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
       acc1 += sm_acc[slot * G + g][2 * lane + 1];
     }
   }
-  if (!live) return;
+  if (skip) return;
   const float inv = den > 0.f ? 1.0f / den : 0.f;
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   h2 o;
@@ -517,7 +651,7 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
   const LaunchShape sh = launch_shape(a.rows);
   const int head_groups = (a.hkv + sh.heads - 1) / sh.heads;
-  const dim3 grid((unsigned)(a.batch * a.num_splits * head_groups));
+  const dim3 grid((unsigned)(plan_slots(a.batch, a.num_splits, a.pages_per_split) * head_groups));
   const dim3 block(sh.heads * 64);
   if (sh.row_blocks == 1) {
     hipLaunchKernelGGL((sqa_partial_kernel<1, 3, 4, 2>), grid, block, 0, stream, a);
@@ -532,8 +666,12 @@ hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream) {
   const int total = a.batch * a.q_len * a.hq;
   // A wave per row while the splits per row fit one pass of eight loads per
-  // lane group; four waves per row beyond that.
-  if (a.num_splits <= 32) {
+  // lane group; four waves per row beyond that. The balanced plan's split
+  // count per sequence is known only on the device: use the batch average.
+  const int per_row = is_balanced(a.pages_per_split)
+                          ? (a.num_splits - a.batch + a.batch - 1) / a.batch
+                          : a.num_splits;
+  if (per_row <= 32) {
     hipLaunchKernelGGL(sqa_merge_kernel<1>, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, a);
   } else {
     hipLaunchKernelGGL(sqa_merge_kernel<4>, dim3((unsigned)total), dim3(256), 0, stream, a);

@@ -47,11 +47,16 @@ def test_version_and_empty_error(lib):
 
 
 def test_workspace_bytes(lib):
-    # rows = q_len * group; items = B * Hkv * splits * rows; 130 floats each.
-    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 1) == 0
-    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 16) == 16 * 8 * 16 * 32 * 130 * 4
-    assert lib.sqa_workspace_bytes(1, 2, 32, 8, 3) == 1 * 8 * 3 * 8 * 130 * 4
-    assert lib.sqa_workspace_bytes(0, 2, 32, 8, 3) == 0
+    # Fixed plan: rows = q_len * group; items = B * Hkv * splits * rows; 130 floats each.
+    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 1, 2048) == 0
+    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 16, 128) == 16 * 8 * 16 * 32 * 130 * 4
+    assert lib.sqa_workspace_bytes(1, 2, 32, 8, 3, 4) == 1 * 8 * 3 * 8 * 130 * 4
+    assert lib.sqa_workspace_bytes(0, 2, 32, 8, 3, 4) == 0
+    # Balanced plan (pages_per_split 0): num_splits slots shared by the batch,
+    # plus one (first slot, count) pair of int32 per sequence.
+    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 272, 0) == 272 * 8 * 32 * 130 * 4 + 16 * 8
+    assert lib.sqa_workspace_bytes(2, 2, 32, 8, 1, 0) == 1 * 8 * 8 * 130 * 4 + 2 * 8
+    assert lib.sqa_workspace_bytes(2, 2, 32, 8, 3, -1) == 0
 
 
 def _plan(lib, **kw):
@@ -105,6 +110,14 @@ def _call(lib, **kw):
     (dict(q_len=32), SQA_ERR_UNSUPPORTED, "exceeds"),
     (dict(splits=0), SQA_ERR_INVALID, "positive"),
     (dict(pps=2049), SQA_ERR_INVALID, "exceeds"),
+    (dict(pps=-1), SQA_ERR_INVALID, "non-negative"),
+    # Balanced plan: at most 256 sequences, at least one spare slot per sequence
+    # plus enough slots to keep every split within 2048 pages.
+    (dict(pps=0, batch=257, splits=600, ws=1, ws_bytes=1 << 40), SQA_ERR_INVALID, "batch <= 256"),
+    (dict(pps=0, batch=4, splits=4, ws=1, ws_bytes=1 << 40), SQA_ERR_INVALID, "num_splits >="),
+    (dict(pps=0, batch=4, splits=7, max_pages=2049, ws=1, ws_bytes=1 << 40), SQA_ERR_INVALID,
+     "num_splits >= batch + 5"),
+    (dict(pps=0, batch=2, splits=3, ws=None), SQA_ERR_WORKSPACE, "workspace"),
     (dict(splits=2, ws=None), SQA_ERR_WORKSPACE, "workspace"),
     (dict(splits=2, ws=1, ws_bytes=100), SQA_ERR_WORKSPACE, "workspace"),
 ])

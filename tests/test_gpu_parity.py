@@ -111,6 +111,47 @@ def test_ragged_batch_on_scattered_pool(q_len):
         assert st["max_abs_vs_f64_oracle"] < 2e-3
 
 
+@pytest.mark.parametrize("q_len", [2, 8, 16])
+def test_balanced_plan_on_a_skewed_batch(q_len):
+    """The automatic plan for 2..256 sequences (pages_per_split 0): one long sequence
+    among empty, tiny and short ones. Splits are sized on the device from the sum of
+    seq_lens; sequences with one split are written by the partial kernel, the rest by
+    the merge, sequences without pages as zeros."""
+    lens = [0, 1, q_len - 1, q_len, 16, 17, 200, 37000, 5, 0, 900, 4096]
+    case = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=400 + q_len)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    bt = tensors[3]
+    ns, pps = _lib.plan_splits(0, len(lens), q_len, 32, 8, max(lens), bt.shape[1], 0)
+    assert pps == 0 and ns > len(lens)
+    ref = _oracle(tensors)
+    out = sqa.paged_mtp_attention(*tensors, 16, max(lens))
+    assert_parity(out, ref, label=f"balanced q{q_len}")
+    fixed = sqa.paged_mtp_attention(*tensors, 16, max(lens), chunk_keys=512)
+    assert (out.float() - fixed.float()).abs().max().item() <= 2e-3
+    assert torch.all(out[0] == 0) and torch.all(out[9] == 0)
+
+
+def test_balanced_plan_at_the_batch_limit():
+    """256 sequences (the balanced plan's limit; one per thread of the plan scan)
+    and 257 (fixed plan), on a block table wide enough that the 2048-page split cap
+    sets the slot count."""
+    for batch in (256, 257):
+        g = torch.Generator().manual_seed(batch)
+        lens = torch.randint(0, 400, (batch,), generator=g).tolist()
+        case = inputs.Case(batch=batch, q_len=4, seq_lens=lens, seed=batch)
+        q, k, v, bt, sl = inputs.make_inputs(case)
+        wide = torch.zeros(batch, 4096, dtype=torch.int32)  # 2x the cap: slots >= 2 * batch
+        wide[:, :bt.shape[1]] = bt
+        tensors = _to_gpu((q, k, v, wide, sl))
+        ns, pps = _lib.plan_splits(0, batch, 4, 32, 8, 0, 4096, 0)
+        if batch == 256:
+            assert pps == 0 and ns >= batch + batch * 4096 // 2048
+        else:
+            assert pps > 0
+        out = sqa.paged_mtp_attention(*tensors, 16)
+        assert_parity(out, _oracle(tensors), label=f"B{batch}")
+
+
 def test_rows_without_visible_keys_are_zero():
     """seq_len < q_len: rows qi < q_len - seq_len see nothing and are written as 0
     (reference v2-v5 merge, csrc/small_q_attention_ext.cu:365); seq_len 0 gives 0."""
@@ -215,7 +256,7 @@ def test_c_abi_direct_with_caller_workspace():
     q, k, v, bt, sl = tensors
     ns, pps = _lib.plan_splits(0, 3, 4, 32, 8, 1500, bt.shape[1], 256)
     assert ns > 1
-    ws = torch.empty(_lib.workspace_bytes(3, 4, 32, 8, ns), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(_lib.workspace_bytes(3, 4, 32, 8, ns, pps), dtype=torch.uint8, device="cuda")
     out = torch.empty_like(q)
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     for e in evs:
