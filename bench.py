@@ -56,6 +56,8 @@ def _parse():
     ap.add_argument("--no-per-q", action="store_true", help="skip the q_len 2/4/16 extras")
     ap.add_argument("--q-len", type=int, default=0,
                     help="override the workload's q_len (profiling other rows per kv head)")
+    ap.add_argument("--config", default="cfg3", choices=("cfg2", "cfg3", "cfg5"),
+                    help="workload (cfg3 is the bench line; others for profiling)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -150,6 +152,17 @@ def cpu_baseline(torch, tensors, case, target_s):
     }
 
 
+def _describe(name, case):
+    lens = set(case.seq_lens)
+    kv = (f"KV{case.seq_lens[0]}" if len(lens) == 1
+          else f"ragged KV {min(lens)}..{max(lens)} (sum {sum(case.seq_lens)})")
+    extra = (f", K x{case.k_outlier_scale:g} on {100 * case.k_outlier_frac:g}% of slots"
+             if case.k_outlier_frac else "")
+    return (f"{name}: B{case.batch} q_len{case.q_len} {kv} Hq/Hkv{case.num_query_heads}/"
+            f"{case.num_kv_heads} d{case.head_dim} page{case.page_size}{extra}, "
+            f"{case.page_mode} page table over a {case.pool_factor}x pool")
+
+
 def _cpu_model():
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -185,7 +198,7 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    case = inputs.baseline_configs()["cfg3"]
+    case = inputs.baseline_configs()[args.config]
     if args.q_len:
         case.q_len = args.q_len
     tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
@@ -215,9 +228,9 @@ def main():
         "dtype": "fp16 in/out, fp32 accumulate",
         "data": "synthetic: N(0,1) fp16 Q/K/V drawn on the device, seeded",
         "config": {
-            "workload": f"cfg3: B16 q_len{case.q_len} KV32768 Hq/Hkv32/8 d128 page16, K x4 on 1% "
-                        "of slots, random page table over a 2x pool",
-            "batch": case.batch, "q_len": case.q_len, "kv_len": case.seq_lens[0],
+            "workload": _describe(args.config, case),
+            "batch": case.batch, "q_len": case.q_len,
+            "kv_len": case.seq_lens[0] if len(set(case.seq_lens)) == 1 else "ragged",
             "num_splits": plan[0], "pages_per_split": plan[1],
             "kv_bytes": kvb, "alg_bytes": inputs.alg_bytes(case),
         },

@@ -44,6 +44,25 @@ def kernel_stats(trace_dir):
             for r in rows if "sqa" in r["Name"]}
 
 
+def last_dispatches_us(trace_dir, n):
+    """Mean duration (us) of each kernel's last ``n`` dispatches: the bench's timed steps
+    (the warmup and clock-ramp calls come first)."""
+    hits = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not hits or n <= 0:
+        return {}
+    per = collections.defaultdict(list)
+    for r in csv.DictReader(open(hits[0])):
+        if "sqa" in r["Kernel_Name"]:
+            per[_short(r["Kernel_Name"])].append(
+                (int(r["Start_Timestamp"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    out = {}
+    for name, d in per.items():
+        d.sort()
+        tail = [dur for _, dur in d[-n:]]
+        out[name] = sum(tail) / len(tail) / 1e3
+    return out
+
+
 def counters(pmc_dir):
     rows = list(csv.DictReader(open(_one(os.path.join(pmc_dir, "**", "*counter_collection.csv")))))
     per = collections.defaultdict(list)
@@ -64,12 +83,15 @@ def main(argv=None):
     ap.add_argument("--write", required=True)
     ap.add_argument("--mfma")
     ap.add_argument("--kv-bytes", type=int, required=True, help="algorithmic KV bytes per call")
+    ap.add_argument("--steps", type=int, default=20,
+                    help="timed steps of the traced bench run (their dispatches come last)")
     ap.add_argument("--workload", required=True)
     ap.add_argument("--command", required=True, help="the command line that produced the CSVs")
     ap.add_argument("--out", required=True)
     args = ap.parse_args(argv)
 
     stats = kernel_stats(args.trace)
+    timed = last_dispatches_us(args.trace, args.steps)
     fetch, fcopy = counters(args.fetch)
     write, wcopy = counters(args.write)
     fscale = COPY_BYTES / (1024 * sum(v for _, v in fcopy) / len(fcopy))
@@ -95,6 +117,12 @@ def main(argv=None):
             partial_traffic = fbytes + wbytes
             lines.append(f"partial_kernel_avg_us: {avg:.2f}")
             lines.append(f"partial_kernel_kv_GBps: {args.kv_bytes / (avg * 1e-6) / 1e9:.1f}")
+            if name in timed:
+                t = timed[name]
+                lines.append(f"partial_kernel_timed_steps_avg_us: {t:.2f} (last {args.steps} "
+                             "dispatches = the bench's timed steps)")
+                lines.append(f"partial_kernel_timed_steps_kv_GBps: "
+                             f"{args.kv_bytes / (t * 1e-6) / 1e9:.1f}")
     if partial_traffic is not None:
         lines.append(f"traffic_bytes_per_launch: {partial_traffic:.0f}")
     if args.mfma:
