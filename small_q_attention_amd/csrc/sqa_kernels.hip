@@ -6,14 +6,16 @@
 // token t is slot t % 16 of page block_tables[b, t / 16]; scale head_dim^-1/2;
 // fp32 softmax; fp16 output.
 //
-// Work decomposition. One workgroup owns (sequence b, kv head, split) and holds
-// every query row that reads that kv head: rows = q_len * group, row
-// r = qi * group + g <-> query head kvh * group + g. Each K/V byte is loaded
-// from HBM once and used by all rows, straight from registers: the four waves
-// of the workgroup take interleaved pages of the split and merge their
-// (max, sum, output) states through LDS at the end.
+// Work decomposition. One workgroup owns one work item (sequence b, split: a
+// range of its pages) for 4 kv heads, one wave per kv head. A wave holds every
+// query row that reads its kv head: rows = q_len * group, row
+// r = qi * group + g <-> query head kvh * group + g, so each K/V byte is loaded
+// from HBM once and used by all rows straight from registers. The four waves
+// walk the same pages in step, so a page's four 256-byte head slices per token
+// are requested together (1 KiB contiguous runs).
 //
-// Per 16-token page a wave issues 4 K and 4 V global_load_dwordx4 (1 KiB each).
+// Per 16-token page a wave issues 4 K and 4 V 16-byte-per-lane buffer loads
+// (1 KiB each).
 //   S^T[token][row] = K . Q^T : v_mfma_f32_16x16x32_f16, A = K (lane l: token
 //     l%16, 8 consecutive dims), B = Q^T (lane l: row l%16, same dims). The head
 //     dimension is contracted in the order d = 32*kk + 8*(l/16) + e, which is
@@ -22,7 +24,7 @@
 //     (lane l: tokens 4*(l/16)+0..3 of row l%16) is exactly the B operand, so
 //     P never leaves its registers. Lane l loads V rows 4*(l/16)+0..3, dims
 //     8*(l%16)+0..7 (four full 256-byte rows per instruction) and regroups
-//     them with one bit-select per half pair: output block mb covers dims
+//     them with one byte permute per half pair: output block mb covers dims
 //     d = 8*m + mb, m = 0..15.
 // Rows beyond q_len*group (q_len*group not a multiple of 16) carry zero Q and
 // are never stored.
