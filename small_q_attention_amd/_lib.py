@@ -7,6 +7,7 @@ point raises ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 from pathlib import Path
 
@@ -64,8 +65,11 @@ def last_error(lib) -> str:
     return msg.decode() if msg else "unknown error"
 
 
+@functools.lru_cache(maxsize=4096)
 def plan_splits(device_index: int, batch: int, q_len: int, num_query_heads: int,
                 num_kv_heads: int, max_seq_len: int, max_pages: int, chunk_keys: int):
+    """``sqa_plan_splits`` -> ``(num_splits, pages_per_split)``; memoised (the plan is a
+    pure function of its arguments and the device's CU count)."""
     lib = load()
     ns, pps = ctypes.c_int(0), ctypes.c_int(0)
     rc = lib.sqa_plan_splits(device_index, batch, q_len, num_query_heads, num_kv_heads,
@@ -75,6 +79,7 @@ def plan_splits(device_index: int, batch: int, q_len: int, num_query_heads: int,
     return ns.value, pps.value
 
 
+@functools.lru_cache(maxsize=4096)
 def workspace_bytes(batch: int, q_len: int, num_query_heads: int, num_kv_heads: int,
                     num_splits: int, pages_per_split: int) -> int:
     """Workspace of a plan from :func:`plan_splits` (``pages_per_split`` 0 = balanced)."""
@@ -82,24 +87,50 @@ def workspace_bytes(batch: int, q_len: int, num_query_heads: int, num_kv_heads: 
                                           pages_per_split))
 
 
+def raw_stream(device_index: int) -> int:
+    """Handle of torch's current stream on ``device_index`` (a ``hipStream_t`` as int)."""
+    import torch
+
+    getter = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if getter is not None:
+        return getter(device_index)
+    return torch.cuda.current_stream(device_index).cuda_stream
+
+
 def launch(query, key_cache, value_cache, block_tables, seq_lens, output, workspace,
            num_splits: int, pages_per_split: int, stream_handle: int, timing_events=None):
     """Call ``sqa_paged_mtp_attention`` on raw device pointers of torch tensors."""
-    lib = load()
+    lib = _LIB if _LIB is not None else load()
     b, q_len, hq, d = query.shape
     ev = None
     if timing_events is not None:
         ev = (ctypes.c_void_p * 3)(*[ctypes.c_void_p(int(e)) for e in timing_events])
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    kshape = key_cache.shape
     rc = lib.sqa_paged_mtp_attention(
         query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
         block_tables.data_ptr(), seq_lens.data_ptr(), output.data_ptr(),
-        ws_ptr, ws_bytes, b, q_len, hq, key_cache.shape[2], d,
-        key_cache.shape[0], key_cache.shape[1], block_tables.shape[1],
+        ws_ptr, ws_bytes, b, q_len, hq, kshape[2], d,
+        kshape[0], kshape[1], block_tables.shape[1],
         num_splits, pages_per_split, stream_handle, ev)
     if rc != SQA_OK:
         raise RuntimeError(f"sqa_paged_mtp_attention failed: {last_error(lib)}")
+
+
+def run(query, key_cache, value_cache, block_tables, seq_lens, num_splits: int,
+        pages_per_split: int):
+    """Allocate the output and workspace with torch's caching allocator and launch on the
+    current stream of the query's device. Returns the output."""
+    import torch
+
+    out = torch.empty_like(query)
+    b, q_len, hq, _ = query.shape
+    nbytes = workspace_bytes(b, q_len, hq, key_cache.shape[2], num_splits, pages_per_split)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=query.device) if nbytes else None
+    launch(query, key_cache, value_cache, block_tables, seq_lens, out, ws, num_splits,
+           pages_per_split, raw_stream(query.device.index))
+    return out
 
 
 def custom_op():

@@ -16,14 +16,8 @@ def paged_mtp_attention(query: torch.Tensor, key_cache: torch.Tensor,
                         value_cache: torch.Tensor, block_tables: torch.Tensor,
                         seq_lens: torch.Tensor, num_splits: int,
                         pages_per_split: int) -> torch.Tensor:
-    out = torch.empty_like(query)
-    b, q_len, hq, _ = query.shape
-    nbytes = _lib.workspace_bytes(b, q_len, hq, key_cache.shape[2], num_splits, pages_per_split)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=query.device) if nbytes else None
-    stream = torch.cuda.current_stream(query.device).cuda_stream
-    _lib.launch(query, key_cache, value_cache, block_tables, seq_lens, out, ws,
-                num_splits, pages_per_split, stream)
-    return out
+    return _lib.run(query, key_cache, value_cache, block_tables, seq_lens, num_splits,
+                    pages_per_split)
 
 
 @paged_mtp_attention.register_fake

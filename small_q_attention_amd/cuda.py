@@ -2,7 +2,8 @@
 
 Mirrors ``/root/reference/src/small_q_attention/cuda.py`` (same names,
 parameter order, defaults and exception classes) over one gfx950 library,
-``libsqa.so``, reached through the ``sqa::paged_mtp_attention`` torch custom op.
+``libsqa.so``. Eager calls go straight to the library; under ``torch.compile`` /
+``torch.export`` the ``sqa::paged_mtp_attention`` torch custom op is used.
 All six ``forward_vN`` run the same HIP kernels (split-KV partial kernel with
 GQA and draft-row reuse, plus the log-sum-exp merge kernel); the version
 number only selects which of the reference's argument checks apply.
@@ -90,21 +91,41 @@ def load_v0(verbose: bool = False):
 load_v1 = load_v2 = load_v3 = load_v4 = load_v5 = load_v0
 
 
+_GPU_SEEN_BY = None  # the torch.cuda.is_available function that last reported a GPU
+
+
+def _gpu_present(torch) -> bool:
+    """``torch.cuda.is_available()``, remembered once true (it costs ~1 us per call)."""
+    global _GPU_SEEN_BY
+    probe = torch.cuda.is_available
+    if _GPU_SEEN_BY is probe:
+        return True
+    if probe():
+        _GPU_SEEN_BY = probe
+        return True
+    return False
+
+
 def _check_python_contract(tag, query, key_cache, value_cache, block_tables, seq_lens,
                            gqa4: bool):
     """The reference's Python-side checks (``cuda.py:65-77,85-95,138-150,197-211``)."""
     import torch
 
-    if not torch.cuda.is_available():
+    if not _gpu_present(torch):
         raise RuntimeError(f"a ROCm GPU is required for the {tag} kernel")
     tensors = (query, key_cache, value_cache, block_tables, seq_lens)
-    if any(not t.is_cuda for t in tensors):
-        raise ValueError(f"all {tag} inputs must be GPU tensors")
-    if any(t.device != query.device for t in tensors):
-        raise ValueError(f"all {tag} inputs must be on the same device")
-    if any(not t.is_contiguous() for t in tensors):
-        raise ValueError(f"all {tag} inputs must be contiguous")
-    if any(t.dtype != torch.float16 for t in (query, key_cache, value_cache)):
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError(f"all {tag} inputs must be GPU tensors")
+    device = query.device
+    for t in tensors:
+        if t.device != device:
+            raise ValueError(f"all {tag} inputs must be on the same device")
+    for t in tensors:
+        if not t.is_contiguous():
+            raise ValueError(f"all {tag} inputs must be contiguous")
+    half = torch.float16
+    if query.dtype != half or key_cache.dtype != half or value_cache.dtype != half:
         raise ValueError(f"{tag} requires FP16 Q/K/V")
     if query.ndim < 2 or query.shape[1] not in SUPPORTED_Q_LENS:
         raise ValueError(f"{tag} supports q_len 2, 4, 8 or 16")
@@ -172,8 +193,19 @@ def _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
     ck = 0 if chunk_keys is None else int(chunk_keys)
     num_splits, pps = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv,
                                        int(max_seq_len), block_tables.shape[1], ck)
-    return _lib.custom_op()(query, key_cache, value_cache, block_tables, seq_lens,
-                            num_splits, pps)
+    if _tracing():
+        # Under torch.compile / export the registered custom op is the traceable unit.
+        return _lib.custom_op()(query, key_cache, value_cache, block_tables, seq_lens,
+                                num_splits, pps)
+    # Eager: the same allocation and launch without the dispatcher round trip.
+    return _lib.run(query, key_cache, value_cache, block_tables, seq_lens, num_splits, pps)
+
+
+def _tracing() -> bool:
+    import torch
+
+    compiler = getattr(torch, "compiler", None)
+    return bool(compiler is not None and compiler.is_compiling())
 
 
 def paged_mtp_attention(query, key_cache, value_cache, block_tables, seq_lens,

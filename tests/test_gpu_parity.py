@@ -249,6 +249,26 @@ def test_graph_capture_and_replay():
         del junk
 
 
+def test_custom_op_matches_the_eager_path():
+    """Eager calls skip the dispatcher; the registered ``sqa::paged_mtp_attention`` op
+    (used under torch.compile/export) runs the same launch and gives the same bits,
+    and its fake implementation shapes the output without running anything."""
+    case = inputs.Case(batch=3, q_len=8, seq_lens=[900, 40, 2100], seed=19)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    ns, pps = _lib.plan_splits(0, 3, 8, 32, 8, 2100, tensors[3].shape[1], 0)
+    eager = sqa.paged_mtp_attention(*tensors, 16, 2100)
+    _lib.custom_op()  # registers the op
+    via_op = torch.ops.sqa.paged_mtp_attention(*tensors, ns, pps)
+    torch.cuda.synchronize()
+    assert torch.equal(eager, via_op)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode() as mode:
+        fakes = [mode.from_tensor(t) for t in tensors]
+        shaped = _lib.custom_op()(*fakes, ns, pps)
+    assert shaped.shape == eager.shape and shaped.dtype == eager.dtype
+
+
 def test_c_abi_direct_with_caller_workspace():
     """sqa_paged_mtp_attention through ctypes with a caller-owned workspace and events."""
     case = inputs.Case(batch=3, q_len=4, seq_lens=[500, 64, 1500], seed=17)
