@@ -70,8 +70,15 @@ struct MergeArgs {
 // head. A workgroup serves `heads` kv heads of one (sequence, split), one wave
 // per head holding all of its rows; all waves walk the same pages, so the
 // heads' slices of a page are read together (>= 4 heads keeps HBM accesses at
-// >= 1 KiB contiguous). `wg_per_cu` workgroups are resident per CU (register
-// file), which sets the split count of the automatic plan.
+// >= 1 KiB contiguous). `wg_per_cu` workgroups are resident per CU, which sets
+// the split count of the automatic plans.
+//
+// One workgroup per CU (one wave per SIMD): when two workgroups share a CU the
+// older one takes nearly all of the CU's memory issue and the other starts in
+// earnest only when it finishes, so equal work items end in two waves and the
+// second wave's spread of end times idles the chip. Alone on its CU a
+// workgroup keeps a deeper ring (D pages per wave) in the registers the second
+// one would have used.
 struct LaunchShape {
   int row_blocks;  // 16-row blocks per wave (1, 2 or 4)
   int heads;       // kv heads per workgroup (one wave each)
@@ -79,13 +86,8 @@ struct LaunchShape {
 };
 
 inline LaunchShape launch_shape(int rows) {
-  // Two 4-wave workgroups per CU (2 waves per SIMD) measured best up to 32
-  // rows: a third (possible at <= 16 rows, 165 VGPRs) adds page streams per
-  // CU and lowers bandwidth. 64 rows take the whole 512-entry register file
-  // (1 wave per SIMD), which beat splitting a head's rows over two waves that
-  // each read its pages.
-  if (rows <= 16) return {1, 4, 2};
-  if (rows <= 32) return {2, 4, 2};
+  if (rows <= 16) return {1, 4, 1};
+  if (rows <= 32) return {2, 4, 1};
   return {4, 4, 1};
 }
 

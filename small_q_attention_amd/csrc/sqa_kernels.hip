@@ -389,6 +389,7 @@ void sqa_partial_kernel(PartialArgs a) {
     }
     vis[nb] = real ? len - a.q_len + 1 + qi : 0;
   }
+  static_assert(2 * D + 1 <= kIdPad, "page-id table padding must cover the ring's look-ahead");
   constexpr int kIdSlots = (kMaxSplitPages + kIdPad + WW * 64 - 1) / (WW * 64);
   int idreg[kIdSlots];
   const int last_id = n_split > 0 ? n_split - 1 : 0;  // p_begin + last_id < max_pages
@@ -656,9 +657,9 @@ hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)(plan_slots(a.batch, a.num_splits, a.pages_per_split) * head_groups));
   const dim3 block(sh.heads * 64);
   if (sh.row_blocks == 1) {
-    hipLaunchKernelGGL((sqa_partial_kernel<1, 3, 4, 2>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((sqa_partial_kernel<1, 4, 4, 1>), grid, block, 0, stream, a);
   } else if (sh.row_blocks == 2) {
-    hipLaunchKernelGGL((sqa_partial_kernel<2, 3, 4, 2>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((sqa_partial_kernel<2, 4, 4, 1>), grid, block, 0, stream, a);
   } else {
     hipLaunchKernelGGL((sqa_partial_kernel<4, 3, 4, 1>), grid, block, 0, stream, a);
   }
