@@ -42,6 +42,11 @@ def build_command(output: Path = LIB_PATH):
         "-shared",
         # Packed fp32 VALU ops are kept out of the generated code.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA operands and results in VGPRs: the softmax reads every score and
+        # rescales every accumulator with VALU ops, and with the default AGPR
+        # form each of those costs a copy (q16: ~1500 copies per 3 pages,
+        # 375 -> 334 us at KV 32K x B16).
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         f"-I{INCLUDE}",
         f"-I{CSRC}",
         *[str(s) for s in SOURCES],
