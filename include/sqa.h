@@ -82,6 +82,81 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
                             int64_t num_pages, int page_size, int max_pages, int num_splits,
                             int pages_per_split, void* stream, void** timing_events);
 
+/*
+ * Where the K and V of a paged cache live, for sqa_paged_attention. Strides
+ * are in fp16 elements; the head dimension is contiguous. Element d of kv head
+ * h at slot t of page p is k[p * page_stride + t * token_stride + h *
+ * head_stride + d] (V alike from v). Strides must be multiples of 8 elements
+ * and k, v 16-byte aligned.
+ *   separate caches [P, 16, Hkv, 128] (the reference's): k = key_cache,
+ *     v = value_cache, page_stride 16*Hkv*128, token_stride Hkv*128, head_stride 128
+ *   interleaved NHD [P, 2, 16, Hkv, 128]: k = kv, v = kv + 16*Hkv*128,
+ *     page_stride 2*16*Hkv*128, token_stride Hkv*128, head_stride 128
+ *   interleaved HND [P, 2, Hkv, 16, 128]: k = kv, v = kv + 16*Hkv*128,
+ *     page_stride 2*16*Hkv*128, token_stride 128, head_stride 16*128
+ */
+typedef struct sqa_kv_cache {
+  const void* k;
+  const void* v;
+  int64_t num_pages;
+  int64_t page_stride;
+  int64_t token_stride;
+  int64_t head_stride;
+} sqa_kv_cache;
+
+/*
+ * Arguments of sqa_paged_attention (set struct_size = sizeof(sqa_attention_args)).
+ * query/output/block_tables/seq_lens/plan/workspace/stream/timing_events mean
+ * what they mean for sqa_paged_mtp_attention. Additions:
+ *   kv          any layout sqa_kv_cache describes.
+ *   draft_mask  NULL: the causal draft chain (row qi sees draft tokens j <= qi).
+ *               Otherwise [batch, q_len, mask_words] uint32, bit j of the row's
+ *               words (word j / 32, bit j % 32) = row qi sees draft token j,
+ *               i.e. token seq_lens[b] - q_len + j; tokens before the draft
+ *               block are always visible. This is the packed speculative-
+ *               decoding mask of the reference's FlashInfer comparisons
+ *               (scripts/run_flashinfer_baseline.py:56-85, viewed as uint32).
+ *               mask_words >= ceil(q_len / 32), at most 2.
+ *   scale       softmax scale (> 0; the reference uses head_dim^-1/2).
+ *   out_scale   multiplier of the normalised output (1 for plain attention).
+ */
+typedef struct sqa_attention_args {
+  size_t struct_size;
+  const void* query;
+  void* output;
+  sqa_kv_cache kv;
+  const int32_t* block_tables;
+  const int32_t* seq_lens;
+  int max_pages;
+  const uint32_t* draft_mask;
+  int mask_words;
+  float scale;
+  float out_scale;
+  int batch;
+  int q_len;
+  int num_query_heads;
+  int num_kv_heads;
+  int head_dim;
+  int page_size;
+  int num_splits;
+  int pages_per_split;
+  void* workspace;
+  size_t workspace_bytes;
+  void* stream;
+  void** timing_events;
+} sqa_attention_args;
+
+/*
+ * The general form of sqa_paged_mtp_attention: any cache layout of
+ * sqa_kv_cache, a caller-given draft mask and scales. No counterpart in the
+ * reference's own launchers; it serves the FlashInfer-shaped entry points its
+ * comparison scripts call (xqa_batch_decode_with_kv_cache,
+ * trtllm_batch_decode_with_kv_cache and the paged decode/prefill wrappers,
+ * scripts/run_flashinfer_baseline.py:99-204, scripts/compare_flashinfer_paths.py:95-160).
+ * Same plan, workspace, status codes and asynchrony as sqa_paged_mtp_attention.
+ */
+int sqa_paged_attention(const sqa_attention_args* args);
+
 /* Compute units of `device` (256 on MI355X), or -1 on error. */
 int sqa_device_cu_count(int device);
 

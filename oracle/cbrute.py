@@ -35,6 +35,11 @@ def _load():
         lib = ctypes.CDLL(str(_LIB_PATH))
         lib.sqa_oracle_f64.restype = ctypes.c_int
         lib.sqa_oracle_f64.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int] * 7 + [ctypes.c_longlong]
+        lib.sqa_oracle_f64_ex.restype = ctypes.c_int
+        lib.sqa_oracle_f64_ex.argtypes = (
+            [ctypes.c_void_p] * 3 + [ctypes.c_longlong] * 3 + [ctypes.c_void_p] * 3
+            + [ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_void_p]
+            + [ctypes.c_int] * 7 + [ctypes.c_longlong])
         lib.sqa_oracle_half_to_double.restype = ctypes.c_double
         lib.sqa_oracle_half_to_double.argtypes = [ctypes.c_uint16]
         _LIB = lib
@@ -58,22 +63,63 @@ def _as_np(x, dtype):
     return np.ascontiguousarray(np.asarray(x), dtype=dtype)
 
 
-def attention_c64(query, key_cache, value_cache, block_tables, seq_lens, page_size, num_kv_heads):
-    """fp16 inputs -> float64 ``[B, Q, Hq, D]`` output, computed in double."""
+def _strided_half(x):
+    """fp16 ``[P, page, Hkv, D]`` view (torch or numpy, any positive strides, contiguous D)
+    -> (numpy view, strides in elements)."""
+    if hasattr(x, "detach"):
+        x = x.detach()
+        if x.device.type != "cpu":
+            x = x.cpu()
+        x = x.numpy()
+    x = np.asarray(x)
+    if x.dtype != np.float16:
+        x = x.astype(np.float16)
+    if x.ndim != 4 or x.strides[3] != 2 or min(x.strides) <= 0:
+        x = np.ascontiguousarray(x)
+    return x, tuple(st // 2 for st in x.strides[:3])
+
+
+def attention_c64(query, key_cache, value_cache, block_tables, seq_lens, page_size, num_kv_heads,
+                  draft_mask=None, scale=None, out_scale=1.0):
+    """fp16 inputs -> float64 ``[B, Q, Hq, D]`` output, computed in double.
+
+    ``key_cache``/``value_cache``: ``[P, page, Hkv, D]`` with any positive strides (so the
+    halves of an interleaved cache are read in place). ``draft_mask``: ``None`` (causal
+    draft chain) or packed words ``[B, Q, W]`` (uint32/int32) or ``[B, Q, 2W]`` (uint16).
+    ``scale`` defaults to ``D**-0.5``; ``out_scale`` multiplies the output.
+    """
     lib = _load()
     q = _as_np(query, np.float16)
-    k = _as_np(key_cache, np.float16)
-    v = _as_np(value_cache, np.float16)
+    k, kst = _strided_half(key_cache)
+    v, vst = _strided_half(value_cache)
     bt = _as_np(block_tables, np.int32)
     sl = _as_np(seq_lens, np.int32)
     n_batch, q_len, n_qheads, dim = q.shape
     if k.shape[1:] != (page_size, num_kv_heads, dim) or v.shape != k.shape:
         raise ValueError("cache shape does not match page_size / num_kv_heads / head_dim")
+    if kst != vst:
+        v = np.ascontiguousarray(v)
+        k = np.ascontiguousarray(k)
+        kst = vst = tuple(st // 2 for st in k.strides[:3])
+    words, n_words = None, 0
+    if draft_mask is not None:
+        m = draft_mask
+        if hasattr(m, "detach"):
+            m = m.detach().cpu().numpy()
+        m = np.ascontiguousarray(np.asarray(m))
+        if m.dtype in (np.uint16, np.int16):
+            m = m.view(np.uint16)
+        words = np.ascontiguousarray(m.view(np.uint32))
+        n_words = words.shape[-1]
+        if words.shape[:2] != (n_batch, q_len) or n_words * 32 < q_len:
+            raise ValueError("draft_mask must be [B, Q, ceil(Q / 32)] words")
     out = np.empty(q.shape, dtype=np.float64)
     ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
-    rc = lib.sqa_oracle_f64(ptr(q), ptr(k), ptr(v), ptr(bt), ptr(sl), ptr(out),
-                            n_batch, q_len, n_qheads, num_kv_heads, dim, page_size,
-                            bt.shape[1], k.shape[0])
+    rc = lib.sqa_oracle_f64_ex(
+        ptr(q), ptr(k), ptr(v), kst[0], kst[1], kst[2], ptr(bt), ptr(sl),
+        ptr(words) if words is not None else None, n_words,
+        float(dim ** -0.5 if scale is None else scale), float(out_scale), ptr(out),
+        n_batch, q_len, n_qheads, num_kv_heads, dim, page_size, bt.shape[1], k.shape[0])
     if rc == -1:
         raise IndexError("block table holds a page id outside the cache")
     if rc == -2:

@@ -46,23 +46,29 @@ static void build_table(void) {
 double sqa_oracle_half_to_double(uint16_t bits) { return half_bits_to_double(bits); }
 
 /*
- * q:  [B, Q, Hq, D] fp16 bits;  kc, vc: [num_pages, page, Hkv, D] fp16 bits;
- * bt: [B, max_pages] int32;  sl: [B] int32;  out: [B, Q, Hq, D] double.
+ * q:  [B, Q, Hq, D] fp16 bits;  out: [B, Q, Hq, D] double;  bt: [B, max_pages]
+ * int32;  sl: [B] int32.  K/V element d of kv head h at slot t of page p is
+ * kc[p * ps + t * ts + h * hs + d] (V alike from vc; strides in elements).
+ * mask: NULL (row qi sees tokens t < sl - Q + qi + 1, the reference's causal
+ * draft chain, reference.py:63) or [B, Q, mask_words] uint32 words: row qi
+ * sees t < sl - Q, and draft token j = t - (sl - Q) (t < sl) when bit j % 32 of
+ * word j / 32 is set. Logits are scaled by `scale`, outputs by `out_scale`.
+ * Rows that see no token are 0.
  * Returns 0, or -1 if a page id read by the computation lies outside
  * [0, num_pages), or -2 if a sequence needs more than max_pages pages.
  */
-int sqa_oracle_f64(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
-                   const int32_t* bt, const int32_t* sl, double* out,
-                   int B, int Q, int Hq, int Hkv, int D, int page, int max_pages,
-                   long long num_pages) {
+int sqa_oracle_f64_ex(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                      long long ps, long long ts, long long hs,
+                      const int32_t* bt, const int32_t* sl, const uint32_t* mask, int mask_words,
+                      double scale, double out_scale, double* out,
+                      int B, int Q, int Hq, int Hkv, int D, int page, int max_pages,
+                      long long num_pages) {
   build_table();
   const int group = Hq / Hkv;
-  const double scale = 1.0 / sqrt((double)D);
   const long long rows = (long long)B * Q * Hq;
-  int status = 0;
 
   for (int b = 0; b < B; ++b) {
-    const long long len = sl[b];
+    const long long len = sl[b] > 0 ? sl[b] : 0;
     const long long pages_used = (len + page - 1) / page;
     if (pages_used > max_pages) return -2;
     for (long long p = 0; p < pages_used; ++p) {
@@ -74,6 +80,7 @@ int sqa_oracle_f64(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
 #pragma omp parallel
   {
     double* logits = NULL;
+    char* seen = NULL;
     long long cap = 0;
     double* qv = (double*)malloc(sizeof(double) * (size_t)D);
     double* acc = (double*)malloc(sizeof(double) * (size_t)D);
@@ -83,22 +90,39 @@ int sqa_oracle_f64(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
       const int qi = (int)((row / Hq) % Q);
       const int b = (int)(row / ((long long)Hq * Q));
       const int kvh = qh / group;
-      const long long visible = (long long)sl[b] - Q + qi + 1;
+      const long long len = sl[b] > 0 ? sl[b] : 0;
+      const long long draft_base = len - Q;
       double* o = out + row * D;
-      if (visible <= 0) {
+      if (len > cap) {
+        free(logits);
+        free(seen);
+        cap = len;
+        logits = (double*)malloc(sizeof(double) * (size_t)cap);
+        seen = (char*)malloc((size_t)cap);
+      }
+      long long n_seen = 0;
+      for (long long t = 0; t < len; ++t) {
+        int vis;
+        if (!mask) {
+          vis = t < draft_base + qi + 1;
+        } else {
+          const long long j = t - draft_base;
+          const uint32_t* words = mask + ((long long)b * Q + qi) * mask_words;
+          vis = j < 0 || ((words[j / 32] >> (j % 32)) & 1u);
+        }
+        seen[t] = (char)vis;
+        n_seen += vis;
+      }
+      if (n_seen == 0) {
         for (int d = 0; d < D; ++d) o[d] = 0.0;
         continue;
       }
-      if (visible > cap) {
-        free(logits);
-        cap = visible;
-        logits = (double*)malloc(sizeof(double) * (size_t)cap);
-      }
       for (int d = 0; d < D; ++d) qv[d] = g_half_table[q[row * D + d]];
       double peak = -INFINITY;
-      for (long long t = 0; t < visible; ++t) {
+      for (long long t = 0; t < len; ++t) {
+        if (!seen[t]) continue;
         const long long pid = bt[(long long)b * max_pages + t / page];
-        const uint16_t* kr = kc + ((pid * page + t % page) * Hkv + kvh) * (long long)D;
+        const uint16_t* kr = kc + pid * ps + (t % page) * ts + (long long)kvh * hs;
         double s = 0.0;
         for (int d = 0; d < D; ++d) s += qv[d] * g_half_table[kr[d]];
         s *= scale;
@@ -107,18 +131,32 @@ int sqa_oracle_f64(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
       }
       double denom = 0.0;
       for (int d = 0; d < D; ++d) acc[d] = 0.0;
-      for (long long t = 0; t < visible; ++t) {
+      for (long long t = 0; t < len; ++t) {
+        if (!seen[t]) continue;
         const double w = exp(logits[t] - peak);
         denom += w;
         const long long pid = bt[(long long)b * max_pages + t / page];
-        const uint16_t* vr = vc + ((pid * page + t % page) * Hkv + kvh) * (long long)D;
+        const uint16_t* vr = vc + pid * ps + (t % page) * ts + (long long)kvh * hs;
         for (int d = 0; d < D; ++d) acc[d] += w * g_half_table[vr[d]];
       }
-      for (int d = 0; d < D; ++d) o[d] = acc[d] / denom;
+      for (int d = 0; d < D; ++d) o[d] = out_scale * acc[d] / denom;
     }
     free(logits);
+    free(seen);
     free(qv);
     free(acc);
   }
-  return status;
+  return 0;
+}
+
+/* The reference's contract: separate [num_pages, page, Hkv, D] caches, causal
+ * draft chain, scale D^-1/2. */
+int sqa_oracle_f64(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                   const int32_t* bt, const int32_t* sl, double* out,
+                   int B, int Q, int Hq, int Hkv, int D, int page, int max_pages,
+                   long long num_pages) {
+  const long long ts = (long long)Hkv * D;
+  return sqa_oracle_f64_ex(q, kc, vc, (long long)page * ts, ts, D, bt, sl, NULL, 0,
+                           1.0 / sqrt((double)D), 1.0, out, B, Q, Hq, Hkv, D, page, max_pages,
+                           num_pages);
 }

@@ -39,8 +39,29 @@ def gather_sequence(key_cache, value_cache, block_row, length, page_size):
     return k, v
 
 
+def unpack_draft_mask(mask, q_len):
+    """Packed speculative-decoding mask -> bool ``[B, Q, Q]`` (row qi sees draft token j).
+
+    The packing is the one of the reference's FlashInfer comparisons
+    (``/root/reference/scripts/run_flashinfer_baseline.py:56-85``): per row,
+    ``ceil(Q / 32)`` little-endian uint32 words, bit ``j % 32`` of word ``j // 32``
+    for draft token j, stored as twice as many uint16 (or as the uint32 / int32
+    words themselves).
+    """
+    m = np.ascontiguousarray(_np(mask))
+    if m.dtype in (np.uint16, np.int16):
+        m = m.view(np.uint16).reshape(m.shape[:-1] + (m.shape[-1] // 2, 2))
+        words = m[..., 0].astype(np.uint64) | (m[..., 1].astype(np.uint64) << np.uint64(16))
+    else:
+        words = m.view(np.uint32).astype(np.uint64)
+    j = np.arange(q_len)
+    bits = (words[..., j // 32] >> (j % 32).astype(np.uint64)) & np.uint64(1)
+    return bits.astype(bool)
+
+
 def attention_numpy(query, key_cache, value_cache, block_tables, seq_lens, page_size,
-                    num_kv_heads, dtype=np.float64, batches=None):
+                    num_kv_heads, dtype=np.float64, batches=None, draft_mask=None, scale=None,
+                    out_scale=1.0):
     """Paged MTP attention; returns ``[B, Q, Hq, D]`` in ``dtype``.
 
     ``batches`` optionally restricts the computation to a subset of sequence
@@ -48,12 +69,23 @@ def attention_numpy(query, key_cache, value_cache, block_tables, seq_lens, page_
     a full-size batch. Rows whose visible-key count is <= 0 are returned as 0
     (the reference raises for them instead; callers that want the raise use
     :func:`oracle.paged_mtp_attention_reference`).
+
+    ``draft_mask`` (packed, see :func:`unpack_draft_mask`, or bool ``[B, Q, Q]``)
+    replaces the causal draft chain: token ``t`` of a sequence of length ``L`` is
+    seen by row qi when ``t < L - Q`` or when draft token ``j = t - (L - Q)`` is
+    marked for that row. ``scale`` (default ``D**-0.5``) scales the logits,
+    ``out_scale`` the output. Key and value caches may be any-stride
+    ``[P, page, Hkv, D]`` views (e.g. the halves of an interleaved cache).
     """
     q = _np(query).astype(dtype)
     bt, sl = _np(block_tables), _np(seq_lens)
     n_batch, q_len, n_qheads, dim = q.shape
     group = n_qheads // num_kv_heads
-    scale = dtype(dim ** -0.5)
+    scale = dtype(dim ** -0.5) if scale is None else dtype(scale)
+    if draft_mask is not None:
+        dm = _np(draft_mask)
+        if dm.dtype != bool:
+            dm = unpack_draft_mask(dm, q_len)
     out = np.full(q.shape, np.nan, dtype=dtype)
     for b in (range(n_batch) if batches is None else batches):
         length = int(sl[b])
@@ -67,16 +99,23 @@ def attention_numpy(query, key_cache, value_cache, block_tables, seq_lens, page_
         qg = q[b].reshape(q_len, num_kv_heads, group, dim).transpose(1, 0, 2, 3)
         qg = qg.reshape(num_kv_heads, q_len * group, dim)
         logits = np.matmul(qg, k.transpose(1, 2, 0)) * scale  # [Hkv, Q*G, L]
-        visible = length - q_len + np.arange(q_len) + 1  # [Q]
-        vis_rows = np.repeat(visible, group)  # [Q*G]
-        mask = np.arange(length)[None, :] < vis_rows[:, None]  # [Q*G, L]
+        if draft_mask is None:
+            visible = length - q_len + np.arange(q_len) + 1  # [Q]
+            vis_rows = np.repeat(visible, group)  # [Q*G]
+            mask = np.arange(length)[None, :] < vis_rows[:, None]  # [Q*G, L]
+        else:
+            t = np.arange(length)
+            j = t - (length - q_len)  # draft index, < 0 before the draft block
+            seen = np.where(j[None, :] < 0, True,
+                            dm[b][:, np.clip(j, 0, q_len - 1)])  # [Q, L]
+            mask = np.repeat(seen, group, axis=0)  # [Q*G, L]
         logits = np.where(mask[None], logits, -np.inf)
         peak = logits.max(axis=-1, keepdims=True)
         peak = np.where(np.isfinite(peak), peak, 0)
         w = np.exp(logits - peak)
         denom = w.sum(axis=-1, keepdims=True)
         o = np.matmul(w, v.transpose(1, 0, 2))  # [Hkv, Q*G, D]
-        o = np.where(denom > 0, o / np.where(denom > 0, denom, 1), 0)
+        o = np.where(denom > 0, o / np.where(denom > 0, denom, 1), 0) * dtype(out_scale)
         o = o.reshape(num_kv_heads, q_len, group, dim).transpose(1, 0, 2, 3)
         out[b] = o.reshape(q_len, n_qheads, dim)
     return out

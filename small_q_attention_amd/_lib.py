@@ -27,11 +27,34 @@ _SIGNATURES = [
     ("sqa_paged_mtp_attention", _C.c_int,
      [_C.c_void_p] * 7 + [_C.c_size_t] + [_C.c_int] * 5 + [_C.c_int64] + [_C.c_int] * 4
      + [_C.c_void_p, _C.c_void_p]),
+    ("sqa_paged_attention", _C.c_int, [_C.c_void_p]),
     ("sqa_device_cu_count", _C.c_int, [_C.c_int]),
     ("sqa_last_error", _C.c_char_p, []),
     ("sqa_version", _C.c_char_p, []),
 ]
 EXPORTED = [name for name, _, _ in _SIGNATURES]
+
+
+class KVCache(ctypes.Structure):
+    """``sqa_kv_cache`` of include/sqa.h (strides in fp16 elements)."""
+
+    _fields_ = [("k", _C.c_void_p), ("v", _C.c_void_p), ("num_pages", _C.c_int64),
+                ("page_stride", _C.c_int64), ("token_stride", _C.c_int64),
+                ("head_stride", _C.c_int64)]
+
+
+class AttentionArgs(ctypes.Structure):
+    """``sqa_attention_args`` of include/sqa.h."""
+
+    _fields_ = [("struct_size", _C.c_size_t), ("query", _C.c_void_p), ("output", _C.c_void_p),
+                ("kv", KVCache), ("block_tables", _C.c_void_p), ("seq_lens", _C.c_void_p),
+                ("max_pages", _C.c_int), ("draft_mask", _C.c_void_p), ("mask_words", _C.c_int),
+                ("scale", _C.c_float), ("out_scale", _C.c_float), ("batch", _C.c_int),
+                ("q_len", _C.c_int), ("num_query_heads", _C.c_int), ("num_kv_heads", _C.c_int),
+                ("head_dim", _C.c_int), ("page_size", _C.c_int), ("num_splits", _C.c_int),
+                ("pages_per_split", _C.c_int), ("workspace", _C.c_void_p),
+                ("workspace_bytes", _C.c_size_t), ("stream", _C.c_void_p),
+                ("timing_events", _C.c_void_p)]
 
 
 def library_path() -> Path:
@@ -116,6 +139,51 @@ def launch(query, key_cache, value_cache, block_tables, seq_lens, output, worksp
         num_splits, pages_per_split, stream_handle, ev)
     if rc != SQA_OK:
         raise RuntimeError(f"sqa_paged_mtp_attention failed: {last_error(lib)}")
+
+
+def kv_cache(k_view, v_view) -> KVCache:
+    """Describe a paged cache from two ``[num_pages, page, Hkv, D]`` views of any strides
+    (separate caches, or the K / V halves of an interleaved NHD or HND cache). The head
+    dimension must be contiguous and K and V must share strides."""
+    if k_view.dim() != 4 or v_view.shape != k_view.shape:
+        raise ValueError("K and V views must both be [num_pages, page, Hkv, D]")
+    if k_view.stride() != v_view.stride() or k_view.stride(3) != 1:
+        raise ValueError("K and V views must share strides with a contiguous head dimension")
+    return KVCache(k_view.data_ptr(), v_view.data_ptr(), k_view.shape[0], k_view.stride(0),
+                   k_view.stride(1), k_view.stride(2))
+
+
+def launch_general(query, output, k_view, v_view, block_tables, seq_lens, draft_mask,
+                   scale: float, out_scale: float, num_splits: int, pages_per_split: int,
+                   workspace, stream_handle: int, timing_events=None):
+    """Call ``sqa_paged_attention``. ``query``/``output``: contiguous ``[B, Q, Hq, D]``;
+    ``k_view``/``v_view``: see :func:`kv_cache`; ``draft_mask``: ``None`` (causal draft
+    chain) or a contiguous 32-bit ``[B, Q, W]`` tensor of packed draft bits."""
+    lib = _LIB if _LIB is not None else load()
+    b, q_len, hq, d = query.shape
+    a = AttentionArgs()
+    a.struct_size = ctypes.sizeof(AttentionArgs)
+    a.query, a.output = query.data_ptr(), output.data_ptr()
+    a.kv = kv_cache(k_view, v_view)
+    a.block_tables, a.seq_lens = block_tables.data_ptr(), seq_lens.data_ptr()
+    a.max_pages = block_tables.shape[1]
+    if draft_mask is not None:
+        a.draft_mask, a.mask_words = draft_mask.data_ptr(), draft_mask.shape[-1]
+    a.scale, a.out_scale = float(scale), float(out_scale)
+    a.batch, a.q_len, a.num_query_heads, a.num_kv_heads = b, q_len, hq, k_view.shape[2]
+    a.head_dim, a.page_size = d, k_view.shape[1]
+    a.num_splits, a.pages_per_split = num_splits, pages_per_split
+    if workspace is not None:
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
+    a.stream = stream_handle
+    ev = None
+    if timing_events is not None:
+        ev = (ctypes.c_void_p * 3)(*[ctypes.c_void_p(int(e)) for e in timing_events])
+        a.timing_events = ctypes.cast(ev, ctypes.c_void_p)
+    rc = lib.sqa_paged_attention(ctypes.byref(a))
+    if rc != SQA_OK:
+        raise RuntimeError(f"sqa_paged_attention failed: {last_error(lib)}")
 
 
 def run(query, key_cache, value_cache, block_tables, seq_lens, num_splits: int,

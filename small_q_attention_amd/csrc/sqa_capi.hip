@@ -127,13 +127,18 @@ size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv
   return bytes;
 }
 
-int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void* value_cache,
-                            const int32_t* block_tables, const int32_t* seq_lens, void* output,
-                            void* workspace, size_t workspace_bytes, int batch, int q_len,
-                            int num_query_heads, int num_kv_heads, int head_dim,
-                            int64_t num_pages, int page_size, int max_pages, int num_splits,
-                            int pages_per_split, void* stream, void** timing_events) {
-  if (!query || !key_cache || !value_cache || !block_tables || !seq_lens || !output)
+}  // extern "C"
+
+namespace {
+
+// Validates a call and launches the kernels. Shared by both entry points.
+int run_attention(const sqa_attention_args& a) {
+  const int batch = a.batch, q_len = a.q_len, num_query_heads = a.num_query_heads;
+  const int num_kv_heads = a.num_kv_heads, head_dim = a.head_dim, page_size = a.page_size;
+  const int max_pages = a.max_pages, num_splits = a.num_splits;
+  const int pages_per_split = a.pages_per_split;
+  const int64_t num_pages = a.kv.num_pages;
+  if (!a.query || !a.kv.k || !a.kv.v || !a.block_tables || !a.seq_lens || !a.output)
     return fail(SQA_ERR_INVALID, "null tensor pointer");
   if (batch <= 0 || q_len <= 0 || num_query_heads <= 0 || num_kv_heads <= 0)
     return fail(SQA_ERR_INVALID, "batch, q_len and head counts must be positive");
@@ -149,6 +154,22 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
   const long long rows = (long long)q_len * group;
   if (rows > sqa::kMaxRows)
     return fail(SQA_ERR_UNSUPPORTED, "q_len * group = %lld exceeds %d", rows, sqa::kMaxRows);
+  // Cache layout: 16-byte aligned bases and strides (the kernel's 16-byte loads),
+  // and one page's K (or V) within 2 GiB of its base (32-bit buffer offsets).
+  const int64_t ps = a.kv.page_stride, ts = a.kv.token_stride, hs = a.kv.head_stride;
+  if (ps < 0 || ts < 0 || hs < 0 || ps % 8 || ts % 8 || hs % 8)
+    return fail(SQA_ERR_INVALID, "cache strides must be non-negative multiples of 8 elements");
+  if (((uintptr_t)a.kv.k | (uintptr_t)a.kv.v) % 16)
+    return fail(SQA_ERR_INVALID, "cache base pointers must be 16-byte aligned");
+  const long long extent =
+      2LL * (((long long)(sqa::kPageSize - 1) * ts) + (long long)(num_kv_heads - 1) * hs + sqa::kHeadDim);
+  if (extent > 0x7fffffffLL)
+    return fail(SQA_ERR_INVALID, "one page of the cache spans more than 2 GiB");
+  if (a.draft_mask && (a.mask_words < (q_len + 31) / 32 || a.mask_words > 2))
+    return fail(SQA_ERR_INVALID, "draft_mask needs %d..2 words per row, got %d", (q_len + 31) / 32,
+                a.mask_words);
+  if (!(a.scale > 0.f) || !isfinite(a.scale) || !isfinite(a.out_scale))
+    return fail(SQA_ERR_INVALID, "scale must be positive and finite, out_scale finite");
   if (num_splits <= 0 || pages_per_split < 0)
     return fail(SQA_ERR_INVALID, "num_splits must be positive and pages_per_split non-negative");
   if (pages_per_split > sqa::kMaxSplitPages)
@@ -174,20 +195,23 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
     return fail(SQA_ERR_INVALID, "grid too large");
   const size_t need = sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, num_splits,
                                           pages_per_split);
-  if (need > 0 && (!workspace || workspace_bytes < need))
+  if (need > 0 && (!a.workspace || a.workspace_bytes < need))
     return fail(SQA_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
-                workspace ? workspace_bytes : (size_t)0);
+                a.workspace ? a.workspace_bytes : (size_t)0);
 
-  hipStream_t s = (hipStream_t)stream;
-  hipEvent_t* ev = (hipEvent_t*)timing_events;
+  hipStream_t s = (hipStream_t)a.stream;
+  hipEvent_t* ev = (hipEvent_t*)a.timing_events;
+  void* workspace = a.workspace;
 
   sqa::PartialArgs pa;
-  pa.q = (const _Float16*)query;
-  pa.k = (const _Float16*)key_cache;
-  pa.v = (const _Float16*)value_cache;
-  pa.block_tables = block_tables;
-  pa.seq_lens = seq_lens;
-  pa.out = (_Float16*)output;
+  pa.q = (const _Float16*)a.query;
+  pa.k = (const _Float16*)a.kv.k;
+  pa.v = (const _Float16*)a.kv.v;
+  pa.block_tables = a.block_tables;
+  pa.seq_lens = a.seq_lens;
+  pa.draft_mask = a.draft_mask;
+  pa.mask_words = a.draft_mask ? a.mask_words : 0;
+  pa.out = (_Float16*)a.output;
   const size_t items =
       (size_t)sqa::plan_slots(batch, num_splits, pages_per_split) * num_kv_heads * rows;
   const bool merged = balanced || num_splits > 1;
@@ -195,6 +219,10 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
   pa.part_ml = merged ? (float*)workspace + items * sqa::kHeadDim : nullptr;
   pa.seq_splits = balanced ? (sqa::SeqSplits*)(pa.part_ml + items * 2) : nullptr;
   pa.num_pages = num_pages;
+  pa.page_stride = 2LL * ps;
+  pa.token_stride = (unsigned)(2 * ts);
+  pa.head_stride = (unsigned)(2 * hs);
+  pa.page_extent = (unsigned)extent;
   pa.batch = batch;
   pa.q_len = q_len;
   pa.hq = num_query_heads;
@@ -204,7 +232,8 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
   pa.max_pages = max_pages;
   pa.pages_per_split = pages_per_split;
   pa.num_splits = num_splits;
-  pa.scale_log2 = (float)(1.4426950408889634 / sqrt((double)head_dim));
+  pa.scale_log2 = (float)(1.4426950408889634 * (double)a.scale);
+  pa.out_scale = a.out_scale;
 
   hipError_t e;
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
@@ -215,7 +244,7 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
     ma.part_o = pa.part_o;
     ma.part_ml = pa.part_ml;
     ma.seq_splits = pa.seq_splits;
-    ma.seq_lens = seq_lens;
+    ma.seq_lens = a.seq_lens;
     ma.out = pa.out;
     ma.batch = batch;
     ma.q_len = q_len;
@@ -226,10 +255,62 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
     ma.max_pages = max_pages;
     ma.pages_per_split = pages_per_split;
     ma.num_splits = num_splits;
+    ma.out_scale = a.out_scale;
     if ((e = sqa::launch_merge(ma, s)) != hipSuccess) return hip_fail(e, "merge kernel launch");
   }
   if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
   return SQA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sqa_paged_attention(const sqa_attention_args* args) {
+  if (!args) return fail(SQA_ERR_INVALID, "null argument struct");
+  if (args->struct_size != sizeof(sqa_attention_args))
+    return fail(SQA_ERR_INVALID, "struct_size %zu does not match this library's %zu",
+                args->struct_size, sizeof(sqa_attention_args));
+  return run_attention(*args);
+}
+
+int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void* value_cache,
+                            const int32_t* block_tables, const int32_t* seq_lens, void* output,
+                            void* workspace, size_t workspace_bytes, int batch, int q_len,
+                            int num_query_heads, int num_kv_heads, int head_dim,
+                            int64_t num_pages, int page_size, int max_pages, int num_splits,
+                            int pages_per_split, void* stream, void** timing_events) {
+  // The reference's separate [num_pages, 16, Hkv, head_dim] caches, causal
+  // draft chain, scale head_dim^-1/2.
+  sqa_attention_args a;
+  memset(&a, 0, sizeof(a));
+  a.struct_size = sizeof(a);
+  a.query = query;
+  a.output = output;
+  a.kv.k = key_cache;
+  a.kv.v = value_cache;
+  a.kv.num_pages = num_pages;
+  a.kv.token_stride = (int64_t)num_kv_heads * head_dim;
+  a.kv.page_stride = (int64_t)page_size * a.kv.token_stride;
+  a.kv.head_stride = head_dim;
+  a.block_tables = block_tables;
+  a.seq_lens = seq_lens;
+  a.max_pages = max_pages;
+  a.scale = head_dim > 0 ? (float)(1.0 / sqrt((double)head_dim)) : 1.f;
+  a.out_scale = 1.f;
+  a.batch = batch;
+  a.q_len = q_len;
+  a.num_query_heads = num_query_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.head_dim = head_dim;
+  a.page_size = page_size;
+  a.num_splits = num_splits;
+  a.pages_per_split = pages_per_split;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  a.stream = stream;
+  a.timing_events = timing_events;
+  return run_attention(a);
 }
 
 }  // extern "C"

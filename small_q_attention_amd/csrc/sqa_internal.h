@@ -34,19 +34,26 @@ struct SeqSplits {
 // pages fit one split are written straight to the output.
 struct PartialArgs {
   const _Float16* q;          // [B, Q, Hq, 128]
-  const _Float16* k;          // [num_pages, 16, Hkv, 128]
-  const _Float16* v;          // [num_pages, 16, Hkv, 128]
+  const _Float16* k;          // K of page 0, slot 0, kv head 0
+  const _Float16* v;          // V of page 0, slot 0, kv head 0
   const int32_t* block_tables;  // [B, max_pages]
   const int32_t* seq_lens;      // [B]
+  const uint32_t* draft_mask;   // NULL (causal draft chain) or [B, Q, mask_words]
   _Float16* out;              // [B, Q, Hq, 128]; written directly when num_splits == 1
   float* part_o;              // [slots, Hkv, rows, 128] unnormalised sums
   float* part_ml;             // [slots, Hkv, rows, 2] (max in log2 units, sum)
   SeqSplits* seq_splits;      // [B] (balanced plan only)
   long long num_pages;        // pages in the cache pool; ids outside are clamped to 0
+  long long page_stride;      // bytes between consecutive pages (K and V alike)
+  unsigned token_stride;      // bytes between consecutive slots of a page
+  unsigned head_stride;       // bytes between consecutive kv heads
+  unsigned page_extent;       // bytes from a page's base that its K (or V) spans
+  int mask_words;             // 32-bit words per draft-mask row (1 or 2)
   int batch, q_len, hq, hkv, group, rows;
   int max_pages;              // block_tables row length
   int pages_per_split, num_splits;
-  float scale_log2;           // head_dim^-1/2 * log2(e)
+  float scale_log2;           // softmax scale * log2(e)
+  float out_scale;            // multiplier applied to the normalised output
 };
 
 __host__ __device__ inline bool is_balanced(int pages_per_split) { return pages_per_split == 0; }
@@ -64,6 +71,7 @@ struct MergeArgs {
   _Float16* out;
   int batch, q_len, hq, hkv, group, rows;
   int max_pages, pages_per_split, num_splits;
+  float out_scale;
 };
 
 // Launch shape of the partial kernel for a given number of query rows per kv

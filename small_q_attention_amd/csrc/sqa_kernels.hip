@@ -102,12 +102,16 @@ __device__ __forceinline__ unsigned pack_hi(unsigned a, unsigned b) {
 }
 
 // One 16-token page for one wave. sm_q: Q fragments in LDS, [nb][kk][lane]
-// (the B-operand layout). c = head_dim^-1/2 * log2(e); scores stay raw until
+// (the B-operand layout). c = softmax scale * log2(e); scores stay raw until
 // the exponent, where the scale and the running max meet in one FMA.
+// Visibility on masked pages: token t < len is seen by a row when it lies
+// before the draft block (t < draft_base = len - q_len) or when bit
+// t - draft_base of the row's draft bits is set.
 template <int NB>
 __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, const h8* sm_q,
-                                             int lane, const int (&vis)[NB], int tok0, int len,
-                                             bool masked, float c) {
+                                             int lane, const unsigned long long (&dbits)[NB],
+                                             int draft_base, int tok0, int len, bool masked,
+                                             float c) {
   // Raw scores S^T[token][row] = K . Q^T for this page.
   f4 s[NB];
 #pragma unroll
@@ -126,7 +130,13 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, co
     for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        if (tok0 + e >= vis[nb]) s[nb][e] = -INFINITY;
+        // Bitwise, not short-circuit, logic: one select per score, no
+        // lane-divergent control flow around the scores.
+        const int t = tok0 + e;
+        const int j = t - draft_base;  // < q_len <= 64 whenever t < len
+        const unsigned bit = (unsigned)(dbits[nb] >> (j & 63)) & 1u;
+        const unsigned seen = (unsigned)(t < len) & ((unsigned)(j < 0) | bit);
+        s[nb][e] = seen ? s[nb][e] : -INFINITY;
       }
     }
     // V rows past the sequence end may hold anything (even NaN); 0 * NaN would
@@ -370,7 +380,7 @@ void sqa_partial_kernel(PartialArgs a) {
   // pages, all in flight at once (Q and ids first, so waiting for them leaves
   // the page loads outstanding).
   h8 qreg[NB][4];
-  int vis[NB];
+  unsigned long long dbits[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     // Loads are unconditional from an in-bounds address (padding rows and idle
@@ -387,7 +397,18 @@ void sqa_partial_kernel(PartialArgs a) {
       const h8 x = *(const h8*)(qp + 32 * kk);
       qreg[nb][kk] = real ? x : h8{0, 0, 0, 0, 0, 0, 0, 0};
     }
-    vis[nb] = real ? len - a.q_len + 1 + qi : 0;
+    // Draft bits of the row: bit j = sees draft token j (the caller's mask, or
+    // the causal chain j <= qi).
+    unsigned long long bits;
+    if (a.draft_mask != nullptr) {
+      const uint32_t* mp = a.draft_mask + (size_t)(b * a.q_len + qi) * a.mask_words;
+      const unsigned long long lo = mp[0];
+      const unsigned long long hi = a.mask_words > 1 ? mp[1] : 0u;
+      bits = lo | (hi << 32);
+    } else {
+      bits = qi >= 63 ? ~0ull : (2ull << qi) - 1ull;
+    }
+    dbits[nb] = real ? bits : 0ull;
   }
   static_assert(2 * D + 1 <= kIdPad, "page-id table padding must cover the ring's look-ahead");
   constexpr int kIdSlots = (kMaxSplitPages + kIdPad + WW * 64 - 1) / (WW * 64);
@@ -404,17 +425,16 @@ void sqa_partial_kernel(PartialArgs a) {
   // page at the page's base address and bounded to the page, and the lane
   // offsets below stay in one VGPR each for the whole loop.
   const int kvh_c = active ? kvh : 0;
-  const unsigned tok_bytes = (unsigned)a.hkv * kHeadDim * 2;   // bytes between tokens
-  const unsigned page_bytes = kPageSize * tok_bytes;           // bytes between pages
-  const unsigned k_lane = l16 * tok_bytes + kvh_c * kHeadDim * 2 + 16 * g16;
-  const unsigned v_lane = 4 * g16 * tok_bytes + kvh_c * kHeadDim * 2 + 16 * l16;
+  const unsigned tok_bytes = a.token_stride;
+  const unsigned k_lane = l16 * tok_bytes + kvh_c * a.head_stride + 16 * g16;
+  const unsigned v_lane = 4 * g16 * tok_bytes + kvh_c * a.head_stride + 16 * l16;
   // pid < 0 gives a zero-length resource: the loads return zeros without
   // touching memory, so every slot refill below is unconditional and the
   // compiler's wait counts stay exact (one page retires per step). K/V are
   // streamed once, so the loads are non-temporal.
   auto load_page = [&](int pid, PageRegs& pg) {
-    const size_t off = pid >= 0 ? (size_t)pid * page_bytes : 0;
-    const int nrec = pid >= 0 ? (int)page_bytes : 0;
+    const size_t off = pid >= 0 ? (size_t)pid * (size_t)a.page_stride : 0;
+    const int nrec = pid >= 0 ? (int)a.page_extent : 0;
     const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)((const char*)a.k + off), (short)0, nrec, kBufferFlags);
     const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
@@ -453,8 +473,8 @@ void sqa_partial_kernel(PartialArgs a) {
     sm_ids[i] = idreg[k] >= 0 ? clamp_page(idreg[k], a.num_pages) : -1;
   }
   auto page_id = [&](int i) -> int { return active ? sm_ids[i] : -1; };
-  // Pages whose last token index >= mask_from need the causal/tail mask.
-  const int mask_from = len - a.q_len + 1;
+  // Pages holding a token >= mask_from (draft block or past the end) are masked.
+  const int mask_from = len - a.q_len;
 
   WaveState<NB> st;
 #pragma unroll
@@ -475,8 +495,8 @@ void sqa_partial_kernel(PartialArgs a) {
       if (ii < n_pages) {
         const int p = p_begin + ii;
         const bool masked = (p + 1) * kPageSize > mask_from;
-        process_page<NB>(st, ring[j], my_q, lane, vis, p * kPageSize + 4 * g16, len, masked,
-                         a.scale_log2);
+        process_page<NB>(st, ring[j], my_q, lane, dbits, mask_from, p * kPageSize + 4 * g16, len,
+                         masked, a.scale_log2);
       }
       const int pid = next_pid;
       next_pid = page_id(ii + D + 1);
@@ -498,7 +518,7 @@ void sqa_partial_kernel(PartialArgs a) {
     const int qi = r / a.group;
     const int gg = r - qi * a.group;
     if (direct) {
-      const float inv = st.l[nb] > 0.f ? 1.0f / st.l[nb] : 0.f;
+      const float inv = st.l[nb] > 0.f ? a.out_scale / st.l[nb] : 0.f;
       _Float16* op =
           a.out + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * kHeadDim + 32 * g16;
 #pragma unroll
@@ -641,7 +661,7 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
     }
   }
   if (skip) return;
-  const float inv = den > 0.f ? 1.0f / den : 0.f;
+  const float inv = den > 0.f ? a.out_scale / den : 0.f;
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   h2 o;
   o[0] = (_Float16)(acc0 * inv);

@@ -1,0 +1,311 @@
+"""FlashInfer-shaped entry points over the gfx950 kernels.
+
+The reference compares its kernels with four FlashInfer paths for the same op
+(``/root/reference/scripts/run_flashinfer_baseline.py:99-204``,
+``scripts/compare_flashinfer_paths.py:95-160``,
+``scripts/probe_decode_wrapper_mtp.py``). This module offers the same call shapes,
+so code written against them runs here unchanged, within the contract of this
+build (fp16 Q/K/V, head_dim 128, 16-token pages, ``q_len * Hq / Hkv <= 64``):
+
+* :func:`xqa_batch_decode_with_kv_cache` — block table + seq_lens, interleaved
+  ``[P, 2, 16, Hkv, D]`` ("NHD") or ``[P, 2, Hkv, 16, D]`` ("HND") cache or a
+  ``(k_cache, v_cache)`` pair, packed draft mask, ``bmm1_scale`` (softmax scale)
+  and ``bmm2_scale`` (output scale).
+* :func:`trtllm_batch_decode_with_kv_cache` — the same with "HND" by default.
+* :class:`BatchDecodeWithPagedKVCacheWrapper` / :class:`BatchPrefillWithPagedKVCacheWrapper`
+  — ``plan()`` over CSR page lists (``indptr``, ``indices``, ``last_page_len``)
+  once, ``run()`` per layer.
+
+Queries are ``[B * Q, Hq, D]`` (request-major, as FlashInfer takes them) and
+every request has the same ``Q`` (``q_len_per_req``, or a uniform ``qo_indptr``).
+The caller's workspace buffer holds the split-KV partials, so a run allocates
+only its output (none when ``out`` is given) and is graph-capturable after
+``plan()``. Arguments outside the contract raise ``ValueError`` (positional
+encodings, soft caps, sliding windows, sinks, custom prefill masks); behaviour
+is pinned against this build's oracle, not against FlashInfer itself.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+from . import _lib
+from .masks import as_words
+
+PAGE_SIZE = 16
+HEAD_DIM = 128
+
+
+def _kv_views(kv_cache, kv_layout: str):
+    """``(k_view, v_view)``: ``[P, 16, Hkv, D]`` views of the caller's cache, no copy."""
+    if isinstance(kv_cache, (tuple, list)):
+        if len(kv_cache) != 2:
+            raise ValueError("a split cache is a (k_cache, v_cache) pair")
+        k, v = kv_cache
+        if kv_layout == "HND":
+            k, v = k.transpose(1, 2), v.transpose(1, 2)
+        return k, v
+    if kv_cache.dim() != 5 or kv_cache.shape[1] != 2:
+        raise ValueError("kv_cache must be [P, 2, 16, Hkv, D] (NHD) or [P, 2, Hkv, 16, D] (HND)")
+    k, v = kv_cache[:, 0], kv_cache[:, 1]
+    if kv_layout == "NHD":
+        return k, v
+    if kv_layout == "HND":
+        return k.transpose(1, 2), v.transpose(1, 2)
+    raise ValueError(f"kv_layout must be 'NHD' or 'HND', got {kv_layout!r}")
+
+
+def _check_tensors(query, k, v, num_qo_heads: Optional[int] = None):
+    import torch
+
+    if not query.is_cuda or not k.is_cuda:
+        raise ValueError("query and kv_cache must be GPU tensors")
+    if query.dtype != torch.float16 or k.dtype != torch.float16:
+        raise ValueError("this build supports fp16 query and KV")
+    if query.dim() != 3 or not query.is_contiguous():
+        raise ValueError("query must be a contiguous [B * Q, Hq, D] tensor")
+    if query.shape[-1] != HEAD_DIM or k.shape[-1] != HEAD_DIM:
+        raise ValueError("this build supports head_dim 128")
+    if k.shape[1] != PAGE_SIZE:
+        raise ValueError("this build supports page_size 16")
+    if num_qo_heads is not None and query.shape[1] != num_qo_heads:
+        raise ValueError(f"query has {query.shape[1]} heads, plan() was given {num_qo_heads}")
+
+
+def _run(query, k, v, block_tables, seq_lens, max_seq_len: int, q_len: int, scale: float,
+         out_scale: float, mask, workspace_buffer, out, plan=None):
+    """Shared launch: ``query`` ``[B * Q, Hq, D]`` -> ``out`` of the same shape."""
+    import torch
+
+    batch = block_tables.shape[0]
+    if q_len < 1 or query.shape[0] != batch * q_len:
+        raise ValueError(f"query holds {query.shape[0]} rows, expected batch {batch} x "
+                         f"q_len_per_req {q_len}")
+    hq, hkv = query.shape[1], k.shape[2]
+    if hkv == 0 or hq % hkv:
+        raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
+    if q_len * (hq // hkv) > 64:
+        raise ValueError("q_len_per_req * (Hq / Hkv) must be at most 64")
+    if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise ValueError("block_tables and seq_lens must be int32")
+    words = None if mask is None else as_words(mask, batch, q_len)
+    q4 = query.view(batch, q_len, hq, HEAD_DIM)
+    if out is None:
+        out = torch.empty_like(query)
+    elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped and typed like query")
+    if plan is None:
+        plan = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv,
+                                int(max_seq_len), block_tables.shape[1], 0)
+    ns, pps = plan
+    need = _lib.workspace_bytes(batch, q_len, hq, hkv, ns, pps)
+    ws = None
+    if need:
+        if workspace_buffer is None:
+            ws = torch.empty(need, dtype=torch.uint8, device=query.device)
+        else:
+            have = workspace_buffer.numel() * workspace_buffer.element_size()
+            if have < need or not workspace_buffer.is_contiguous():
+                raise ValueError(f"workspace_buffer must be contiguous and hold at least {need} "
+                                 f"bytes for this batch (has {have})")
+            ws = workspace_buffer
+    _lib.launch_general(q4, out.view(batch, q_len, hq, HEAD_DIM), k, v, block_tables, seq_lens,
+                        words, scale, out_scale, ns, pps, ws,
+                        _lib.raw_stream(query.device.index))
+    return out
+
+
+def _scalar(x, name):
+    if hasattr(x, "item"):
+        if x.numel() != 1:
+            raise ValueError(f"{name} must be a scalar")
+        x = x.item()
+    return float(x)
+
+
+def xqa_batch_decode_with_kv_cache(query, kv_cache, workspace_buffer, block_tables, seq_lens,
+                                   max_seq_len, bmm1_scale, bmm2_scale, window_left=-1,
+                                   out=None, sinks=None, kv_layout="NHD", enable_pdl=None,
+                                   q_len_per_req=1, mask=None):
+    """Paged decode of ``q_len_per_req`` draft tokens per request.
+
+    Call shape of ``flashinfer.decode.xqa_batch_decode_with_kv_cache`` as the
+    reference uses it (``run_flashinfer_baseline.py:153-177``). ``bmm1_scale`` is
+    the softmax scale, ``bmm2_scale`` multiplies the output; ``mask`` is the packed
+    draft mask (``None``: causal draft chain). ``max_seq_len`` bounds every
+    ``seq_lens[b]``. Returns ``out`` (``[B * Q, Hq, D]``).
+    """
+    if window_left not in (-1, None):
+        raise ValueError("sliding windows are not supported (window_left must be -1)")
+    if sinks is not None:
+        raise ValueError("attention sinks are not supported")
+    k, v = _kv_views(kv_cache, kv_layout)
+    _check_tensors(query, k, v)
+    return _run(query, k, v, block_tables, seq_lens, int(max_seq_len), int(q_len_per_req),
+                _scalar(bmm1_scale, "bmm1_scale"), _scalar(bmm2_scale, "bmm2_scale"), mask,
+                workspace_buffer, out)
+
+
+def trtllm_batch_decode_with_kv_cache(query, kv_cache, workspace_buffer, block_tables, seq_lens,
+                                      max_seq_len, bmm1_scale, bmm2_scale, window_left=-1,
+                                      out=None, sinks=None, kv_layout="HND", enable_pdl=None,
+                                      q_len_per_req=1, mask=None):
+    """Call shape of ``flashinfer.decode.trtllm_batch_decode_with_kv_cache``
+    (``run_flashinfer_baseline.py:180-204``): as :func:`xqa_batch_decode_with_kv_cache`
+    with the "HND" cache layout by default."""
+    return xqa_batch_decode_with_kv_cache(query, kv_cache, workspace_buffer, block_tables,
+                                          seq_lens, max_seq_len, bmm1_scale, bmm2_scale,
+                                          window_left, out=out, sinks=sinks, kv_layout=kv_layout,
+                                          enable_pdl=enable_pdl, q_len_per_req=q_len_per_req,
+                                          mask=mask)
+
+
+def csr_to_block_table(indptr, indices, last_page_len, page_size: int = PAGE_SIZE):
+    """CSR page lists -> ``(block_tables [B, max_pages] int32, seq_lens [B] int32)`` on the
+    same device: row b lists ``indices[indptr[b]:indptr[b + 1]]`` (padded with page 0)
+    and holds ``(n_b - 1) * page_size + last_page_len[b]`` tokens (0 when ``n_b == 0``).
+    One host read of the longest list (plan time)."""
+    import torch
+
+    indptr = indptr.to(torch.int64)
+    counts = indptr[1:] - indptr[:-1]
+    if counts.numel() == 0:
+        raise ValueError("indptr must hold batch + 1 entries")
+    if bool((counts < 0).any()):
+        raise ValueError("indptr must be non-decreasing")
+    max_pages = max(1, int(counts.max()))
+    j = torch.arange(max_pages, device=indptr.device)
+    valid = j[None, :] < counts[:, None]
+    pos = (indptr[:-1, None] + j[None, :]).clamp(max=max(indices.numel() - 1, 0))
+    if indices.numel() == 0:
+        block_tables = torch.zeros(counts.numel(), max_pages, dtype=torch.int32,
+                                   device=indptr.device)
+    else:
+        block_tables = torch.where(valid, indices.to(torch.int64)[pos], 0).to(torch.int32)
+    last = last_page_len.to(torch.int64)
+    if bool(((counts > 0) & ((last < 1) | (last > page_size))).any()):
+        raise ValueError(f"last_page_len must be in [1, {page_size}] for non-empty requests")
+    seq_lens = torch.where(counts > 0, (counts - 1) * page_size + last, 0).to(torch.int32)
+    return block_tables.contiguous(), seq_lens.contiguous()
+
+
+class _PagedWrapper:
+    """Plan once (CSR -> block table, split plan, workspace check), run per layer."""
+
+    def __init__(self, float_workspace_buffer, kv_layout="NHD", use_cuda_graph=False,
+                 use_tensor_cores=False, **_unused):
+        if kv_layout not in ("NHD", "HND"):
+            raise ValueError(f"kv_layout must be 'NHD' or 'HND', got {kv_layout!r}")
+        self._workspace = float_workspace_buffer
+        self._kv_layout = kv_layout
+        self._planned = None
+
+    def reset_workspace_buffer(self, float_workspace_buffer, *_unused):
+        self._workspace = float_workspace_buffer
+
+    def _plan(self, indptr, indices, last_page_len, num_qo_heads, num_kv_heads, head_dim,
+              page_size, q_len, mask_words, sm_scale, pos_encoding_mode, window_left,
+              logits_soft_cap, q_data_type, kv_data_type):
+        import torch
+
+        if pos_encoding_mode not in ("NONE", None):
+            raise ValueError("only pos_encoding_mode='NONE' is supported")
+        if window_left not in (-1, None):
+            raise ValueError("sliding windows are not supported (window_left must be -1)")
+        if logits_soft_cap not in (None, 0, 0.0):
+            raise ValueError("logits soft capping is not supported")
+        for dt in (q_data_type, kv_data_type):
+            if dt not in (None, torch.float16, "float16", "fp16"):
+                raise ValueError("this build supports fp16 query and KV")
+        if head_dim != HEAD_DIM or page_size != PAGE_SIZE:
+            raise ValueError("this build supports head_dim 128 and page_size 16")
+        if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
+            raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
+        block_tables, seq_lens = csr_to_block_table(indptr, indices, last_page_len, page_size)
+        batch = block_tables.shape[0]
+        max_seq_len = int(seq_lens.max()) if batch else 0
+        plan = _lib.plan_splits(block_tables.device.index or 0, batch, q_len, num_qo_heads,
+                                num_kv_heads, max(max_seq_len, 1), block_tables.shape[1], 0)
+        need = _lib.workspace_bytes(batch, q_len, num_qo_heads, num_kv_heads, *plan)
+        if need and self._workspace is not None:
+            have = self._workspace.numel() * self._workspace.element_size()
+            if have < need:
+                raise ValueError(f"float_workspace_buffer holds {have} bytes, this plan needs "
+                                 f"{need}")
+        self._planned = dict(block_tables=block_tables, seq_lens=seq_lens, plan=plan,
+                             q_len=q_len, hq=num_qo_heads, hkv=num_kv_heads,
+                             max_seq_len=max_seq_len, mask_words=mask_words,
+                             scale=HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale))
+
+    def run(self, q, paged_kv_cache, *_unused, out=None, **_kw):
+        if self._planned is None:
+            raise RuntimeError("plan() must be called before run()")
+        p = self._planned
+        k, v = _kv_views(paged_kv_cache, self._kv_layout)
+        _check_tensors(q, k, v, p["hq"])
+        if k.shape[2] != p["hkv"]:
+            raise ValueError(f"kv_cache has {k.shape[2]} kv heads, plan() was given {p['hkv']}")
+        return _run(q, k, v, p["block_tables"], p["seq_lens"], p["max_seq_len"], p["q_len"],
+                    p["scale"], 1.0, p["mask_words"], self._workspace, out, plan=p["plan"])
+
+    forward = run
+
+
+class BatchDecodeWithPagedKVCacheWrapper(_PagedWrapper):
+    """Call shape of ``flashinfer.decode.BatchDecodeWithPagedKVCacheWrapper`` as the
+    reference uses it (``compare_flashinfer_paths.py:103-118``): ``plan(indptr, indices,
+    last_page_len, num_qo_heads, num_kv_heads, head_dim, page_size, ...,
+    q_len_per_req=Q)`` then ``run(q, paged_kv_cache)``; ``Q`` draft rows per request
+    under the causal draft chain."""
+
+    def plan(self, indptr, indices, last_page_len, num_qo_heads, num_kv_heads, head_dim,
+             page_size, pos_encoding_mode="NONE", window_left=-1, logits_soft_cap=None,
+             q_data_type=None, kv_data_type=None, data_type=None, sm_scale=None,
+             rope_scale=None, rope_theta=None, non_blocking=True, q_len_per_req=1, **_unused):
+        self._plan(indptr, indices, last_page_len, num_qo_heads, num_kv_heads, head_dim,
+                   page_size, int(q_len_per_req), None, sm_scale, pos_encoding_mode,
+                   window_left, logits_soft_cap, q_data_type or data_type, kv_data_type)
+
+
+class BatchPrefillWithPagedKVCacheWrapper(_PagedWrapper):
+    """Call shape of ``flashinfer.prefill.BatchPrefillWithPagedKVCacheWrapper`` as the
+    reference uses it (``run_flashinfer_baseline.py:121-151``) for draft blocks:
+    every request has the same query length ``Q`` (``qo_indptr`` in steps of ``Q``),
+    its queries are the last ``Q`` positions of its KV. ``causal=True`` gives the
+    draft chain; ``causal=False`` lets every row see every token. Custom prefill
+    masks are not supported (use the packed draft mask of
+    :func:`xqa_batch_decode_with_kv_cache`)."""
+
+    def plan(self, qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len,
+             num_qo_heads, num_kv_heads, head_dim_qk, page_size, head_dim_vo=None,
+             custom_mask=None, packed_custom_mask=None, causal=False, pos_encoding_mode="NONE",
+             use_fp16_qk_reduction=False, sm_scale=None, window_left=-1, logits_soft_cap=None,
+             rope_scale=None, rope_theta=None, q_data_type=None, kv_data_type=None,
+             non_blocking=True, **_unused):
+        import torch
+
+        if custom_mask is not None or packed_custom_mask is not None:
+            raise ValueError("custom prefill masks are not supported")
+        if head_dim_vo not in (None, head_dim_qk):
+            raise ValueError("head_dim_vo must equal head_dim_qk")
+        qo = qo_indptr.to(torch.int64).cpu()
+        steps = qo[1:] - qo[:-1]
+        if steps.numel() == 0 or int(qo[0]) != 0 or bool((steps != steps[0]).any()):
+            raise ValueError("every request must have the same query length (uniform qo_indptr)")
+        q_len = int(steps[0])
+        if q_len < 1:
+            raise ValueError("query length must be positive")
+        mask = None
+        if not causal:
+            from .masks import spec_dec_mask
+
+            mask = as_words(spec_dec_mask(steps.numel(), q_len, "full",
+                                          device=paged_kv_indptr.device), steps.numel(), q_len)
+        self._plan(paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len, num_qo_heads,
+                   num_kv_heads, head_dim_qk, page_size, q_len, mask, sm_scale,
+                   pos_encoding_mode, window_left, logits_soft_cap, q_data_type, kv_data_type)
+
+
+__all__ = ["xqa_batch_decode_with_kv_cache", "trtllm_batch_decode_with_kv_cache",
+           "BatchDecodeWithPagedKVCacheWrapper", "BatchPrefillWithPagedKVCacheWrapper",
+           "csr_to_block_table"]

@@ -91,8 +91,9 @@ def test_plan_rejects_bad_arguments(lib):
 
 
 def _call(lib, **kw):
-    args = dict(q=1, k=1, v=1, bt=1, sl=1, out=1, ws=None, ws_bytes=0, batch=1, q_len=2, hq=32,
-                hkv=8, dim=128, num_pages=4, page=16, max_pages=2, splits=1, pps=2)
+    # Fake, 16-byte aligned device addresses: validation fails before any is used.
+    args = dict(q=16, k=16, v=16, bt=16, sl=16, out=16, ws=None, ws_bytes=0, batch=1, q_len=2,
+                hq=32, hkv=8, dim=128, num_pages=4, page=16, max_pages=2, splits=1, pps=2)
     args.update(kw)
     return lib.sqa_paged_mtp_attention(
         args["q"], args["k"], args["v"], args["bt"], args["sl"], args["out"], args["ws"],
@@ -113,15 +114,59 @@ def _call(lib, **kw):
     (dict(pps=-1), SQA_ERR_INVALID, "non-negative"),
     # Balanced plan: at most 256 sequences, at least one spare slot per sequence
     # plus enough slots to keep every split within 2048 pages.
-    (dict(pps=0, batch=257, splits=600, ws=1, ws_bytes=1 << 40), SQA_ERR_INVALID, "batch <= 256"),
-    (dict(pps=0, batch=4, splits=4, ws=1, ws_bytes=1 << 40), SQA_ERR_INVALID, "num_splits >="),
-    (dict(pps=0, batch=4, splits=7, max_pages=2049, ws=1, ws_bytes=1 << 40), SQA_ERR_INVALID,
+    (dict(pps=0, batch=257, splits=600, ws=16, ws_bytes=1 << 40), SQA_ERR_INVALID, "batch <= 256"),
+    (dict(pps=0, batch=4, splits=4, ws=16, ws_bytes=1 << 40), SQA_ERR_INVALID, "num_splits >="),
+    (dict(pps=0, batch=4, splits=7, max_pages=2049, ws=16, ws_bytes=1 << 40), SQA_ERR_INVALID,
      "num_splits >= batch + 5"),
     (dict(pps=0, batch=2, splits=3, ws=None), SQA_ERR_WORKSPACE, "workspace"),
     (dict(splits=2, ws=None), SQA_ERR_WORKSPACE, "workspace"),
-    (dict(splits=2, ws=1, ws_bytes=100), SQA_ERR_WORKSPACE, "workspace"),
+    (dict(splits=2, ws=16, ws_bytes=100), SQA_ERR_WORKSPACE, "workspace"),
+    (dict(k=24), SQA_ERR_INVALID, "16-byte aligned"),
 ])
 def test_launch_rejects_bad_arguments_without_a_gpu(lib, kw, code, msg):
     # Validation runs before any HIP call, so these pointers are never touched.
     assert _call(lib, **kw) == code
     assert msg in lib.sqa_last_error().decode()
+
+
+def _general(lib, **kw):
+    """sqa_paged_attention with fake aligned pointers and the given overrides."""
+    a = _lib.AttentionArgs()
+    a.struct_size = ctypes.sizeof(_lib.AttentionArgs)
+    a.query = a.output = a.block_tables = a.seq_lens = 16
+    a.kv = _lib.KVCache(16, 16, 4, 16 * 8 * 128, 8 * 128, 128)
+    a.max_pages, a.scale, a.out_scale = 2, 128 ** -0.5, 1.0
+    a.batch, a.q_len, a.num_query_heads, a.num_kv_heads = 1, 2, 32, 8
+    a.head_dim, a.page_size, a.num_splits, a.pages_per_split = 128, 16, 1, 2
+    for k, v in kw.items():
+        if k.startswith("kv_"):
+            setattr(a.kv, k[3:], v)
+        else:
+            setattr(a, k, v)
+    return lib.sqa_paged_attention(ctypes.byref(a))
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(struct_size=8), SQA_ERR_INVALID, "struct_size"),
+    (dict(kv_k=None), SQA_ERR_INVALID, "null"),
+    (dict(kv_token_stride=100), SQA_ERR_INVALID, "multiples of 8"),
+    (dict(kv_head_stride=-8), SQA_ERR_INVALID, "multiples of 8"),
+    (dict(kv_v=40), SQA_ERR_INVALID, "16-byte aligned"),
+    (dict(kv_token_stride=1 << 27), SQA_ERR_INVALID, "2 GiB"),
+    (dict(draft_mask=16, mask_words=0), SQA_ERR_INVALID, "draft_mask"),
+    (dict(draft_mask=16, mask_words=3), SQA_ERR_INVALID, "draft_mask"),
+    (dict(scale=0.0), SQA_ERR_INVALID, "scale"),
+    (dict(out_scale=float("inf")), SQA_ERR_INVALID, "out_scale"),
+    (dict(head_dim=64), SQA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(num_splits=2), SQA_ERR_WORKSPACE, "workspace"),
+])
+def test_general_entry_rejects_bad_arguments_without_a_gpu(lib, kw, code, msg):
+    assert _general(lib, **kw) == code
+    assert msg in lib.sqa_last_error().decode()
+
+
+def test_general_entry_struct_matches_the_header(lib):
+    # A struct of the wrong size is refused; the right one gets past that check
+    # (and is then refused for a missing workspace, before any device access).
+    assert _general(lib, struct_size=ctypes.sizeof(_lib.AttentionArgs) - 8) == SQA_ERR_INVALID
+    assert _general(lib, num_splits=2) == SQA_ERR_WORKSPACE

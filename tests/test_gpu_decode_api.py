@@ -1,0 +1,248 @@
+"""GPU parity of the general entry point (``sqa_paged_attention``) and the FlashInfer-shaped
+API (``small_q_attention_amd.decode_api``) with the oracle.
+
+Interleaved NHD / HND caches must give the same bits as the separate caches
+(the kernel reads the same values through other strides); draft masks, scales
+and CSR page lists are checked against the float64 C oracle at the parity bar
+``|a - r| <= 2e-3 + 1e-2 |r|``.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_c64
+from small_q_attention_amd import _lib, cuda as sqa, decode_api as fi, inputs
+from small_q_attention_amd.masks import pack_draft_mask, spec_dec_mask
+from tests._helpers import assert_parity, compact_sequences
+
+pytestmark = pytest.mark.gpu
+
+WORKSPACE = 64 << 20
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    sys.__stderr__.write(f"\n[gpu-test] {request.node.nodeid}\n")
+    sys.__stderr__.flush()
+
+
+def _inputs(lens, q_len, seed, **kw):
+    c = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=seed, **kw)
+    return tuple(t.cuda() for t in inputs.make_inputs(c))
+
+
+def _nhd(k, v):
+    return torch.stack([k, v], dim=1).contiguous()
+
+
+def _hnd(k, v):
+    return torch.stack([k, v], dim=1).permute(0, 1, 3, 2, 4).contiguous()
+
+
+def _oracle(q, k, v, bt, sl, **kw):
+    return attention_c64(q.cpu(), k.cpu(), v.cpu(), bt.cpu(), sl.cpu(), 16, k.shape[2], **kw)
+
+
+def _flat(q):
+    return q.reshape(-1, q.shape[2], q.shape[3])
+
+
+@pytest.mark.parametrize("q_len", [2, 8, 16])
+def test_interleaved_layouts_give_the_same_bits(q_len):
+    lens = [1, q_len, 333, 4100]
+    q, k, v, bt, sl = _inputs(lens, q_len, seed=500 + q_len)
+    base = sqa.paged_mtp_attention(q, k, v, bt, sl, 16, max(lens))
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    for layout, kv in (("NHD", _nhd(k, v)), ("HND", _hnd(k, v))):
+        out = fi.xqa_batch_decode_with_kv_cache(_flat(q), kv, ws, bt, sl, max(lens), 128 ** -0.5,
+                                                1.0, kv_layout=layout, q_len_per_req=q_len)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view_as(base), base), layout
+    # A (k_cache, v_cache) pair in HND order as well.
+    hk = k.transpose(1, 2).contiguous()
+    hv = v.transpose(1, 2).contiguous()
+    out = fi.trtllm_batch_decode_with_kv_cache(_flat(q), (hk, hv), ws, bt, sl, max(lens),
+                                               128 ** -0.5, 1.0, q_len_per_req=q_len)
+    assert torch.equal(out.view_as(base), base)
+    assert_parity(base, _oracle(q, k, v, bt, sl), label=f"q{q_len}")
+
+
+@pytest.mark.parametrize("q_len", [2, 4, 8, 16])
+def test_draft_masks(q_len):
+    """Causal packed mask = the default chain (same bits); full and random tree masks vs
+    the oracle, on sequences shorter than, equal to and far longer than the draft."""
+    lens = [max(1, q_len - 1), q_len, 17, 700, 5000]
+    q, k, v, bt, sl = _inputs(lens, q_len, seed=600 + q_len)
+    nhd = _nhd(k, v)
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    B = len(lens)
+
+    def call(mask, **kw):
+        o = fi.xqa_batch_decode_with_kv_cache(_flat(q), nhd, ws, bt, sl, max(lens), 128 ** -0.5,
+                                              1.0, q_len_per_req=q_len, mask=mask, **kw)
+        torch.cuda.synchronize()
+        return o.view_as(q)
+
+    default = call(None)
+    assert torch.equal(call(spec_dec_mask(B, q_len, device="cuda")), default)
+    full = spec_dec_mask(B, q_len, "full", device="cuda")
+    assert_parity(call(full), _oracle(q, k, v, bt, sl, draft_mask=full.cpu()), label="full")
+    g = torch.Generator().manual_seed(q_len)
+    vis = torch.rand(B, q_len, q_len, generator=g) < 0.4
+    vis[:, torch.arange(q_len), torch.arange(q_len)] = True
+    tree = pack_draft_mask(vis)
+    got = call(tree.cuda())
+    assert_parity(got, _oracle(q, k, v, bt, sl, draft_mask=tree), label="tree")
+    # Explicit fixed plans (several splits per sequence) agree with the automatic one.
+    for ck in (32, 512):
+        ns, pps = _lib.plan_splits(0, B, q_len, 32, 8, max(lens), bt.shape[1], ck)
+        out = torch.empty_like(q)
+        words = torch.from_numpy(tree.numpy().view(np.int32)).cuda()
+        wsb = torch.empty(max(1, _lib.workspace_bytes(B, q_len, 32, 8, ns, pps)),
+                          dtype=torch.uint8, device="cuda")
+        _lib.launch_general(q, out, nhd[:, 0], nhd[:, 1], bt, sl, words, 128 ** -0.5, 1.0, ns,
+                            pps, wsb, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert (out.float() - got.float()).abs().max().item() <= 2e-3, ck
+
+
+def test_scales():
+    q_len, lens = 4, [50, 3000]
+    q, k, v, bt, sl = _inputs(lens, q_len, seed=700)
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    for s1, s2 in ((0.05, 0.5), (0.2, 2.0), (torch.tensor(0.1), torch.tensor(1.5))):
+        out = fi.xqa_batch_decode_with_kv_cache(_flat(q), _nhd(k, v), ws, bt, sl, 3000, s1, s2,
+                                                q_len_per_req=q_len)
+        ref = _oracle(q, k, v, bt, sl, scale=float(s1), out_scale=float(s2))
+        assert_parity(out.view_as(q), ref, label=f"{float(s1)},{float(s2)}")
+
+
+def _csr(lens, page=16, seed=0, pool_pages=None):
+    """Ragged CSR page lists over a shuffled pool, plus the cache pages they index."""
+    g = torch.Generator().manual_seed(seed)
+    counts = [-(-n // page) for n in lens]
+    total = sum(counts)
+    pool = pool_pages or 2 * total + 3
+    ids = torch.randperm(pool, generator=g)[:total].to(torch.int32)
+    indptr = torch.tensor([0] + list(np.cumsum(counts)), dtype=torch.int32)
+    last = torch.tensor([(n - 1) % page + 1 if n else 1 for n in lens], dtype=torch.int32)
+    return indptr, ids, last, pool
+
+
+@pytest.mark.parametrize("q_len", [1, 3, 8])
+def test_wrappers_over_csr_pages(q_len):
+    lens = [q_len, 16, 1000, 37, 4096 + 5]
+    indptr, ids, last, pool = _csr(lens, seed=q_len)
+    g = torch.Generator().manual_seed(800 + q_len)
+    hq, hkv = 32, 8
+    kv = torch.randn(pool, 2, 16, hkv, 128, generator=g).half().cuda()
+    q = torch.randn(len(lens) * q_len, hq, 128, generator=g).half().cuda()
+    bt, sl = fi.csr_to_block_table(indptr, ids, last)
+    assert sl.tolist() == lens
+    q4 = q.view(len(lens), q_len, hq, 128)
+    ref = _oracle(q4, kv[:, 0], kv[:, 1], bt, sl)
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+
+    dec = fi.BatchDecodeWithPagedKVCacheWrapper(ws, "NHD", use_tensor_cores=True)
+    dec.plan(indptr.cuda(), ids.cuda(), last.cuda(), hq, hkv, 128, 16, pos_encoding_mode="NONE",
+             q_data_type=torch.float16, kv_data_type=torch.float16, q_len_per_req=q_len)
+    for _ in range(2):  # plan once, run per layer
+        assert_parity(dec.run(q, kv).view_as(q4), ref, label="decode")
+
+    pre = fi.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    qo = torch.arange(0, (len(lens) + 1) * q_len, q_len, dtype=torch.int32, device="cuda")
+    pre.plan(qo, indptr.cuda(), ids.cuda(), last.cuda(), hq, hkv, 128, 16, causal=True,
+             pos_encoding_mode="NONE", logits_soft_cap=0.0, q_data_type=torch.float16,
+             kv_data_type=torch.float16)
+    assert_parity(pre.run(q, kv).view_as(q4), ref, label="prefill causal")
+    pre.plan(qo, indptr.cuda(), ids.cuda(), last.cuda(), hq, hkv, 128, 16, causal=False)
+    full = spec_dec_mask(len(lens), q_len, "full")
+    ref_full = _oracle(q4, kv[:, 0], kv[:, 1], bt, sl, draft_mask=full)
+    assert_parity(pre.run(q, kv).view_as(q4), ref_full, label="prefill full")
+
+    hnd = kv.permute(0, 1, 3, 2, 4).contiguous()
+    dec_h = fi.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    dec_h.plan(indptr.cuda(), ids.cuda(), last.cuda(), hq, hkv, 128, 16, q_len_per_req=q_len)
+    assert torch.equal(dec_h.run(q, hnd), dec.run(q, kv))
+
+
+def test_wrapper_run_is_graph_capturable():
+    q_len, lens = 8, [3000, 1200, 64]
+    indptr, ids, last, pool = _csr(lens, seed=9)
+    g = torch.Generator().manual_seed(9)
+    kv = torch.randn(pool, 2, 16, 8, 128, generator=g).half().cuda()
+    q = torch.randn(len(lens) * q_len, 32, 128, generator=g).half().cuda()
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    dec = fi.BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
+    dec.plan(indptr.cuda(), ids.cuda(), last.cuda(), 32, 8, 128, 16, q_len_per_req=q_len)
+    out = torch.empty_like(q)
+    eager = dec.run(q, kv).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        dec.run(q, kv, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        dec.run(q, kv, out=out)
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        junk = torch.randn(1 << 20, device="cuda").sum()
+        torch.cuda.synchronize()
+        del junk
+
+
+def test_full_size_properties():
+    """cfg3 shape (B16 q8 KV 32768): the NHD cache and a causal packed mask give the
+    separate-cache bits; a tree mask changes only rows whose draft bits change."""
+    case = inputs.baseline_configs()["cfg3"]
+    q, k, v, bt, sl = inputs.make_inputs(case, device="cuda", gen_device="cuda")
+    base = sqa.paged_mtp_attention(q, k, v, bt, sl, 16, 32768)
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    nhd = _nhd(k, v)
+    del k, v
+    torch.cuda.empty_cache()
+    mask = spec_dec_mask(16, 8, device="cuda")
+    out = fi.xqa_batch_decode_with_kv_cache(_flat(q), nhd, ws, bt, sl, 32768, 128 ** -0.5, 1.0,
+                                            q_len_per_req=8, mask=mask)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view_as(base), base)
+    vis = torch.tril(torch.ones(8, 8, dtype=torch.bool)).repeat(16, 1, 1)
+    vis[3, 5, 2] = False  # sequence 3, row 5 no longer sees draft token 2
+    out = fi.xqa_batch_decode_with_kv_cache(_flat(q), nhd, ws, bt, sl, 32768, 128 ** -0.5, 1.0,
+                                            q_len_per_req=8, mask=pack_draft_mask(vis).cuda())
+    torch.cuda.synchronize()
+    out = out.view_as(base)
+    changed = (out != base).flatten(2).any(-1)  # [B, Q]
+    assert changed[3, 5]
+    # Other rows move at most by rounding (the wave's rescale points can shift).
+    others = torch.ones_like(changed)
+    others[3, 5] = False
+    assert (out.float() - base.float()).abs().amax((2, 3))[others].max().item() <= 2e-3
+    # Sequence 3 against the oracle with its mask.
+    cq, ck, cv, cbt, csl = compact_sequences(q, nhd[:, 0], nhd[:, 1], bt, sl, [3])
+    ref = attention_c64(cq, ck, cv, cbt, csl, 16, 8, draft_mask=pack_draft_mask(vis[3:4]))
+    assert_parity(out[3:4], ref, label="cfg3 tree row")
+
+
+def test_workspace_and_argument_checks():
+    q, k, v, bt, sl = _inputs([100, 200], 4, seed=1)
+    small = torch.zeros(64, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError, match="workspace"):
+        fi.xqa_batch_decode_with_kv_cache(_flat(q), _nhd(k, v), small, bt, sl, 200, 0.1, 1.0,
+                                          q_len_per_req=4)
+    with pytest.raises(ValueError, match="window"):
+        fi.xqa_batch_decode_with_kv_cache(_flat(q), _nhd(k, v), None, bt, sl, 200, 0.1, 1.0, 8,
+                                          q_len_per_req=4)
+    with pytest.raises(ValueError, match="rows"):
+        fi.xqa_batch_decode_with_kv_cache(_flat(q), _nhd(k, v), None, bt, sl, 200, 0.1, 1.0,
+                                          q_len_per_req=2)
+    with pytest.raises(ValueError, match="draft mask"):
+        fi.xqa_batch_decode_with_kv_cache(_flat(q), _nhd(k, v), None, bt, sl, 200, 0.1, 1.0,
+                                          q_len_per_req=4, mask=spec_dec_mask(2, 2).cuda())
