@@ -6,7 +6,8 @@
  * Tensor contract (reference: /root/reference/csrc/small_q_attention_ext.cu:976-1002,
  * /root/reference/src/small_q_attention/cuda.py:61-78):
  *   query        [batch, q_len, num_query_heads, 128]  fp16, contiguous, device
- *   key_cache    [num_pages, 16, num_kv_heads, 128]    fp16, contiguous, device
+ *   key_cache    [num_pages, page_size, num_kv_heads, 128]  fp16, contiguous, device;
+ *                page_size 16 (the reference's), 32 or 64
  *   value_cache  same shape as key_cache
  *   block_tables [batch, max_pages] int32, device
  *   seq_lens     [batch] int32, device; KV length including the q_len draft tokens
@@ -46,6 +47,8 @@ extern "C" {
  *     sizes the splits on the device from the sum of seq_lens, so ragged
  *     batches spread evenly over the chip without a host sync. Otherwise a
  *     fixed plan as above.
+ * max_pages: 16-token pages a block-table row addresses (block_tables columns
+ * x page_size / 16); num_splits and pages_per_split count 16-token pages too.
  * max_seq_len <= 0 means "unknown": a fixed plan covers max_pages * 16 tokens.
  * Writes *num_splits >= 1 and *pages_per_split >= 0.
  */
@@ -68,7 +71,8 @@ size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv
  * forward, forward_v1..forward_v5 (csrc/small_q_attention_ext.cu:969-1378,
  * :1380-1390). num_splits/pages_per_split come from sqa_plan_splits
  * (pages_per_split 0: balanced plan, batch <= 256 and num_splits >= batch +
- * max(1, ceil(batch * max_pages / 2048))). `workspace` must hold
+ * max(1, ceil(batch * max_pages * page_size / 16 / 2048))); max_pages is the
+ * block_tables row length. `workspace` must hold
  * sqa_workspace_bytes(...) bytes (may be NULL when that is 0). Allocates
  * nothing and never synchronises.
  * `timing_events`: NULL, or an array of 3 hipEvent_t recorded on `stream`

@@ -148,8 +148,14 @@ int run_attention(const sqa_attention_args& a) {
     return fail(SQA_ERR_INVALID, "num_query_heads must be divisible by num_kv_heads");
   if (head_dim != sqa::kHeadDim)
     return fail(SQA_ERR_UNSUPPORTED, "head_dim must be %d (got %d)", sqa::kHeadDim, head_dim);
-  if (page_size != sqa::kPageSize)
-    return fail(SQA_ERR_UNSUPPORTED, "page_size must be %d (got %d)", sqa::kPageSize, page_size);
+  int page_shift = -1;
+  for (int sh = 0; sh <= sqa::kMaxPageShift; ++sh)
+    if (page_size == (sqa::kPageSize << sh)) page_shift = sh;
+  if (page_shift < 0)
+    return fail(SQA_ERR_UNSUPPORTED, "page_size must be 16, 32 or 64 (got %d)", page_size);
+  // The kernels work in 16-token pages; a cache page is 1 << page_shift of them.
+  const long long kernel_pages = (long long)max_pages << page_shift;
+  if (kernel_pages > 0x7fffffffLL) return fail(SQA_ERR_INVALID, "block table too wide");
   const int group = num_query_heads / num_kv_heads;
   const long long rows = (long long)q_len * group;
   if (rows > sqa::kMaxRows)
@@ -181,7 +187,7 @@ int run_attention(const sqa_attention_args& a) {
     if (batch > sqa::kMaxBalancedBatch)
       return fail(SQA_ERR_INVALID, "balanced plan (pages_per_split 0) needs batch <= %d, got %d",
                   sqa::kMaxBalancedBatch, batch);
-    const long long cap = ceil_div((long long)batch * max_pages, sqa::kMaxSplitPages);
+    const long long cap = ceil_div((long long)batch * kernel_pages, sqa::kMaxSplitPages);
     if ((long long)num_splits - batch < (cap > 1 ? cap : 1))
       return fail(SQA_ERR_INVALID,
                   "balanced plan needs num_splits >= batch + %lld (batch %d), got %d",
@@ -229,7 +235,9 @@ int run_attention(const sqa_attention_args& a) {
   pa.hkv = num_kv_heads;
   pa.group = group;
   pa.rows = (int)rows;
-  pa.max_pages = max_pages;
+  pa.bt_stride = max_pages;
+  pa.page_shift = page_shift;
+  pa.max_pages = (int)kernel_pages;
   pa.pages_per_split = pages_per_split;
   pa.num_splits = num_splits;
   pa.scale_log2 = (float)(1.4426950408889634 * (double)a.scale);
@@ -252,7 +260,7 @@ int run_attention(const sqa_attention_args& a) {
     ma.hkv = num_kv_heads;
     ma.group = group;
     ma.rows = (int)rows;
-    ma.max_pages = max_pages;
+    ma.max_pages = (int)kernel_pages;
     ma.pages_per_split = pages_per_split;
     ma.num_splits = num_splits;
     ma.out_scale = a.out_scale;

@@ -8,7 +8,8 @@
 namespace sqa {
 
 constexpr int kHeadDim = 128;   // contract: head_dim 128
-constexpr int kPageSize = 16;   // contract: 16-token pages
+constexpr int kPageSize = 16;   // kernel page: 16 tokens (one MFMA tile of keys)
+constexpr int kMaxPageShift = 2;  // cache pages of 16 << shift tokens: 16, 32, 64
 constexpr int kMaxRows = 64;    // q_len * (Hq / Hkv) rows one work item holds
 constexpr int kMaxSplitPages = 2048;  // pages one split may own (LDS page-id table)
 constexpr int kMinSplitPages = 4;     // fewest pages the automatic plans give a split
@@ -36,7 +37,7 @@ struct PartialArgs {
   const _Float16* q;          // [B, Q, Hq, 128]
   const _Float16* k;          // K of page 0, slot 0, kv head 0
   const _Float16* v;          // V of page 0, slot 0, kv head 0
-  const int32_t* block_tables;  // [B, max_pages]
+  const int32_t* block_tables;  // [B, bt_stride] cache-page ids
   const int32_t* seq_lens;      // [B]
   const uint32_t* draft_mask;   // NULL (causal draft chain) or [B, Q, mask_words]
   _Float16* out;              // [B, Q, Hq, 128]; written directly when num_splits == 1
@@ -44,13 +45,15 @@ struct PartialArgs {
   float* part_ml;             // [slots, Hkv, rows, 2] (max in log2 units, sum)
   SeqSplits* seq_splits;      // [B] (balanced plan only)
   long long num_pages;        // pages in the cache pool; ids outside are clamped to 0
-  long long page_stride;      // bytes between consecutive pages (K and V alike)
+  long long page_stride;      // bytes between consecutive cache pages (K and V alike)
   unsigned token_stride;      // bytes between consecutive slots of a page
   unsigned head_stride;       // bytes between consecutive kv heads
-  unsigned page_extent;       // bytes from a page's base that its K (or V) spans
+  unsigned page_extent;       // bytes from a kernel page's base that its K (or V) spans
   int mask_words;             // 32-bit words per draft-mask row (1 or 2)
   int batch, q_len, hq, hkv, group, rows;
-  int max_pages;              // block_tables row length
+  int bt_stride;              // block_tables row length (cache pages)
+  int page_shift;             // cache page = 16 << page_shift tokens = 1 << page_shift kernel pages
+  int max_pages;              // kernel pages a block-table row addresses (bt_stride << page_shift)
   int pages_per_split, num_splits;
   float scale_log2;           // softmax scale * log2(e)
   float out_scale;            // multiplier applied to the normalised output
@@ -70,7 +73,8 @@ struct MergeArgs {
   const int32_t* seq_lens;
   _Float16* out;
   int batch, q_len, hq, hkv, group, rows;
-  int max_pages, pages_per_split, num_splits;
+  int max_pages;  // kernel pages a block-table row addresses
+  int pages_per_split, num_splits;
   float out_scale;
 };
 

@@ -354,20 +354,32 @@ void sqa_partial_kernel(PartialArgs a) {
   // alongside; balanced plan: all seq_lens and a workgroup scan).
   __shared__ int sm_plan[16];
   const bool balanced = is_balanced(a.pages_per_split);
-  const ItemRange it = balanced ? balanced_item<WW * 64>(a, item, sm_plan) : fixed_item(a, item);
+  ItemRange it = balanced ? balanced_item<WW * 64>(a, item, sm_plan) : fixed_item(a, item);
+  // The work item is the same for the whole workgroup; saying so keeps it (and
+  // the buffer-resource addresses built from it) in scalar registers.
+  it.b = __builtin_amdgcn_readfirstlane(it.b);
+  it.split = __builtin_amdgcn_readfirstlane(it.split);
+  it.p_begin = __builtin_amdgcn_readfirstlane(it.p_begin);
+  it.p_end = __builtin_amdgcn_readfirstlane(it.p_end);
+  it.len = __builtin_amdgcn_readfirstlane(it.len);
+  it.n_valid = __builtin_amdgcn_readfirstlane(it.n_valid);
+  it.slot0 = __builtin_amdgcn_readfirstlane(it.slot0);
   const bool single = !balanced && a.num_splits == 1;  // no merge kernel follows
   const int b = max(it.b, 0);
   const int split = it.split;
   const int len = it.len;
   const int p_begin = it.p_begin;
   const int p_end = it.p_end;
-  const int32_t* bt_row = a.block_tables + (size_t)b * a.max_pages;
+  const int32_t* bt_row = a.block_tables + (size_t)b * a.bt_stride;
+  const int shift = a.page_shift;
+  const int sub_mask = (1 << shift) - 1;
   // Ids of the split's first D pages (index clamped into the block-table row;
   // ids past the split are never used), issued before the exits below so the
   // fixed plan loads them together with the sequence length.
   int first_id[D];
 #pragma unroll
-  for (int j = 0; j < D; ++j) first_id[j] = bt_row[min(max(p_begin + j, 0), a.max_pages - 1)];
+  for (int j = 0; j < D; ++j)
+    first_id[j] = bt_row[min(max(p_begin + j, 0), a.max_pages - 1) >> shift];
   if (it.b < 0) return;                           // uniform: no work item
   if (p_begin >= p_end && !single) return;        // uniform; never merged
   const int n_split = p_end > p_begin ? p_end - p_begin : 0;
@@ -417,7 +429,7 @@ void sqa_partial_kernel(PartialArgs a) {
 #pragma unroll
   for (int k = 0; k < kIdSlots; ++k) {
     const int i = threadIdx.x + k * WW * 64;
-    const int x = bt_row[p_begin + min(i, last_id)];
+    const int x = bt_row[(p_begin + min(i, last_id)) >> shift];
     idreg[k] = i < n_split ? x : -1;
   }
 
@@ -432,8 +444,12 @@ void sqa_partial_kernel(PartialArgs a) {
   // touching memory, so every slot refill below is unconditional and the
   // compiler's wait counts stay exact (one page retires per step). K/V are
   // streamed once, so the loads are non-temporal.
-  auto load_page = [&](int pid, PageRegs& pg) {
-    const size_t off = pid >= 0 ? (size_t)pid * (size_t)a.page_stride : 0;
+  // Kernel page p of the sequence is sub-page p & sub_mask of cache page
+  // block_tables[b][p >> shift].
+  const size_t sub_bytes = (size_t)kPageSize * tok_bytes;
+  auto load_page = [&](int pid, int p, PageRegs& pg) {
+    const size_t off =
+        pid >= 0 ? (size_t)pid * (size_t)a.page_stride + (size_t)(p & sub_mask) * sub_bytes : 0;
     const int nrec = pid >= 0 ? (int)a.page_extent : 0;
     const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)((const char*)a.k + off), (short)0, nrec, kBufferFlags);
@@ -451,7 +467,7 @@ void sqa_partial_kernel(PartialArgs a) {
   PageRegs ring[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {
-    load_page(j < n_pages ? clamp_page(first_id[j], a.num_pages) : -1, ring[j]);
+    load_page(j < n_pages ? clamp_page(first_id[j], a.num_pages) : -1, p_begin + j, ring[j]);
   }
 
   // LDS: the Q fragments of this wave's rows, [wave][nb][kk][lane] (the
@@ -500,7 +516,7 @@ void sqa_partial_kernel(PartialArgs a) {
       }
       const int pid = next_pid;
       next_pid = page_id(ii + D + 1);
-      load_page(pid, ring[j]);
+      load_page(pid, p_begin + ii + D, ring[j]);
     }
   }
   if (!active) return;

@@ -19,8 +19,8 @@ non-contiguous, not fp16, an unsupported ``q_len`` or ``head_dim``
 Deliberate contract differences:
 * ``q_len`` 16 is accepted (the reference allows 2, 4, 8): ``q_len * group``
   must be at most 64 rows.
-* ``page_size`` must be 16 and ``head_dim`` 128 (the reference's launchers take
-  any page size, but every reference caller uses 16).
+* ``page_size`` must be 16, 32 or 64 and ``head_dim`` 128 (the reference's
+  launchers take any page size, but every reference caller uses 16).
 * ``chunk_keys=None`` selects the automatic split plan (from the CU count).
 * ``token_group`` (v5) is validated and otherwise ignored: every draft row
   already shares one K/V load.
@@ -36,6 +36,7 @@ from . import _lib
 SUPPORTED_Q_LENS = (2, 4, 8, 16)
 HEAD_DIM = 128
 PAGE_SIZE = 16
+SUPPORTED_PAGE_SIZES = (16, 32, 64)
 MAX_ROWS = 64
 
 
@@ -168,8 +169,8 @@ def _check_launcher_contract(query, key_cache, value_cache, block_tables, seq_le
         raise RuntimeError("empty KV cache is not supported")
     if batch == 0:
         raise RuntimeError("batch must be positive")
-    if cache_page != PAGE_SIZE:
-        raise ValueError("this build supports page_size 16")
+    if cache_page not in SUPPORTED_PAGE_SIZES:
+        raise ValueError("this build supports page_size 16, 32 or 64")
     if q_len * (hq // hkv) > MAX_ROWS:
         raise ValueError("q_len * (Hq / Hkv) must be at most 64")
 
@@ -191,8 +192,10 @@ def _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
     batch, q_len, hq, _ = query.shape
     hkv = key_cache.shape[2]
     ck = 0 if chunk_keys is None else int(chunk_keys)
+    # The plan counts 16-token kernel pages.
+    kernel_pages = block_tables.shape[1] * (key_cache.shape[1] // PAGE_SIZE)
     num_splits, pps = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv,
-                                       int(max_seq_len), block_tables.shape[1], ck)
+                                       int(max_seq_len), kernel_pages, ck)
     if _tracing():
         # Under torch.compile / export the registered custom op is the traceable unit.
         return _lib.custom_op()(query, key_cache, value_cache, block_tables, seq_lens,

@@ -5,7 +5,8 @@ The reference compares its kernels with four FlashInfer paths for the same op
 ``scripts/compare_flashinfer_paths.py:95-160``,
 ``scripts/probe_decode_wrapper_mtp.py``). This module offers the same call shapes,
 so code written against them runs here unchanged, within the contract of this
-build (fp16 Q/K/V, head_dim 128, 16-token pages, ``q_len * Hq / Hkv <= 64``):
+build (fp16 Q/K/V, head_dim 128, pages of 16, 32 or 64 tokens,
+``q_len * Hq / Hkv <= 64``):
 
 * :func:`xqa_batch_decode_with_kv_cache` — block table + seq_lens, interleaved
   ``[P, 2, 16, Hkv, D]`` ("NHD") or ``[P, 2, Hkv, 16, D]`` ("HND") cache or a
@@ -32,7 +33,8 @@ from typing import Optional
 from . import _lib
 from .masks import as_words
 
-PAGE_SIZE = 16
+PAGE_SIZE = 16  # tokens per kernel page; cache pages hold 16, 32 or 64
+PAGE_SIZES = (16, 32, 64)
 HEAD_DIM = 128
 
 
@@ -66,8 +68,8 @@ def _check_tensors(query, k, v, num_qo_heads: Optional[int] = None):
         raise ValueError("query must be a contiguous [B * Q, Hq, D] tensor")
     if query.shape[-1] != HEAD_DIM or k.shape[-1] != HEAD_DIM:
         raise ValueError("this build supports head_dim 128")
-    if k.shape[1] != PAGE_SIZE:
-        raise ValueError("this build supports page_size 16")
+    if k.shape[1] not in PAGE_SIZES:
+        raise ValueError("this build supports page_size 16, 32 or 64")
     if num_qo_heads is not None and query.shape[1] != num_qo_heads:
         raise ValueError(f"query has {query.shape[1]} heads, plan() was given {num_qo_heads}")
 
@@ -95,8 +97,8 @@ def _run(query, k, v, block_tables, seq_lens, max_seq_len: int, q_len: int, scal
     elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor shaped and typed like query")
     if plan is None:
-        plan = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv,
-                                int(max_seq_len), block_tables.shape[1], 0)
+        plan = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv, int(max_seq_len),
+                                block_tables.shape[1] * (k.shape[1] // PAGE_SIZE), 0)
     ns, pps = plan
     need = _lib.workspace_bytes(batch, q_len, hq, hkv, ns, pps)
     ws = None
@@ -217,15 +219,16 @@ class _PagedWrapper:
         for dt in (q_data_type, kv_data_type):
             if dt not in (None, torch.float16, "float16", "fp16"):
                 raise ValueError("this build supports fp16 query and KV")
-        if head_dim != HEAD_DIM or page_size != PAGE_SIZE:
-            raise ValueError("this build supports head_dim 128 and page_size 16")
+        if head_dim != HEAD_DIM or page_size not in PAGE_SIZES:
+            raise ValueError("this build supports head_dim 128 and page_size 16, 32 or 64")
         if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
             raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
         block_tables, seq_lens = csr_to_block_table(indptr, indices, last_page_len, page_size)
         batch = block_tables.shape[0]
         max_seq_len = int(seq_lens.max()) if batch else 0
         plan = _lib.plan_splits(block_tables.device.index or 0, batch, q_len, num_qo_heads,
-                                num_kv_heads, max(max_seq_len, 1), block_tables.shape[1], 0)
+                                num_kv_heads, max(max_seq_len, 1),
+                                block_tables.shape[1] * (page_size // PAGE_SIZE), 0)
         need = _lib.workspace_bytes(batch, q_len, num_qo_heads, num_kv_heads, *plan)
         if need and self._workspace is not None:
             have = self._workspace.numel() * self._workspace.element_size()
@@ -235,6 +238,7 @@ class _PagedWrapper:
         self._planned = dict(block_tables=block_tables, seq_lens=seq_lens, plan=plan,
                              q_len=q_len, hq=num_qo_heads, hkv=num_kv_heads,
                              max_seq_len=max_seq_len, mask_words=mask_words,
+                             page_size=page_size,
                              scale=HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale))
 
     def run(self, q, paged_kv_cache, *_unused, out=None, **_kw):
@@ -245,6 +249,9 @@ class _PagedWrapper:
         _check_tensors(q, k, v, p["hq"])
         if k.shape[2] != p["hkv"]:
             raise ValueError(f"kv_cache has {k.shape[2]} kv heads, plan() was given {p['hkv']}")
+        if k.shape[1] != p["page_size"]:
+            raise ValueError(f"kv_cache pages hold {k.shape[1]} tokens, plan() was given "
+                             f"{p['page_size']}")
         return _run(q, k, v, p["block_tables"], p["seq_lens"], p["max_seq_len"], p["q_len"],
                     p["scale"], 1.0, p["mask_words"], self._workspace, out, plan=p["plan"])
 

@@ -162,6 +162,6 @@ def test_launcher_contract_raises_runtime_error(fake_gpu, mutation):
 
 def test_unsupported_page_size_and_row_count_raise_value_error(fake_gpu):
     with pytest.raises(ValueError):
-        sqa.forward_v0(*_args(good_inputs(page=32))[:5], 32)
+        sqa.forward_v0(*_args(good_inputs(page=8))[:5], 8)
     with pytest.raises(ValueError):  # q_len 16 x group 8 = 128 rows > 64
         sqa.forward_v0(*_args(good_inputs(q_len=16, hq=32, hkv=4)))

@@ -107,7 +107,11 @@ def _call(lib, **kw):
     (dict(num_pages=0), SQA_ERR_INVALID, "empty"),
     (dict(hkv=5), SQA_ERR_INVALID, "divisible"),
     (dict(dim=64), SQA_ERR_UNSUPPORTED, "head_dim"),
-    (dict(page=32), SQA_ERR_UNSUPPORTED, "page_size"),
+    (dict(page=24), SQA_ERR_UNSUPPORTED, "page_size"),
+    (dict(page=128), SQA_ERR_UNSUPPORTED, "page_size"),
+    # 64-token pages: the balanced plan's slot bound counts 16-token pages.
+    (dict(pps=0, batch=4, splits=7, max_pages=513, page=64, ws=16, ws_bytes=1 << 40),
+     SQA_ERR_INVALID, "num_splits >= batch + 5"),
     (dict(q_len=32), SQA_ERR_UNSUPPORTED, "exceeds"),
     (dict(splits=0), SQA_ERR_INVALID, "positive"),
     (dict(pps=2049), SQA_ERR_INVALID, "exceeds"),

@@ -43,7 +43,8 @@ def _hnd(k, v):
 
 
 def _oracle(q, k, v, bt, sl, **kw):
-    return attention_c64(q.cpu(), k.cpu(), v.cpu(), bt.cpu(), sl.cpu(), 16, k.shape[2], **kw)
+    return attention_c64(q.cpu(), k.cpu(), v.cpu(), bt.cpu(), sl.cpu(), k.shape[1], k.shape[2],
+                         **kw)
 
 
 def _flat(q):
@@ -246,3 +247,57 @@ def test_workspace_and_argument_checks():
     with pytest.raises(ValueError, match="draft mask"):
         fi.xqa_batch_decode_with_kv_cache(_flat(q), _nhd(k, v), None, bt, sl, 200, 0.1, 1.0,
                                           q_len_per_req=4, mask=spec_dec_mask(2, 2).cuda())
+
+
+def _as_16_token_pages(k, v, bt, page):
+    """The same cache memory viewed as 16-token pages: cache page p is 16-token
+    pages p * r .. p * r + r - 1 (r = page / 16)."""
+    r = page // 16
+    k16 = k.view(k.shape[0] * r, 16, k.shape[2], k.shape[3])
+    v16 = v.view(v.shape[0] * r, 16, v.shape[2], v.shape[3])
+    sub = torch.arange(r, dtype=torch.int32, device=bt.device)
+    bt16 = (bt[:, :, None] * r + sub).reshape(bt.shape[0], -1).contiguous()
+    return k16, v16, bt16
+
+
+@pytest.mark.parametrize("page", [32, 64])
+@pytest.mark.parametrize("q_len", [2, 8, 16])
+def test_larger_cache_pages(page, q_len):
+    """32- and 64-token cache pages through the reference boundary and the
+    FlashInfer-shaped calls: parity with the oracle, and the same bits as the same
+    memory addressed as 16-token pages."""
+    lens = [1, q_len, page - 1, page, page + 1, 700, 5000]
+    c = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=900 + page + q_len,
+                    page_size=page)
+    q, k, v, bt, sl = (t.cuda() for t in inputs.make_inputs(c))
+    ref = _oracle(q, k, v, bt, sl)
+    auto = sqa.paged_mtp_attention(q, k, v, bt, sl, page, max(lens))
+    assert_parity(auto, ref, label=f"p{page} auto")
+    assert_parity(sqa.forward_v3(q, k, v, bt, sl, page, 128, max(lens)), ref, label="v3 c128")
+    assert_parity(sqa.forward_v0(q, k, v, bt, sl, page), ref, label="v0")
+    k16, v16, bt16 = _as_16_token_pages(k, v, bt, page)
+    assert torch.equal(sqa.paged_mtp_attention(q, k16, v16, bt16, sl, 16, max(lens)), auto)
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    g = torch.Generator().manual_seed(page + q_len)
+    vis = torch.rand(len(lens), q_len, q_len, generator=g) < 0.5
+    vis[:, torch.arange(q_len), torch.arange(q_len)] = True
+    mask = pack_draft_mask(vis)
+    out = fi.xqa_batch_decode_with_kv_cache(_flat(q), _hnd(k, v), ws, bt, sl, max(lens),
+                                            128 ** -0.5, 1.0, kv_layout="HND",
+                                            q_len_per_req=q_len, mask=mask.cuda())
+    assert_parity(out.view_as(q), _oracle(q, k, v, bt, sl, draft_mask=mask), label="HND tree")
+
+
+def test_larger_cache_pages_full_size():
+    """cfg3 shape with 64-token pages: the same bits as the 16-token view of the memory."""
+    case = inputs.baseline_configs()["cfg3"]
+    case.page_size = 64
+    q, k, v, bt, sl = inputs.make_inputs(case, device="cuda", gen_device="cuda")
+    out64 = sqa.paged_mtp_attention(q, k, v, bt, sl, 64, 32768)
+    k16, v16, bt16 = _as_16_token_pages(k, v, bt, 64)
+    out16 = sqa.paged_mtp_attention(q, k16, v16, bt16, sl, 16, 32768)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out64.float()).all()
+    assert torch.equal(out64, out16)
+    cq, ck, cv, cbt, csl = compact_sequences(q, k16, v16, bt16, sl, [0, 11])
+    assert_parity(out64[[0, 11]], attention_c64(cq, ck, cv, cbt, csl, 16, 8), label="cfg3 p64")
