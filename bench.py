@@ -262,6 +262,29 @@ def main():
                                "kernel_us": round(px * 1e3, 2),
                                "kernel_frac": round(kvb / (px * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
         result["per_q_len"] = extra
+        # The same workload with bf16 Q/K/V (general entry point).
+        qb, kb, vb = q.bfloat16(), k.bfloat16(), v.bfloat16()
+        outb = torch.empty_like(qb)
+        nbytes = _lib.workspace_bytes(case.batch, case.q_len, case.num_query_heads,
+                                      case.num_kv_heads, plan[0], plan[1])
+        wsb = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+        handle = torch.cuda.current_stream().cuda_stream
+
+        def bf16_call(ev=None):
+            _lib.launch_general(qb, outb, kb, vb, bt, sl, None, case.head_dim ** -0.5, 1.0,
+                                plan[0], plan[1], wsb, handle, timing_events=ev)
+
+        for _ in range(args.warmup):
+            bf16_call()
+        kev = _events(torch, 3 * args.steps)
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            bf16_call([e.cuda_event for e in kev[3 * i:3 * i + 3]])
+        torch.cuda.synchronize()
+        pb = statistics.mean(kev[3 * i].elapsed_time(kev[3 * i + 1]) for i in range(args.steps))
+        result["bf16"] = {"kernel_us": round(pb * 1e3, 2),
+                          "kernel_frac": round(kvb / (pb * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+        del qb, kb, vb, outb, wsb
     if not args.no_per_q:
         # The other single-GPU BASELINE configs, same timing (extra fields only).
         others = {}

@@ -34,6 +34,10 @@ extern "C" {
 #define SQA_ERR_WORKSPACE 3   /* workspace missing or too small */
 #define SQA_ERR_HIP 4         /* HIP runtime error (launch, device query) */
 
+/* Element types of sqa_attention_args.dtype (query, caches and output alike). */
+#define SQA_DTYPE_F16 0
+#define SQA_DTYPE_BF16 1
+
 /*
  * Chooses the split-KV decomposition.
  * Replaces the reference chunking policy (csrc/small_q_attention_ext.cu:1096-1099,
@@ -123,6 +127,9 @@ typedef struct sqa_kv_cache {
  *               mask_words >= ceil(q_len / 32), at most 2.
  *   scale       softmax scale (> 0; the reference uses head_dim^-1/2).
  *   out_scale   multiplier of the normalised output (1 for plain attention).
+ *   dtype       SQA_DTYPE_F16 (the reference's) or SQA_DTYPE_BF16 for query,
+ *               caches and output; probabilities are rounded to the same type
+ *               before the PV product, accumulation is fp32.
  */
 typedef struct sqa_attention_args {
   size_t struct_size;
@@ -148,6 +155,7 @@ typedef struct sqa_attention_args {
   size_t workspace_bytes;
   void* stream;
   void** timing_events;
+  int dtype;
 } sqa_attention_args;
 
 /*

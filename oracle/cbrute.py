@@ -38,10 +38,12 @@ def _load():
         lib.sqa_oracle_f64_ex.restype = ctypes.c_int
         lib.sqa_oracle_f64_ex.argtypes = (
             [ctypes.c_void_p] * 3 + [ctypes.c_longlong] * 3 + [ctypes.c_void_p] * 3
-            + [ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_void_p]
+            + [ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_int, ctypes.c_void_p]
             + [ctypes.c_int] * 7 + [ctypes.c_longlong])
         lib.sqa_oracle_half_to_double.restype = ctypes.c_double
         lib.sqa_oracle_half_to_double.argtypes = [ctypes.c_uint16]
+        lib.sqa_oracle_bf16_to_double.restype = ctypes.c_double
+        lib.sqa_oracle_bf16_to_double.argtypes = [ctypes.c_uint16]
         _LIB = lib
     return _LIB
 
@@ -63,17 +65,32 @@ def _as_np(x, dtype):
     return np.ascontiguousarray(np.asarray(x), dtype=dtype)
 
 
-def _strided_half(x):
-    """fp16 ``[P, page, Hkv, D]`` view (torch or numpy, any positive strides, contiguous D)
-    -> (numpy view, strides in elements)."""
+def _is_bf16(x):
+    return hasattr(x, "dtype") and str(x.dtype) == "torch.bfloat16"
+
+
+def _bits(x):
+    """Torch fp16/bf16 tensor -> numpy uint16 bit patterns (same strides); numpy fp16
+    arrays pass through."""
     if hasattr(x, "detach"):
         x = x.detach()
         if x.device.type != "cpu":
             x = x.cpu()
+        if _is_bf16(x):
+            import torch
+
+            return x.view(torch.int16).numpy().view(np.uint16)
         x = x.numpy()
     x = np.asarray(x)
-    if x.dtype != np.float16:
+    if x.dtype not in (np.float16, np.uint16):
         x = x.astype(np.float16)
+    return x
+
+
+def _strided_half(x):
+    """fp16/bf16 ``[P, page, Hkv, D]`` view (torch or numpy, any positive strides,
+    contiguous D) -> (numpy view of the 16-bit patterns, strides in elements)."""
+    x = _bits(x)
     if x.ndim != 4 or x.strides[3] != 2 or min(x.strides) <= 0:
         x = np.ascontiguousarray(x)
     return x, tuple(st // 2 for st in x.strides[:3])
@@ -89,7 +106,10 @@ def attention_c64(query, key_cache, value_cache, block_tables, seq_lens, page_si
     ``scale`` defaults to ``D**-0.5``; ``out_scale`` multiplies the output.
     """
     lib = _load()
-    q = _as_np(query, np.float16)
+    bf16 = _is_bf16(query)
+    if bf16 != _is_bf16(key_cache) or bf16 != _is_bf16(value_cache):
+        raise ValueError("query and caches must share the element type")
+    q = np.ascontiguousarray(_bits(query))
     k, kst = _strided_half(key_cache)
     v, vst = _strided_half(value_cache)
     bt = _as_np(block_tables, np.int32)
@@ -118,7 +138,7 @@ def attention_c64(query, key_cache, value_cache, block_tables, seq_lens, page_si
     rc = lib.sqa_oracle_f64_ex(
         ptr(q), ptr(k), ptr(v), kst[0], kst[1], kst[2], ptr(bt), ptr(sl),
         ptr(words) if words is not None else None, n_words,
-        float(dim ** -0.5 if scale is None else scale), float(out_scale), ptr(out),
+        float(dim ** -0.5 if scale is None else scale), float(out_scale), int(bf16), ptr(out),
         n_batch, q_len, n_qheads, num_kv_heads, dim, page_size, bt.shape[1], k.shape[0])
     if rc == -1:
         raise IndexError("block table holds a page id outside the cache")

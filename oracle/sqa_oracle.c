@@ -19,6 +19,7 @@
 #include <string.h>
 
 static double g_half_table[65536];
+static double g_bf16_table[65536];
 static int g_table_ready = 0;
 
 /* IEEE-754 binary16 bit pattern -> double. */
@@ -37,13 +38,25 @@ static double half_bits_to_double(uint16_t h) {
   return sign ? -v : v;
 }
 
+/* bfloat16 bit pattern -> double: the top half of an IEEE-754 binary32. */
+static double bf16_bits_to_double(uint16_t h) {
+  const uint32_t w = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &w, sizeof(f));
+  return (double)f;
+}
+
 static void build_table(void) {
   if (g_table_ready) return;
-  for (int i = 0; i < 65536; ++i) g_half_table[i] = half_bits_to_double((uint16_t)i);
+  for (int i = 0; i < 65536; ++i) {
+    g_half_table[i] = half_bits_to_double((uint16_t)i);
+    g_bf16_table[i] = bf16_bits_to_double((uint16_t)i);
+  }
   g_table_ready = 1;
 }
 
 double sqa_oracle_half_to_double(uint16_t bits) { return half_bits_to_double(bits); }
+double sqa_oracle_bf16_to_double(uint16_t bits) { return bf16_bits_to_double(bits); }
 
 /*
  * q:  [B, Q, Hq, D] fp16 bits;  out: [B, Q, Hq, D] double;  bt: [B, max_pages]
@@ -53,6 +66,7 @@ double sqa_oracle_half_to_double(uint16_t bits) { return half_bits_to_double(bit
  * draft chain, reference.py:63) or [B, Q, mask_words] uint32 words: row qi
  * sees t < sl - Q, and draft token j = t - (sl - Q) (t < sl) when bit j % 32 of
  * word j / 32 is set. Logits are scaled by `scale`, outputs by `out_scale`.
+ * q, kc, vc hold binary16 (bf16 == 0) or bfloat16 (bf16 != 0) bit patterns.
  * Rows that see no token are 0.
  * Returns 0, or -1 if a page id read by the computation lies outside
  * [0, num_pages), or -2 if a sequence needs more than max_pages pages.
@@ -60,10 +74,11 @@ double sqa_oracle_half_to_double(uint16_t bits) { return half_bits_to_double(bit
 int sqa_oracle_f64_ex(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                       long long ps, long long ts, long long hs,
                       const int32_t* bt, const int32_t* sl, const uint32_t* mask, int mask_words,
-                      double scale, double out_scale, double* out,
+                      double scale, double out_scale, int bf16, double* out,
                       int B, int Q, int Hq, int Hkv, int D, int page, int max_pages,
                       long long num_pages) {
   build_table();
+  const double* g_val = bf16 ? g_bf16_table : g_half_table;
   const int group = Hq / Hkv;
   const long long rows = (long long)B * Q * Hq;
 
@@ -117,14 +132,14 @@ int sqa_oracle_f64_ex(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
         for (int d = 0; d < D; ++d) o[d] = 0.0;
         continue;
       }
-      for (int d = 0; d < D; ++d) qv[d] = g_half_table[q[row * D + d]];
+      for (int d = 0; d < D; ++d) qv[d] = g_val[q[row * D + d]];
       double peak = -INFINITY;
       for (long long t = 0; t < len; ++t) {
         if (!seen[t]) continue;
         const long long pid = bt[(long long)b * max_pages + t / page];
         const uint16_t* kr = kc + pid * ps + (t % page) * ts + (long long)kvh * hs;
         double s = 0.0;
-        for (int d = 0; d < D; ++d) s += qv[d] * g_half_table[kr[d]];
+        for (int d = 0; d < D; ++d) s += qv[d] * g_val[kr[d]];
         s *= scale;
         logits[t] = s;
         if (s > peak) peak = s;
@@ -137,7 +152,7 @@ int sqa_oracle_f64_ex(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
         denom += w;
         const long long pid = bt[(long long)b * max_pages + t / page];
         const uint16_t* vr = vc + pid * ps + (t % page) * ts + (long long)kvh * hs;
-        for (int d = 0; d < D; ++d) acc[d] += w * g_half_table[vr[d]];
+        for (int d = 0; d < D; ++d) acc[d] += w * g_val[vr[d]];
       }
       for (int d = 0; d < D; ++d) o[d] = out_scale * acc[d] / denom;
     }
@@ -157,6 +172,6 @@ int sqa_oracle_f64(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                    long long num_pages) {
   const long long ts = (long long)Hkv * D;
   return sqa_oracle_f64_ex(q, kc, vc, (long long)page * ts, ts, D, bt, sl, NULL, 0,
-                           1.0 / sqrt((double)D), 1.0, out, B, Q, Hq, Hkv, D, page, max_pages,
+                           1.0 / sqrt((double)D), 1.0, 0, out, B, Q, Hq, Hkv, D, page, max_pages,
                            num_pages);
 }

@@ -15,11 +15,14 @@ import numpy as np
 
 
 def _np(x):
-    """Accept torch tensors or numpy arrays; returns a numpy view/copy on CPU."""
+    """Accept torch tensors or numpy arrays; returns a numpy view/copy on CPU
+    (bfloat16, which numpy lacks, is widened exactly to float32)."""
     if hasattr(x, "detach"):
         x = x.detach()
         if x.device.type != "cpu":
             x = x.cpu()
+        if str(x.dtype) == "torch.bfloat16":
+            x = x.float()
         return x.numpy()
     return np.asarray(x)
 

@@ -54,7 +54,10 @@ class AttentionArgs(ctypes.Structure):
                 ("head_dim", _C.c_int), ("page_size", _C.c_int), ("num_splits", _C.c_int),
                 ("pages_per_split", _C.c_int), ("workspace", _C.c_void_p),
                 ("workspace_bytes", _C.c_size_t), ("stream", _C.c_void_p),
-                ("timing_events", _C.c_void_p)]
+                ("timing_events", _C.c_void_p), ("dtype", _C.c_int)]
+
+
+DTYPE_F16, DTYPE_BF16 = 0, 1
 
 
 def library_path() -> Path:
@@ -177,6 +180,7 @@ def launch_general(query, output, k_view, v_view, block_tables, seq_lens, draft_
         a.workspace = workspace.data_ptr()
         a.workspace_bytes = workspace.numel() * workspace.element_size()
     a.stream = stream_handle
+    a.dtype = DTYPE_BF16 if str(query.dtype) == "torch.bfloat16" else DTYPE_F16
     ev = None
     if timing_events is not None:
         ev = (ctypes.c_void_p * 3)(*[ctypes.c_void_p(int(e)) for e in timing_events])
@@ -196,8 +200,13 @@ def run(query, key_cache, value_cache, block_tables, seq_lens, num_splits: int,
     b, q_len, hq, _ = query.shape
     nbytes = workspace_bytes(b, q_len, hq, key_cache.shape[2], num_splits, pages_per_split)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=query.device) if nbytes else None
-    launch(query, key_cache, value_cache, block_tables, seq_lens, out, ws, num_splits,
-           pages_per_split, raw_stream(query.device.index))
+    stream = raw_stream(query.device.index)
+    if query.dtype == torch.float16:
+        launch(query, key_cache, value_cache, block_tables, seq_lens, out, ws, num_splits,
+               pages_per_split, stream)
+    else:  # bf16: the general entry point carries the element type
+        launch_general(query, out, key_cache, value_cache, block_tables, seq_lens, None,
+                       query.shape[-1] ** -0.5, 1.0, num_splits, pages_per_split, ws, stream)
     return out
 
 

@@ -176,6 +176,9 @@ int run_attention(const sqa_attention_args& a) {
                 a.mask_words);
   if (!(a.scale > 0.f) || !isfinite(a.scale) || !isfinite(a.out_scale))
     return fail(SQA_ERR_INVALID, "scale must be positive and finite, out_scale finite");
+  if (a.dtype != SQA_DTYPE_F16 && a.dtype != SQA_DTYPE_BF16)
+    return fail(SQA_ERR_UNSUPPORTED, "dtype must be SQA_DTYPE_F16 or SQA_DTYPE_BF16 (got %d)",
+                a.dtype);
   if (num_splits <= 0 || pages_per_split < 0)
     return fail(SQA_ERR_INVALID, "num_splits must be positive and pages_per_split non-negative");
   if (pages_per_split > sqa::kMaxSplitPages)
@@ -242,6 +245,7 @@ int run_attention(const sqa_attention_args& a) {
   pa.num_splits = num_splits;
   pa.scale_log2 = (float)(1.4426950408889634 * (double)a.scale);
   pa.out_scale = a.out_scale;
+  pa.bf16 = a.dtype == SQA_DTYPE_BF16;
 
   hipError_t e;
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
@@ -264,6 +268,7 @@ int run_attention(const sqa_attention_args& a) {
     ma.pages_per_split = pages_per_split;
     ma.num_splits = num_splits;
     ma.out_scale = a.out_scale;
+    ma.bf16 = pa.bf16;
     if ((e = sqa::launch_merge(ma, s)) != hipSuccess) return hip_fail(e, "merge kernel launch");
   }
   if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");

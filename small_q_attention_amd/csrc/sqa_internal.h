@@ -57,6 +57,7 @@ struct PartialArgs {
   int pages_per_split, num_splits;
   float scale_log2;           // softmax scale * log2(e)
   float out_scale;            // multiplier applied to the normalised output
+  int bf16;                   // element type of Q, K, V and out: 0 fp16, 1 bf16
 };
 
 __host__ __device__ inline bool is_balanced(int pages_per_split) { return pages_per_split == 0; }
@@ -76,6 +77,7 @@ struct MergeArgs {
   int max_pages;  // kernel pages a block-table row addresses
   int pages_per_split, num_splits;
   float out_scale;
+  int bf16;
 };
 
 // Launch shape of the partial kernel for a given number of query rows per kv

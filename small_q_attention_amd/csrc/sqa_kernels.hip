@@ -40,6 +40,79 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef unsigned u4 __attribute__((ext_vector_type(4)));
 typedef unsigned u2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+
+// Element types of Q, K, V and the output. Operands travel as raw 16-bit
+// lanes (u4 = 8 elements, u2 = 4); the traits pick the MFMA and the rounding.
+struct ElemF16 {
+  // P goes into the PV product as one fp16 operand (relative error 2^-11).
+  static constexpr bool kSplitP = false;
+  // S^T += K . Q^T over 32 head dims.
+  static __device__ __forceinline__ f4 mma_qk(u4 k, u4 q, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, k),
+                                                  __builtin_bit_cast(h8, q), c, 0, 0, 0);
+  }
+  // O^T += V^T . P^T over 16 tokens.
+  static __device__ __forceinline__ f4 mma_pv(u2 v, u2 p, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, v),
+                                                 __builtin_bit_cast(h4, p), c, 0, 0, 0);
+  }
+  // Rounds four probabilities once; adds the rounded values to l (v_dot2
+  // against ones) so O stays an exact convex combination.
+  static __device__ __forceinline__ u2 round_p(float p0, float p1, float p2, float p3, float& l,
+                                               u2& /*lo*/) {
+    const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    const h2 lo = {(_Float16)p0, (_Float16)p1};
+    const h2 hi = {(_Float16)p2, (_Float16)p3};
+    l = __builtin_amdgcn_fdot2(hi, ones, __builtin_amdgcn_fdot2(lo, ones, l, false), false);
+    return __builtin_bit_cast(u2, h4{lo[0], lo[1], hi[0], hi[1]});
+  }
+  static __device__ __forceinline__ u4 pack8(const float (&x)[8]) {
+    h8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (_Float16)x[i];
+    return __builtin_bit_cast(u4, o);
+  }
+  static __device__ __forceinline__ unsigned pack2(float x, float y) {
+    return __builtin_bit_cast(unsigned, h2{(_Float16)x, (_Float16)y});
+  }
+};
+
+struct ElemBF16 {
+  // One bf16 P (relative error 2^-9) would cost up to ~1% on rows that average
+  // a few keys; P goes in as hi + lo bf16 parts (two PV products, ~2^-17).
+  static constexpr bool kSplitP = true;
+  static __device__ __forceinline__ f4 mma_qk(u4 k, u4 q, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, k),
+                                                   __builtin_bit_cast(b8, q), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f4 mma_pv(u2 v, u2 p, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, v),
+                                                     __builtin_bit_cast(s4, p), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ u2 round_p(float p0, float p1, float p2, float p3, float& l,
+                                               u2& lo) {
+    const b4 hi = {(__bf16)p0, (__bf16)p1, (__bf16)p2, (__bf16)p3};
+    const float h0 = (float)hi[0], h1 = (float)hi[1], h2v = (float)hi[2], h3 = (float)hi[3];
+    const b4 lw = {(__bf16)(p0 - h0), (__bf16)(p1 - h1), (__bf16)(p2 - h2v), (__bf16)(p3 - h3)};
+    l += ((h0 + (float)lw[0]) + (h1 + (float)lw[1])) + ((h2v + (float)lw[2]) + (h3 + (float)lw[3]));
+    lo = __builtin_bit_cast(u2, lw);
+    return __builtin_bit_cast(u2, hi);
+  }
+  static __device__ __forceinline__ u4 pack8(const float (&x)[8]) {
+    b8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (__bf16)x[i];
+    return __builtin_bit_cast(u4, o);
+  }
+  static __device__ __forceinline__ unsigned pack2(float x, float y) {
+    typedef __bf16 bb2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(unsigned, bb2{(__bf16)x, (__bf16)y});
+  }
+};
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -107,8 +180,8 @@ __device__ __forceinline__ unsigned pack_hi(unsigned a, unsigned b) {
 // Visibility on masked pages: token t < len is seen by a row when it lies
 // before the draft block (t < draft_base = len - q_len) or when bit
 // t - draft_base of the row's draft bits is set.
-template <int NB>
-__device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, const h8* sm_q,
+template <int NB, typename E>
+__device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, const u4* sm_q,
                                              int lane, const unsigned long long (&dbits)[NB],
                                              int draft_base, int tok0, int len, bool masked,
                                              float c) {
@@ -119,9 +192,8 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, co
     s[nb] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const h8 qf = sm_q[(nb * 4 + kk) * 64 + lane];
-      s[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, pg.k[kk]), qf, s[nb],
-                                                    0, 0, 0);
+      const u4 qf = sm_q[(nb * 4 + kk) * 64 + lane];
+      s[nb] = E::mma_qk(pg.k[kk], qf, s[nb]);
     }
   }
   if (masked) {
@@ -168,22 +240,15 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, co
     }
   }
 
-  // P = 2^(c*s - m), rounded once to fp16; the row sum is taken over the
-  // rounded values (v_dot2 against ones) so O is an exact convex combination.
-  h4 ph[NB];
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+  // P = 2^(c*s - m), rounded once to the element type; the row sum is taken
+  // over the rounded values so O is an exact convex combination.
+  u2 ph[NB], pl[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const float mu = st.m[nb] == -INFINITY ? 0.f : st.m[nb];
-    h2 lo, hi;
-    lo[0] = (_Float16)fast_exp2(fmaf(s[nb][0], c, -mu));
-    lo[1] = (_Float16)fast_exp2(fmaf(s[nb][1], c, -mu));
-    hi[0] = (_Float16)fast_exp2(fmaf(s[nb][2], c, -mu));
-    hi[1] = (_Float16)fast_exp2(fmaf(s[nb][3], c, -mu));
-    st.l[nb] = __builtin_amdgcn_fdot2(hi, ones, __builtin_amdgcn_fdot2(lo, ones, st.l[nb], false),
-                                      false);
-    ph[nb] = h4{lo[0], lo[1], hi[0], hi[1]};
+    ph[nb] = E::round_p(fast_exp2(fmaf(s[nb][0], c, -mu)), fast_exp2(fmaf(s[nb][1], c, -mu)),
+                        fast_exp2(fmaf(s[nb][2], c, -mu)), fast_exp2(fmaf(s[nb][3], c, -mu)),
+                        st.l[nb], pl[nb]);
   }
 
   // O^T += V^T . P^T, one 16x16x16 MFMA per (dim block, row block). Dim block
@@ -194,10 +259,10 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, co
     const unsigned w0 = pg.v[0][j], w1 = pg.v[1][j], w2 = pg.v[2][j], w3 = pg.v[3][j];
     const u2 av = (mb & 1) == 0 ? u2{pack_lo(w0, w1), pack_lo(w2, w3)}
                                 : u2{pack_hi(w0, w1), pack_hi(w2, w3)};
-    const h4 a = __builtin_bit_cast(h4, av);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      st.acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, ph[nb], st.acc[mb][nb], 0, 0, 0);
+      st.acc[mb][nb] = E::mma_pv(av, ph[nb], st.acc[mb][nb]);
+      if constexpr (E::kSplitP) st.acc[mb][nb] = E::mma_pv(av, pl[nb], st.acc[mb][nb]);
     }
   }
 }
@@ -332,7 +397,7 @@ __device__ ItemRange balanced_item(const PartialArgs& a, int item, int* sm) {
 // dispatch neighbours. Each wave keeps its own softmax state and writes its
 // own partial (or, with a single split, the output). Every K/V byte is read by
 // one wave only, so the loads are non-temporal.
-template <int NB, int D, int WW, int WPE>
+template <int NB, int D, int WW, int WPE, typename E>
 __global__ __launch_bounds__(WW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void sqa_partial_kernel(PartialArgs a) {
   const int lane = threadIdx.x & 63;
@@ -391,7 +456,7 @@ void sqa_partial_kernel(PartialArgs a) {
   // Second: Q fragments, the rest of the split's page ids and the first D
   // pages, all in flight at once (Q and ids first, so waiting for them leaves
   // the page loads outstanding).
-  h8 qreg[NB][4];
+  u4 qreg[NB][4];
   unsigned long long dbits[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -406,8 +471,8 @@ void sqa_partial_kernel(PartialArgs a) {
     const _Float16* qp = a.q + ((size_t)(b * a.q_len + qi) * a.hq + hh) * kHeadDim + 8 * g16;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const h8 x = *(const h8*)(qp + 32 * kk);
-      qreg[nb][kk] = real ? x : h8{0, 0, 0, 0, 0, 0, 0, 0};
+      const u4 x = *(const u4*)(qp + 32 * kk);
+      qreg[nb][kk] = real ? x : u4{0u, 0u, 0u, 0u};
     }
     // Draft bits of the row: bit j = sees draft token j (the caller's mask, or
     // the causal chain j <= qi).
@@ -475,9 +540,9 @@ void sqa_partial_kernel(PartialArgs a) {
   // and the split's page ids: ids of [p_begin, p_end) clamped into the pool,
   // then -1 for the ring's look-ahead. Waves read ids back a step ahead of
   // use, so no page waits on a block-table load from memory.
-  __shared__ h8 sm_q[WW * NB * 4 * 64];
+  __shared__ u4 sm_q[WW * NB * 4 * 64];
   __shared__ int sm_ids[kIdSlots * WW * 64];
-  h8* my_q = sm_q + wave * NB * 4 * 64;
+  u4* my_q = sm_q + wave * NB * 4 * 64;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
@@ -511,8 +576,8 @@ void sqa_partial_kernel(PartialArgs a) {
       if (ii < n_pages) {
         const int p = p_begin + ii;
         const bool masked = (p + 1) * kPageSize > mask_from;
-        process_page<NB>(st, ring[j], my_q, lane, dbits, mask_from, p * kPageSize + 4 * g16, len,
-                         masked, a.scale_log2);
+        process_page<NB, E>(st, ring[j], my_q, lane, dbits, mask_from, p * kPageSize + 4 * g16,
+                            len, masked, a.scale_log2);
       }
       const int pid = next_pid;
       next_pid = page_id(ii + D + 1);
@@ -539,10 +604,10 @@ void sqa_partial_kernel(PartialArgs a) {
           a.out + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * kHeadDim + 32 * g16;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        h8 o;
+        float o[8];
 #pragma unroll
-        for (int mb = 0; mb < 8; ++mb) o[mb] = (_Float16)(st.acc[mb][nb][rr] * inv);
-        *(h8*)(op + 8 * rr) = o;
+        for (int mb = 0; mb < 8; ++mb) o[mb] = st.acc[mb][nb][rr] * inv;
+        *(u4*)(op + 8 * rr) = E::pack8(o);
       }
     } else {
       const size_t pitem = ((size_t)(it.slot0 + split) * a.hkv + kvh) * a.rows + r;
@@ -574,7 +639,7 @@ void sqa_partial_kernel(PartialArgs a) {
 // eight loads in flight. G = 1 (a wave per row) suits a few splits per row,
 // G = 4 spreads many splits over the workgroup; the G partial sums and the
 // global max meet in LDS.
-template <int G>
+template <int G, typename E>
 __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   constexpr int kRowsPerWg = 4 / G;
   const int t = threadIdx.x;
@@ -678,11 +743,30 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   }
   if (skip) return;
   const float inv = den > 0.f ? a.out_scale / den : 0.f;
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  h2 o;
-  o[0] = (_Float16)(acc0 * inv);
-  o[1] = (_Float16)(acc1 * inv);
-  *(h2*)(a.out + (size_t)row * kHeadDim + 2 * lane) = o;
+  *(unsigned*)(a.out + (size_t)row * kHeadDim + 2 * lane) = E::pack2(acc0 * inv, acc1 * inv);
+}
+
+template <typename E>
+void launch_partial_as(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
+                       hipStream_t stream) {
+  if (sh.row_blocks == 1) {
+    hipLaunchKernelGGL((sqa_partial_kernel<1, 4, 4, 1, E>), grid, block, 0, stream, a);
+  } else if (sh.row_blocks == 2) {
+    hipLaunchKernelGGL((sqa_partial_kernel<2, 4, 4, 1, E>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((sqa_partial_kernel<4, 3, 4, 1, E>), grid, block, 0, stream, a);
+  }
+}
+
+template <typename E>
+void launch_merge_as(const MergeArgs& a, int per_row, hipStream_t stream) {
+  const int total = a.batch * a.q_len * a.hq;
+  if (per_row <= 32) {
+    hipLaunchKernelGGL((sqa_merge_kernel<1, E>), dim3((unsigned)((total + 3) / 4)), dim3(256), 0,
+                       stream, a);
+  } else {
+    hipLaunchKernelGGL((sqa_merge_kernel<4, E>), dim3((unsigned)total), dim3(256), 0, stream, a);
+  }
 }
 
 }  // namespace
@@ -692,29 +776,24 @@ hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
   const int head_groups = (a.hkv + sh.heads - 1) / sh.heads;
   const dim3 grid((unsigned)(plan_slots(a.batch, a.num_splits, a.pages_per_split) * head_groups));
   const dim3 block(sh.heads * 64);
-  if (sh.row_blocks == 1) {
-    hipLaunchKernelGGL((sqa_partial_kernel<1, 4, 4, 1>), grid, block, 0, stream, a);
-  } else if (sh.row_blocks == 2) {
-    hipLaunchKernelGGL((sqa_partial_kernel<2, 4, 4, 1>), grid, block, 0, stream, a);
-  } else {
-    hipLaunchKernelGGL((sqa_partial_kernel<4, 3, 4, 1>), grid, block, 0, stream, a);
-  }
+  if (a.bf16)
+    launch_partial_as<ElemBF16>(a, sh, grid, block, stream);
+  else
+    launch_partial_as<ElemF16>(a, sh, grid, block, stream);
   return hipGetLastError();
 }
 
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream) {
-  const int total = a.batch * a.q_len * a.hq;
   // A wave per row while the splits per row fit one pass of eight loads per
   // lane group; four waves per row beyond that. The balanced plan's split
   // count per sequence is known only on the device: use the batch average.
   const int per_row = is_balanced(a.pages_per_split)
                           ? (a.num_splits - a.batch + a.batch - 1) / a.batch
                           : a.num_splits;
-  if (per_row <= 32) {
-    hipLaunchKernelGGL(sqa_merge_kernel<1>, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, stream, a);
-  } else {
-    hipLaunchKernelGGL(sqa_merge_kernel<4>, dim3((unsigned)total), dim3(256), 0, stream, a);
-  }
+  if (a.bf16)
+    launch_merge_as<ElemBF16>(a, per_row, stream);
+  else
+    launch_merge_as<ElemF16>(a, per_row, stream);
   return hipGetLastError();
 }
 

@@ -108,8 +108,9 @@ def _gpu_present(torch) -> bool:
 
 
 def _check_python_contract(tag, query, key_cache, value_cache, block_tables, seq_lens,
-                           gqa4: bool):
-    """The reference's Python-side checks (``cuda.py:65-77,85-95,138-150,197-211``)."""
+                           gqa4: bool, allow_bf16: bool = False):
+    """The reference's Python-side checks (``cuda.py:65-77,85-95,138-150,197-211``).
+    ``allow_bf16`` (native entry only) also accepts Q/K/V all in bfloat16."""
     import torch
 
     if not _gpu_present(torch):
@@ -127,7 +128,10 @@ def _check_python_contract(tag, query, key_cache, value_cache, block_tables, seq
             raise ValueError(f"all {tag} inputs must be contiguous")
     half = torch.float16
     if query.dtype != half or key_cache.dtype != half or value_cache.dtype != half:
-        raise ValueError(f"{tag} requires FP16 Q/K/V")
+        bf = torch.bfloat16
+        if not (allow_bf16 and query.dtype == bf and key_cache.dtype == bf
+                and value_cache.dtype == bf):
+            raise ValueError(f"{tag} requires FP16 Q/K/V" + (" (or all BF16)" if allow_bf16 else ""))
     if query.ndim < 2 or query.shape[1] not in SUPPORTED_Q_LENS:
         raise ValueError(f"{tag} supports q_len 2, 4, 8 or 16")
     if query.shape[-1] != HEAD_DIM:
@@ -217,9 +221,11 @@ def paged_mtp_attention(query, key_cache, value_cache, block_tables, seq_lens,
     """Native entry: automatic split plan, no host sync unless ``max_seq_len < 0``.
 
     ``max_seq_len`` > 0 promises every ``seq_lens[b] <= max_seq_len``; 0 plans
-    over the whole block-table row.
+    over the whole block-table row. Q, K and V may also all be bfloat16 (the
+    ``forward_vN`` names keep the reference's fp16-only contract).
     """
-    _check_python_contract("sqa", query, key_cache, value_cache, block_tables, seq_lens, False)
+    _check_python_contract("sqa", query, key_cache, value_cache, block_tables, seq_lens, False,
+                           allow_bf16=True)
     if chunk_keys is not None and chunk_keys <= 0:
         raise ValueError("chunk_keys must be positive")
     _load()

@@ -5,7 +5,7 @@ The reference compares its kernels with four FlashInfer paths for the same op
 ``scripts/compare_flashinfer_paths.py:95-160``,
 ``scripts/probe_decode_wrapper_mtp.py``). This module offers the same call shapes,
 so code written against them runs here unchanged, within the contract of this
-build (fp16 Q/K/V, head_dim 128, pages of 16, 32 or 64 tokens,
+build (fp16 or bf16 Q/K/V, head_dim 128, pages of 16, 32 or 64 tokens,
 ``q_len * Hq / Hkv <= 64``):
 
 * :func:`xqa_batch_decode_with_kv_cache` — block table + seq_lens, interleaved
@@ -62,8 +62,8 @@ def _check_tensors(query, k, v, num_qo_heads: Optional[int] = None):
 
     if not query.is_cuda or not k.is_cuda:
         raise ValueError("query and kv_cache must be GPU tensors")
-    if query.dtype != torch.float16 or k.dtype != torch.float16:
-        raise ValueError("this build supports fp16 query and KV")
+    if query.dtype not in (torch.float16, torch.bfloat16) or k.dtype != query.dtype:
+        raise ValueError("this build supports fp16 or bf16 query and KV of the same type")
     if query.dim() != 3 or not query.is_contiguous():
         raise ValueError("query must be a contiguous [B * Q, Hq, D] tensor")
     if query.shape[-1] != HEAD_DIM or k.shape[-1] != HEAD_DIM:
@@ -216,9 +216,10 @@ class _PagedWrapper:
             raise ValueError("sliding windows are not supported (window_left must be -1)")
         if logits_soft_cap not in (None, 0, 0.0):
             raise ValueError("logits soft capping is not supported")
+        ok = (None, torch.float16, "float16", "fp16", torch.bfloat16, "bfloat16", "bf16")
         for dt in (q_data_type, kv_data_type):
-            if dt not in (None, torch.float16, "float16", "fp16"):
-                raise ValueError("this build supports fp16 query and KV")
+            if dt not in ok:
+                raise ValueError("this build supports fp16 or bf16 query and KV")
         if head_dim != HEAD_DIM or page_size not in PAGE_SIZES:
             raise ValueError("this build supports head_dim 128 and page_size 16, 32 or 64")
         if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:

@@ -14,13 +14,19 @@ TOL_REL = 1e-2
 
 
 def parity_stats(actual, ref64, batches=None):
-    """Compare a kernel output (torch fp16, any device) with a float64 oracle array."""
+    """Compare a kernel output (torch fp16 or bf16, any device) with a float64 oracle
+    array rounded to the output's type."""
+    import torch
+
     a = actual.detach().float().cpu().numpy().astype(np.float64)
     r = np.asarray(ref64, dtype=np.float64)
     if batches is not None:
         a = a[list(batches)]
         r = r[list(batches)]
-    r16 = r.astype(np.float16).astype(np.float64)
+    if actual.dtype == torch.bfloat16:
+        r16 = torch.from_numpy(r).to(torch.bfloat16).double().numpy()
+    else:
+        r16 = r.astype(np.float16).astype(np.float64)
     err16 = np.abs(a - r16)
     ok = bool(np.all(err16 <= TOL_ABS + TOL_REL * np.abs(r16)))
     return {

@@ -55,7 +55,7 @@ def test_wrappers_reject_unsupported_plans():
     for kw, match in ((dict(pos_encoding_mode="ROPE_LLAMA"), "pos_encoding"),
                       (dict(logits_soft_cap=30.0), "soft"),
                       (dict(window_left=64), "window"),
-                      (dict(q_data_type=torch.bfloat16), "fp16")):
+                      (dict(q_data_type=torch.float32), "fp16 or bf16")):
         with pytest.raises(ValueError, match=match):
             dec.plan(indptr, ids, last, 32, 8, 128, 16, **kw)
     with pytest.raises(ValueError, match="head_dim"):

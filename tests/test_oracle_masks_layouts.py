@@ -154,3 +154,44 @@ def test_csr_to_block_table():
     with pytest.raises(ValueError):
         csr_to_block_table(torch.tensor([0, 3, 2], dtype=torch.int32), indices[:3],
                            torch.tensor([1, 1], dtype=torch.int32))
+
+
+def test_bf16_decoding_matches_torch_on_every_pattern():
+    from oracle.cbrute import _load
+
+    lib = _load()
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    want = bits.view(torch.bfloat16).double().numpy()
+    got = np.array([lib.sqa_oracle_bf16_to_double(i) for i in range(65536)])
+    same = (got == want) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+
+
+def _bf16_case(lens, q_len, seed, exact_in_fp16=False):
+    q, k, v, bt, sl = _case(lens, q_len, seed)
+    if exact_in_fp16:
+        # Multiples of 1/8 in [-4, 4]: exactly representable in fp16 and in bf16.
+        q, k, v = ((t.float() * 8).round().clamp(-32, 32) / 8 for t in (q, k, v))
+    return q.bfloat16(), k.bfloat16(), v.bfloat16(), bt, sl
+
+
+def test_bf16_oracles_agree():
+    q, k, v, bt, sl = _bf16_case([9, 40, 300], 4, seed=21)
+    c = attention_c64(q, k, v, bt, sl, 16, 8)
+    n = attention_numpy(q, k, v, bt, sl, 16, 8)
+    assert np.allclose(c, n, rtol=0, atol=1e-12)
+    mask = spec_dec_mask(3, 4, "full")
+    c = attention_c64(q, k, v, bt, sl, 16, 8, draft_mask=mask)
+    n = attention_numpy(q, k, v, bt, sl, 16, 8, draft_mask=mask)
+    assert np.allclose(c, n, rtol=0, atol=1e-12)
+
+
+def test_bf16_and_fp16_paths_agree_on_shared_values():
+    """Values representable in both types: the bf16 and fp16 decodings must give the
+    same float64 result bit for bit."""
+    q, k, v, bt, sl = _bf16_case([33, 200], 8, seed=22, exact_in_fp16=True)
+    as_bf16 = attention_c64(q, k, v, bt, sl, 16, 8)
+    as_fp16 = attention_c64(q.half(), k.half(), v.half(), bt, sl, 16, 8)
+    assert np.array_equal(as_bf16, as_fp16)
+    with pytest.raises(ValueError, match="element type"):
+        attention_c64(q, k.half(), v.half(), bt, sl, 16, 8)
