@@ -285,6 +285,27 @@ def main():
         result["bf16"] = {"kernel_us": round(pb * 1e3, 2),
                           "kernel_frac": round(kvb / (pb * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
         del qb, kb, vb, outb, wsb
+        # fp16 queries over an OCP e4m3 cache of the same shape (half the KV bytes).
+        k8, v8 = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
+        out8 = torch.empty_like(q)
+        ws8 = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+
+        def fp8_call(ev=None):
+            _lib.launch_general(q, out8, k8, v8, bt, sl, None, case.head_dim ** -0.5, 1.0,
+                                plan[0], plan[1], ws8, handle, timing_events=ev)
+
+        for _ in range(args.warmup):
+            fp8_call()
+        kev = _events(torch, 3 * args.steps)
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            fp8_call([e.cuda_event for e in kev[3 * i:3 * i + 3]])
+        torch.cuda.synchronize()
+        p8 = statistics.mean(kev[3 * i].elapsed_time(kev[3 * i + 1]) for i in range(args.steps))
+        result["fp8_kv"] = {"kernel_us": round(p8 * 1e3, 2), "kv_bytes": kvb // 2,
+                            "kernel_frac": round(kvb / 2 / (p8 * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                            "speedup_vs_fp16_kv": round(part_ms / p8, 3)}
+        del k8, v8, out8, ws8
     if not args.no_per_q:
         # The other single-GPU BASELINE configs, same timing (extra fields only).
         others = {}

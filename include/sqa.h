@@ -34,9 +34,11 @@ extern "C" {
 #define SQA_ERR_WORKSPACE 3   /* workspace missing or too small */
 #define SQA_ERR_HIP 4         /* HIP runtime error (launch, device query) */
 
-/* Element types of sqa_attention_args.dtype (query, caches and output alike). */
+/* Element types of sqa_attention_args.dtype (query and output) and .kv_dtype
+ * (caches: the query's type, or OCP FP8 E4M3 bytes). */
 #define SQA_DTYPE_F16 0
 #define SQA_DTYPE_BF16 1
+#define SQA_DTYPE_FP8_E4M3 2
 
 /*
  * Chooses the split-KV decomposition.
@@ -127,9 +129,12 @@ typedef struct sqa_kv_cache {
  *               mask_words >= ceil(q_len / 32), at most 2.
  *   scale       softmax scale (> 0; the reference uses head_dim^-1/2).
  *   out_scale   multiplier of the normalised output (1 for plain attention).
- *   dtype       SQA_DTYPE_F16 (the reference's) or SQA_DTYPE_BF16 for query,
- *               caches and output; probabilities are rounded to the same type
- *               before the PV product, accumulation is fp32.
+ *   dtype       SQA_DTYPE_F16 (the reference's) or SQA_DTYPE_BF16 for query
+ *               and output; accumulation is fp32.
+ *   kv_dtype    dtype (caches of the query's type) or SQA_DTYPE_FP8_E4M3:
+ *               one byte per element (strides still count elements), widened
+ *               exactly to dtype in registers; per-tensor K / V scales go into
+ *               scale / out_scale.
  */
 typedef struct sqa_attention_args {
   size_t struct_size;
@@ -156,6 +161,7 @@ typedef struct sqa_attention_args {
   void* stream;
   void** timing_events;
   int dtype;
+  int kv_dtype;
 } sqa_attention_args;
 
 /*

@@ -38,12 +38,15 @@ def _load():
         lib.sqa_oracle_f64_ex.restype = ctypes.c_int
         lib.sqa_oracle_f64_ex.argtypes = (
             [ctypes.c_void_p] * 3 + [ctypes.c_longlong] * 3 + [ctypes.c_void_p] * 3
-            + [ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_int, ctypes.c_void_p]
+            + [ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_int, ctypes.c_int,
+               ctypes.c_void_p]
             + [ctypes.c_int] * 7 + [ctypes.c_longlong])
         lib.sqa_oracle_half_to_double.restype = ctypes.c_double
         lib.sqa_oracle_half_to_double.argtypes = [ctypes.c_uint16]
         lib.sqa_oracle_bf16_to_double.restype = ctypes.c_double
         lib.sqa_oracle_bf16_to_double.argtypes = [ctypes.c_uint16]
+        lib.sqa_oracle_fp8_to_double.restype = ctypes.c_double
+        lib.sqa_oracle_fp8_to_double.argtypes = [ctypes.c_uint8]
         _LIB = lib
     return _LIB
 
@@ -69,31 +72,38 @@ def _is_bf16(x):
     return hasattr(x, "dtype") and str(x.dtype) == "torch.bfloat16"
 
 
+def _is_fp8(x):
+    return hasattr(x, "dtype") and str(x.dtype) == "torch.float8_e4m3fn"
+
+
 def _bits(x):
-    """Torch fp16/bf16 tensor -> numpy uint16 bit patterns (same strides); numpy fp16
-    arrays pass through."""
+    """Torch fp16/bf16/e4m3 tensor -> numpy uint16 (uint8 for e4m3) bit patterns with
+    the same strides; numpy fp16 arrays pass through."""
     if hasattr(x, "detach"):
         x = x.detach()
         if x.device.type != "cpu":
             x = x.cpu()
-        if _is_bf16(x):
+        if _is_bf16(x) or _is_fp8(x):
             import torch
 
+            if _is_fp8(x):
+                return x.view(torch.uint8).numpy()
             return x.view(torch.int16).numpy().view(np.uint16)
         x = x.numpy()
     x = np.asarray(x)
-    if x.dtype not in (np.float16, np.uint16):
+    if x.dtype not in (np.float16, np.uint16, np.uint8):
         x = x.astype(np.float16)
     return x
 
 
 def _strided_half(x):
-    """fp16/bf16 ``[P, page, Hkv, D]`` view (torch or numpy, any positive strides,
-    contiguous D) -> (numpy view of the 16-bit patterns, strides in elements)."""
+    """fp16/bf16/e4m3 ``[P, page, Hkv, D]`` view (torch or numpy, any positive strides,
+    contiguous D) -> (numpy view of the bit patterns, strides in elements)."""
     x = _bits(x)
-    if x.ndim != 4 or x.strides[3] != 2 or min(x.strides) <= 0:
+    size = x.itemsize
+    if x.ndim != 4 or x.strides[3] != size or min(x.strides) <= 0:
         x = np.ascontiguousarray(x)
-    return x, tuple(st // 2 for st in x.strides[:3])
+    return x, tuple(st // size for st in x.strides[:3])
 
 
 def attention_c64(query, key_cache, value_cache, block_tables, seq_lens, page_size, num_kv_heads,
@@ -107,8 +117,12 @@ def attention_c64(query, key_cache, value_cache, block_tables, seq_lens, page_si
     """
     lib = _load()
     bf16 = _is_bf16(query)
-    if bf16 != _is_bf16(key_cache) or bf16 != _is_bf16(value_cache):
-        raise ValueError("query and caches must share the element type")
+    kv_fp8 = _is_fp8(key_cache)
+    if kv_fp8 != _is_fp8(value_cache):
+        raise ValueError("key and value caches must share the element type")
+    if not kv_fp8 and (bf16 != _is_bf16(key_cache) or bf16 != _is_bf16(value_cache)):
+        raise ValueError("query and caches must share the element type (or caches in e4m3)")
+    kv_elem = 2 if kv_fp8 else int(bf16)
     q = np.ascontiguousarray(_bits(query))
     k, kst = _strided_half(key_cache)
     v, vst = _strided_half(value_cache)
@@ -120,7 +134,7 @@ def attention_c64(query, key_cache, value_cache, block_tables, seq_lens, page_si
     if kst != vst:
         v = np.ascontiguousarray(v)
         k = np.ascontiguousarray(k)
-        kst = vst = tuple(st // 2 for st in k.strides[:3])
+        kst = vst = tuple(st // k.itemsize for st in k.strides[:3])
     words, n_words = None, 0
     if draft_mask is not None:
         m = draft_mask
@@ -138,7 +152,8 @@ def attention_c64(query, key_cache, value_cache, block_tables, seq_lens, page_si
     rc = lib.sqa_oracle_f64_ex(
         ptr(q), ptr(k), ptr(v), kst[0], kst[1], kst[2], ptr(bt), ptr(sl),
         ptr(words) if words is not None else None, n_words,
-        float(dim ** -0.5 if scale is None else scale), float(out_scale), int(bf16), ptr(out),
+        float(dim ** -0.5 if scale is None else scale), float(out_scale), int(bf16), kv_elem,
+        ptr(out),
         n_batch, q_len, n_qheads, num_kv_heads, dim, page_size, bt.shape[1], k.shape[0])
     if rc == -1:
         raise IndexError("block table holds a page id outside the cache")

@@ -20,6 +20,7 @@
 
 static double g_half_table[65536];
 static double g_bf16_table[65536];
+static double g_fp8_table[256];
 static int g_table_ready = 0;
 
 /* IEEE-754 binary16 bit pattern -> double. */
@@ -46,17 +47,43 @@ static double bf16_bits_to_double(uint16_t h) {
   return (double)f;
 }
 
+/* OCP FP8 E4M3 ("e4m3fn") byte -> double: 1 sign, 4 exponent (bias 7) and 3
+ * mantissa bits, subnormals at exponent 0, NaN at S.1111.111, no infinities. */
+static double fp8_e4m3_to_double(uint8_t h) {
+  const int sign = h >> 7;
+  const int expo = (h >> 3) & 15;
+  const int mant = h & 7;
+  double v;
+  if (expo == 15 && mant == 7) {
+    v = NAN;
+  } else if (expo == 0) {
+    v = ldexp((double)mant, -9);
+  } else {
+    v = ldexp((double)(mant | 8), expo - 10);
+  }
+  return sign ? -v : v;
+}
+
 static void build_table(void) {
   if (g_table_ready) return;
   for (int i = 0; i < 65536; ++i) {
     g_half_table[i] = half_bits_to_double((uint16_t)i);
     g_bf16_table[i] = bf16_bits_to_double((uint16_t)i);
   }
+  for (int i = 0; i < 256; ++i) g_fp8_table[i] = fp8_e4m3_to_double((uint8_t)i);
   g_table_ready = 1;
+}
+
+/* Element e of a K/V array of type kv_elem (0 binary16, 1 bfloat16, 2 e4m3). */
+static inline double kv_value(const void* base, long long e, int kv_elem) {
+  if (kv_elem == 2) return g_fp8_table[((const uint8_t*)base)[e]];
+  const uint16_t bits = ((const uint16_t*)base)[e];
+  return kv_elem == 1 ? g_bf16_table[bits] : g_half_table[bits];
 }
 
 double sqa_oracle_half_to_double(uint16_t bits) { return half_bits_to_double(bits); }
 double sqa_oracle_bf16_to_double(uint16_t bits) { return bf16_bits_to_double(bits); }
+double sqa_oracle_fp8_to_double(uint8_t bits) { return fp8_e4m3_to_double(bits); }
 
 /*
  * q:  [B, Q, Hq, D] fp16 bits;  out: [B, Q, Hq, D] double;  bt: [B, max_pages]
@@ -66,15 +93,17 @@ double sqa_oracle_bf16_to_double(uint16_t bits) { return bf16_bits_to_double(bit
  * draft chain, reference.py:63) or [B, Q, mask_words] uint32 words: row qi
  * sees t < sl - Q, and draft token j = t - (sl - Q) (t < sl) when bit j % 32 of
  * word j / 32 is set. Logits are scaled by `scale`, outputs by `out_scale`.
- * q, kc, vc hold binary16 (bf16 == 0) or bfloat16 (bf16 != 0) bit patterns.
+ * q holds binary16 (bf16 == 0) or bfloat16 (bf16 != 0) bit patterns; kc, vc
+ * hold elements of kv_elem (0 binary16, 1 bfloat16, 2 OCP e4m3 bytes), the
+ * strides counting elements.
  * Rows that see no token are 0.
  * Returns 0, or -1 if a page id read by the computation lies outside
  * [0, num_pages), or -2 if a sequence needs more than max_pages pages.
  */
-int sqa_oracle_f64_ex(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+int sqa_oracle_f64_ex(const uint16_t* q, const void* kc, const void* vc,
                       long long ps, long long ts, long long hs,
                       const int32_t* bt, const int32_t* sl, const uint32_t* mask, int mask_words,
-                      double scale, double out_scale, int bf16, double* out,
+                      double scale, double out_scale, int bf16, int kv_elem, double* out,
                       int B, int Q, int Hq, int Hkv, int D, int page, int max_pages,
                       long long num_pages) {
   build_table();
@@ -137,9 +166,9 @@ int sqa_oracle_f64_ex(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
       for (long long t = 0; t < len; ++t) {
         if (!seen[t]) continue;
         const long long pid = bt[(long long)b * max_pages + t / page];
-        const uint16_t* kr = kc + pid * ps + (t % page) * ts + (long long)kvh * hs;
+        const long long kr = pid * ps + (t % page) * ts + (long long)kvh * hs;
         double s = 0.0;
-        for (int d = 0; d < D; ++d) s += qv[d] * g_val[kr[d]];
+        for (int d = 0; d < D; ++d) s += qv[d] * kv_value(kc, kr + d, kv_elem);
         s *= scale;
         logits[t] = s;
         if (s > peak) peak = s;
@@ -151,8 +180,8 @@ int sqa_oracle_f64_ex(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
         const double w = exp(logits[t] - peak);
         denom += w;
         const long long pid = bt[(long long)b * max_pages + t / page];
-        const uint16_t* vr = vc + pid * ps + (t % page) * ts + (long long)kvh * hs;
-        for (int d = 0; d < D; ++d) acc[d] += w * g_val[vr[d]];
+        const long long vr = pid * ps + (t % page) * ts + (long long)kvh * hs;
+        for (int d = 0; d < D; ++d) acc[d] += w * kv_value(vc, vr + d, kv_elem);
       }
       for (int d = 0; d < D; ++d) o[d] = out_scale * acc[d] / denom;
     }
@@ -172,6 +201,6 @@ int sqa_oracle_f64(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                    long long num_pages) {
   const long long ts = (long long)Hkv * D;
   return sqa_oracle_f64_ex(q, kc, vc, (long long)page * ts, ts, D, bt, sl, NULL, 0,
-                           1.0 / sqrt((double)D), 1.0, 0, out, B, Q, Hq, Hkv, D, page, max_pages,
-                           num_pages);
+                           1.0 / sqrt((double)D), 1.0, 0, 0, out, B, Q, Hq, Hkv, D, page,
+                           max_pages, num_pages);
 }

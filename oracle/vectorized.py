@@ -21,7 +21,7 @@ def _np(x):
         x = x.detach()
         if x.device.type != "cpu":
             x = x.cpu()
-        if str(x.dtype) == "torch.bfloat16":
+        if str(x.dtype) in ("torch.bfloat16", "torch.float8_e4m3fn"):
             x = x.float()
         return x.numpy()
     return np.asarray(x)

@@ -54,10 +54,10 @@ class AttentionArgs(ctypes.Structure):
                 ("head_dim", _C.c_int), ("page_size", _C.c_int), ("num_splits", _C.c_int),
                 ("pages_per_split", _C.c_int), ("workspace", _C.c_void_p),
                 ("workspace_bytes", _C.c_size_t), ("stream", _C.c_void_p),
-                ("timing_events", _C.c_void_p), ("dtype", _C.c_int)]
+                ("timing_events", _C.c_void_p), ("dtype", _C.c_int), ("kv_dtype", _C.c_int)]
 
 
-DTYPE_F16, DTYPE_BF16 = 0, 1
+DTYPE_F16, DTYPE_BF16, DTYPE_FP8_E4M3 = 0, 1, 2
 
 
 def library_path() -> Path:
@@ -181,6 +181,7 @@ def launch_general(query, output, k_view, v_view, block_tables, seq_lens, draft_
         a.workspace_bytes = workspace.numel() * workspace.element_size()
     a.stream = stream_handle
     a.dtype = DTYPE_BF16 if str(query.dtype) == "torch.bfloat16" else DTYPE_F16
+    a.kv_dtype = DTYPE_FP8_E4M3 if str(k_view.dtype) == "torch.float8_e4m3fn" else a.dtype
     ev = None
     if timing_events is not None:
         ev = (ctypes.c_void_p * 3)(*[ctypes.c_void_p(int(e)) for e in timing_events])

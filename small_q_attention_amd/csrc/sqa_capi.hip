@@ -160,15 +160,25 @@ int run_attention(const sqa_attention_args& a) {
   const long long rows = (long long)q_len * group;
   if (rows > sqa::kMaxRows)
     return fail(SQA_ERR_UNSUPPORTED, "q_len * group = %lld exceeds %d", rows, sqa::kMaxRows);
-  // Cache layout: 16-byte aligned bases and strides (the kernel's 16-byte loads),
-  // and one page's K (or V) within 2 GiB of its base (32-bit buffer offsets).
+  if (a.dtype != SQA_DTYPE_F16 && a.dtype != SQA_DTYPE_BF16)
+    return fail(SQA_ERR_UNSUPPORTED, "dtype must be SQA_DTYPE_F16 or SQA_DTYPE_BF16 (got %d)",
+                a.dtype);
+  if (a.kv_dtype != a.dtype && a.kv_dtype != SQA_DTYPE_FP8_E4M3)
+    return fail(SQA_ERR_UNSUPPORTED, "kv_dtype must equal dtype or be SQA_DTYPE_FP8_E4M3 (got %d)",
+                a.kv_dtype);
+  const bool kv_fp8 = a.kv_dtype == SQA_DTYPE_FP8_E4M3;
+  const long long kv_bytes = kv_fp8 ? 1 : 2;
+  // Cache layout: 16-byte aligned bases, strides of whole 8-element groups (the
+  // kernel's 16- or 8-byte loads), and one kernel page's K (or V) within 2 GiB
+  // of its base (32-bit buffer offsets).
   const int64_t ps = a.kv.page_stride, ts = a.kv.token_stride, hs = a.kv.head_stride;
   if (ps < 0 || ts < 0 || hs < 0 || ps % 8 || ts % 8 || hs % 8)
     return fail(SQA_ERR_INVALID, "cache strides must be non-negative multiples of 8 elements");
   if (((uintptr_t)a.kv.k | (uintptr_t)a.kv.v) % 16)
     return fail(SQA_ERR_INVALID, "cache base pointers must be 16-byte aligned");
   const long long extent =
-      2LL * (((long long)(sqa::kPageSize - 1) * ts) + (long long)(num_kv_heads - 1) * hs + sqa::kHeadDim);
+      kv_bytes * ((long long)(sqa::kPageSize - 1) * ts + (long long)(num_kv_heads - 1) * hs +
+                  sqa::kHeadDim);
   if (extent > 0x7fffffffLL)
     return fail(SQA_ERR_INVALID, "one page of the cache spans more than 2 GiB");
   if (a.draft_mask && (a.mask_words < (q_len + 31) / 32 || a.mask_words > 2))
@@ -176,9 +186,6 @@ int run_attention(const sqa_attention_args& a) {
                 a.mask_words);
   if (!(a.scale > 0.f) || !isfinite(a.scale) || !isfinite(a.out_scale))
     return fail(SQA_ERR_INVALID, "scale must be positive and finite, out_scale finite");
-  if (a.dtype != SQA_DTYPE_F16 && a.dtype != SQA_DTYPE_BF16)
-    return fail(SQA_ERR_UNSUPPORTED, "dtype must be SQA_DTYPE_F16 or SQA_DTYPE_BF16 (got %d)",
-                a.dtype);
   if (num_splits <= 0 || pages_per_split < 0)
     return fail(SQA_ERR_INVALID, "num_splits must be positive and pages_per_split non-negative");
   if (pages_per_split > sqa::kMaxSplitPages)
@@ -228,9 +235,9 @@ int run_attention(const sqa_attention_args& a) {
   pa.part_ml = merged ? (float*)workspace + items * sqa::kHeadDim : nullptr;
   pa.seq_splits = balanced ? (sqa::SeqSplits*)(pa.part_ml + items * 2) : nullptr;
   pa.num_pages = num_pages;
-  pa.page_stride = 2LL * ps;
-  pa.token_stride = (unsigned)(2 * ts);
-  pa.head_stride = (unsigned)(2 * hs);
+  pa.page_stride = kv_bytes * ps;
+  pa.token_stride = (unsigned)(kv_bytes * ts);
+  pa.head_stride = (unsigned)(kv_bytes * hs);
   pa.page_extent = (unsigned)extent;
   pa.batch = batch;
   pa.q_len = q_len;
@@ -246,6 +253,7 @@ int run_attention(const sqa_attention_args& a) {
   pa.scale_log2 = (float)(1.4426950408889634 * (double)a.scale);
   pa.out_scale = a.out_scale;
   pa.bf16 = a.dtype == SQA_DTYPE_BF16;
+  pa.kv_fp8 = kv_fp8;
 
   hipError_t e;
   if (ev && (e = hipEventRecord(ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");

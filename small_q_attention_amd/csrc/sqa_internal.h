@@ -57,7 +57,8 @@ struct PartialArgs {
   int pages_per_split, num_splits;
   float scale_log2;           // softmax scale * log2(e)
   float out_scale;            // multiplier applied to the normalised output
-  int bf16;                   // element type of Q, K, V and out: 0 fp16, 1 bf16
+  int bf16;                   // element type of Q and out (and of K, V unless kv_fp8): 0 fp16, 1 bf16
+  int kv_fp8;                 // K and V hold OCP e4m3 bytes
 };
 
 __host__ __device__ inline bool is_balanced(int pages_per_split) { return pages_per_split == 0; }

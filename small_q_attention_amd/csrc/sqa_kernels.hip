@@ -79,6 +79,13 @@ struct ElemF16 {
   static __device__ __forceinline__ unsigned pack2(float x, float y) {
     return __builtin_bit_cast(unsigned, h2{(_Float16)x, (_Float16)y});
   }
+  // Eight OCP e4m3 values (bytes of w, low first) -> eight fp16 (exact).
+  static __device__ __forceinline__ u4 widen_fp8(u2 w) {
+    return u4{__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0], 1.f, false)),
+              __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0], 1.f, true)),
+              __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[1], 1.f, false)),
+              __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[1], 1.f, true))};
+  }
 };
 
 struct ElemBF16 {
@@ -112,6 +119,12 @@ struct ElemBF16 {
     typedef __bf16 bb2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(unsigned, bb2{(__bf16)x, (__bf16)y});
   }
+  static __device__ __forceinline__ u4 widen_fp8(u2 w) {
+    return u4{__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.f, false)),
+              __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.f, true)),
+              __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[1], 1.f, false)),
+              __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[1], 1.f, true))};
+  }
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -132,10 +145,71 @@ __device__ __forceinline__ float xor_sum(float x) {
   return x + __shfl_xor(x, 32);
 }
 
-// One page worth of registers: K (4 x 16 B) and V (4 x 16 B) per lane.
-struct PageRegs {
+// Buffer-resource word 3 for gfx9-family raw (untyped, 32-bit) accesses.
+constexpr int kBufferFlags = 0x00020000;
+// Cache-policy operand of the K/V buffer loads: non-temporal (read once).
+constexpr int kStreamAux = 2;
+
+// K/V storage. Per page a lane holds K for token l%16, dims 32*kk + 8*(l/16)
+// + 0..7 (kk = 0..3), and V for tokens 4*(l/16) + 0..3, dims 8*(l%16) + 0..7:
+// the same dims and tokens whatever the element width, so Q and the output
+// mapping never change. expand() hands the MFMAs 16-bit elements.
+// One page of K and V in the query's 16-bit type (what the MFMAs take).
+struct PageVals {
   u4 k[4];
   u4 v[4];
+};
+
+struct KvNative {  // the query's 16-bit type
+  static constexpr int kBytes = 2;
+  struct Regs {
+    u4 k[4];
+    u4 v[4];
+  };
+  static __device__ __forceinline__ void load(Regs& r, __amdgpu_buffer_rsrc_t kr,
+                                              __amdgpu_buffer_rsrc_t vr, unsigned k_lane,
+                                              unsigned v_lane, unsigned tok) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      r.k[kk] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * kk, 0, kStreamAux);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      r.v[e] = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane, e * tok, kStreamAux);
+  }
+  template <typename E>
+  static __device__ __forceinline__ void expand(const Regs& r, u4 (&k)[4], u4 (&v)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      k[i] = r.k[i];
+      v[i] = r.v[i];
+    }
+  }
+};
+
+struct KvFp8 {  // OCP e4m3 bytes, widened exactly to the query's type
+  static constexpr int kBytes = 1;
+  struct Regs {
+    u2 k[4];
+    u2 v[4];
+  };
+  static __device__ __forceinline__ void load(Regs& r, __amdgpu_buffer_rsrc_t kr,
+                                              __amdgpu_buffer_rsrc_t vr, unsigned k_lane,
+                                              unsigned v_lane, unsigned tok) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      r.k[kk] = __builtin_amdgcn_raw_buffer_load_b64(kr, k_lane + 32 * kk, 0, kStreamAux);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      r.v[e] = __builtin_amdgcn_raw_buffer_load_b64(vr, v_lane, e * tok, kStreamAux);
+  }
+  template <typename E>
+  static __device__ __forceinline__ void expand(const Regs& r, u4 (&k)[4], u4 (&v)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      k[i] = E::widen_fp8(r.k[i]);
+      v[i] = E::widen_fp8(r.v[i]);
+    }
+  }
 };
 
 template <int NB>
@@ -145,13 +219,9 @@ struct WaveState {
   float l[NB];     // partial row sum over this lane's tokens
 };
 
-// Buffer-resource word 3 for gfx9-family raw (untyped, 32-bit) accesses.
-constexpr int kBufferFlags = 0x00020000;
-// Cache-policy operand of the K/V buffer loads: non-temporal (read once).
-constexpr int kStreamAux = 2;
 // Padding of the LDS page-id table beyond the split's last page: covers the
 // ring's look-ahead (at most 2 * D + 1 entries past the end).
-constexpr int kIdPad = 16;
+constexpr int kIdPad = 32;
 
 __device__ __forceinline__ int clamp_page(int pid, long long num_pages) {
   return (pid >= 0 && (long long)pid < num_pages) ? pid : 0;
@@ -180,11 +250,14 @@ __device__ __forceinline__ unsigned pack_hi(unsigned a, unsigned b) {
 // Visibility on masked pages: token t < len is seen by a row when it lies
 // before the draft block (t < draft_base = len - q_len) or when bit
 // t - draft_base of the row's draft bits is set.
-template <int NB, typename E>
-__device__ __forceinline__ void process_page(WaveState<NB>& st, PageRegs& pg, const u4* sm_q,
+template <int NB, typename E, typename KV>
+__device__ __forceinline__ void process_page(WaveState<NB>& st, const typename KV::Regs& raw,
+                                             const u4* sm_q,
                                              int lane, const unsigned long long (&dbits)[NB],
                                              int draft_base, int tok0, int len, bool masked,
                                              float c) {
+  PageVals pg;
+  KV::template expand<E>(raw, pg.k, pg.v);
   // Raw scores S^T[token][row] = K . Q^T for this page.
   f4 s[NB];
 #pragma unroll
@@ -397,7 +470,7 @@ __device__ ItemRange balanced_item(const PartialArgs& a, int item, int* sm) {
 // dispatch neighbours. Each wave keeps its own softmax state and writes its
 // own partial (or, with a single split, the output). Every K/V byte is read by
 // one wave only, so the loads are non-temporal.
-template <int NB, int D, int WW, int WPE, typename E>
+template <int NB, int D, int WW, int WPE, typename E, typename KV>
 __global__ __launch_bounds__(WW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void sqa_partial_kernel(PartialArgs a) {
   const int lane = threadIdx.x & 63;
@@ -503,8 +576,8 @@ void sqa_partial_kernel(PartialArgs a) {
   // offsets below stay in one VGPR each for the whole loop.
   const int kvh_c = active ? kvh : 0;
   const unsigned tok_bytes = a.token_stride;
-  const unsigned k_lane = l16 * tok_bytes + kvh_c * a.head_stride + 16 * g16;
-  const unsigned v_lane = 4 * g16 * tok_bytes + kvh_c * a.head_stride + 16 * l16;
+  const unsigned k_lane = l16 * tok_bytes + kvh_c * a.head_stride + 8 * KV::kBytes * g16;
+  const unsigned v_lane = 4 * g16 * tok_bytes + kvh_c * a.head_stride + 8 * KV::kBytes * l16;
   // pid < 0 gives a zero-length resource: the loads return zeros without
   // touching memory, so every slot refill below is unconditional and the
   // compiler's wait counts stay exact (one page retires per step). K/V are
@@ -512,7 +585,7 @@ void sqa_partial_kernel(PartialArgs a) {
   // Kernel page p of the sequence is sub-page p & sub_mask of cache page
   // block_tables[b][p >> shift].
   const size_t sub_bytes = (size_t)kPageSize * tok_bytes;
-  auto load_page = [&](int pid, int p, PageRegs& pg) {
+  auto load_page = [&](int pid, int p, typename KV::Regs& pg) {
     const size_t off =
         pid >= 0 ? (size_t)pid * (size_t)a.page_stride + (size_t)(p & sub_mask) * sub_bytes : 0;
     const int nrec = pid >= 0 ? (int)a.page_extent : 0;
@@ -520,16 +593,11 @@ void sqa_partial_kernel(PartialArgs a) {
         (void*)((const char*)a.k + off), (short)0, nrec, kBufferFlags);
     const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)((const char*)a.v + off), (short)0, nrec, kBufferFlags);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      pg.k[kk] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * kk, 0, kStreamAux);
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      pg.v[e] = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane, e * tok_bytes, kStreamAux);
+    KV::load(pg, kr, vr, k_lane, v_lane, tok_bytes);
   };
   // Ring of D pages in flight: page i is processed from slot i % D, which is
   // then refilled with page i + D.
-  PageRegs ring[D];
+  typename KV::Regs ring[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {
     load_page(j < n_pages ? clamp_page(first_id[j], a.num_pages) : -1, p_begin + j, ring[j]);
@@ -576,8 +644,8 @@ void sqa_partial_kernel(PartialArgs a) {
       if (ii < n_pages) {
         const int p = p_begin + ii;
         const bool masked = (p + 1) * kPageSize > mask_from;
-        process_page<NB, E>(st, ring[j], my_q, lane, dbits, mask_from, p * kPageSize + 4 * g16,
-                            len, masked, a.scale_log2);
+        process_page<NB, E, KV>(st, ring[j], my_q, lane, dbits, mask_from,
+                                p * kPageSize + 4 * g16, len, masked, a.scale_log2);
       }
       const int pid = next_pid;
       next_pid = page_id(ii + D + 1);
@@ -746,15 +814,18 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   *(unsigned*)(a.out + (size_t)row * kHeadDim + 2 * lane) = E::pack2(acc0 * inv, acc1 * inv);
 }
 
-template <typename E>
+// Ring depth: 4 pages (3 at 64 rows, where the registers run out); fp8 pages
+// are half the bytes and half the registers, so twice as many stay in flight.
+template <typename E, typename KV>
 void launch_partial_as(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
                        hipStream_t stream) {
+  constexpr int R = KV::kBytes == 1 ? 2 : 1;
   if (sh.row_blocks == 1) {
-    hipLaunchKernelGGL((sqa_partial_kernel<1, 4, 4, 1, E>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((sqa_partial_kernel<1, 4 * R, 4, 1, E, KV>), grid, block, 0, stream, a);
   } else if (sh.row_blocks == 2) {
-    hipLaunchKernelGGL((sqa_partial_kernel<2, 4, 4, 1, E>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((sqa_partial_kernel<2, 4 * R, 4, 1, E, KV>), grid, block, 0, stream, a);
   } else {
-    hipLaunchKernelGGL((sqa_partial_kernel<4, 3, 4, 1, E>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((sqa_partial_kernel<4, 3 * R, 4, 1, E, KV>), grid, block, 0, stream, a);
   }
 }
 
@@ -776,10 +847,17 @@ hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
   const int head_groups = (a.hkv + sh.heads - 1) / sh.heads;
   const dim3 grid((unsigned)(plan_slots(a.batch, a.num_splits, a.pages_per_split) * head_groups));
   const dim3 block(sh.heads * 64);
-  if (a.bf16)
-    launch_partial_as<ElemBF16>(a, sh, grid, block, stream);
-  else
-    launch_partial_as<ElemF16>(a, sh, grid, block, stream);
+  if (a.bf16) {
+    if (a.kv_fp8)
+      launch_partial_as<ElemBF16, KvFp8>(a, sh, grid, block, stream);
+    else
+      launch_partial_as<ElemBF16, KvNative>(a, sh, grid, block, stream);
+  } else {
+    if (a.kv_fp8)
+      launch_partial_as<ElemF16, KvFp8>(a, sh, grid, block, stream);
+    else
+      launch_partial_as<ElemF16, KvNative>(a, sh, grid, block, stream);
+  }
   return hipGetLastError();
 }
 

@@ -5,8 +5,9 @@ The reference compares its kernels with four FlashInfer paths for the same op
 ``scripts/compare_flashinfer_paths.py:95-160``,
 ``scripts/probe_decode_wrapper_mtp.py``). This module offers the same call shapes,
 so code written against them runs here unchanged, within the contract of this
-build (fp16 or bf16 Q/K/V, head_dim 128, pages of 16, 32 or 64 tokens,
-``q_len * Hq / Hkv <= 64``):
+build (fp16 or bf16 Q, K/V of the same type or OCP FP8 E4M3
+(``torch.float8_e4m3fn``, K/V scales folded into ``bmm1_scale``/``bmm2_scale``),
+head_dim 128, pages of 16, 32 or 64 tokens, ``q_len * Hq / Hkv <= 64``):
 
 * :func:`xqa_batch_decode_with_kv_cache` — block table + seq_lens, interleaved
   ``[P, 2, 16, Hkv, D]`` ("NHD") or ``[P, 2, Hkv, 16, D]`` ("HND") cache or a
@@ -62,8 +63,13 @@ def _check_tensors(query, k, v, num_qo_heads: Optional[int] = None):
 
     if not query.is_cuda or not k.is_cuda:
         raise ValueError("query and kv_cache must be GPU tensors")
-    if query.dtype not in (torch.float16, torch.bfloat16) or k.dtype != query.dtype:
-        raise ValueError("this build supports fp16 or bf16 query and KV of the same type")
+    fp8 = getattr(torch, "float8_e4m3fn", None)
+    if query.dtype not in (torch.float16, torch.bfloat16) or (
+            k.dtype != query.dtype and (fp8 is None or k.dtype != fp8)):
+        raise ValueError("this build supports fp16 or bf16 query with KV of the same type or "
+                         "float8_e4m3fn")
+    if v.dtype != k.dtype:
+        raise ValueError("key and value caches must share the element type")
     if query.dim() != 3 or not query.is_contiguous():
         raise ValueError("query must be a contiguous [B * Q, Hq, D] tensor")
     if query.shape[-1] != HEAD_DIM or k.shape[-1] != HEAD_DIM:
@@ -217,9 +223,10 @@ class _PagedWrapper:
         if logits_soft_cap not in (None, 0, 0.0):
             raise ValueError("logits soft capping is not supported")
         ok = (None, torch.float16, "float16", "fp16", torch.bfloat16, "bfloat16", "bf16")
-        for dt in (q_data_type, kv_data_type):
-            if dt not in ok:
-                raise ValueError("this build supports fp16 or bf16 query and KV")
+        fp8 = (getattr(torch, "float8_e4m3fn", None), "float8_e4m3fn", "e4m3")
+        if q_data_type not in ok or kv_data_type not in ok + fp8:
+            raise ValueError("this build supports fp16 or bf16 query and KV "
+                             "(KV also float8_e4m3fn)")
         if head_dim != HEAD_DIM or page_size not in PAGE_SIZES:
             raise ValueError("this build supports head_dim 128 and page_size 16, 32 or 64")
         if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:

@@ -195,3 +195,39 @@ def test_bf16_and_fp16_paths_agree_on_shared_values():
     assert np.array_equal(as_bf16, as_fp16)
     with pytest.raises(ValueError, match="element type"):
         attention_c64(q, k.half(), v.half(), bt, sl, 16, 8)
+
+
+def test_fp8_decoding_matches_torch_on_every_pattern():
+    from oracle.cbrute import _load
+
+    lib = _load()
+    want = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn)
+    want = want.double().numpy()
+    got = np.array([lib.sqa_oracle_fp8_to_double(i) for i in range(256)])
+    same = (got == want) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+    assert got[0x7E] == 448.0 and got[0x01] == 2.0 ** -9 and np.isnan(got[0x7F])
+
+
+def _fp8_case(lens, q_len, seed):
+    q, k, v, bt, sl = _case(lens, q_len, seed)
+    return q, k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn), bt, sl
+
+
+def test_fp8_cache_oracle():
+    """e4m3 caches: every e4m3 value is exact in fp16, so the oracle on the e4m3 bytes
+    equals the oracle on the same values stored as fp16 (bit for bit), for fp16 and
+    bf16 queries; the numpy restatement agrees."""
+    q, k8, v8, bt, sl = _fp8_case([9, 70, 300], 8, seed=31)
+    k16, v16 = k8.to(torch.float16), v8.to(torch.float16)
+    assert torch.equal(k16.to(torch.float8_e4m3fn).view(torch.uint8), k8.view(torch.uint8))
+    a = attention_c64(q, k8, v8, bt, sl, 16, 8)
+    assert np.array_equal(a, attention_c64(q, k16, v16, bt, sl, 16, 8))
+    assert np.allclose(a, attention_numpy(q, k8, v8, bt, sl, 16, 8), rtol=0, atol=1e-12)
+    qb = q.bfloat16()
+    ab = attention_c64(qb, k8, v8, bt, sl, 16, 8, scale=0.05, out_scale=2.0)
+    assert np.array_equal(ab, attention_c64(qb, k16.bfloat16(), v16.bfloat16(), bt, sl, 16, 8,
+                                            scale=0.05, out_scale=2.0))
+    # Interleaved e4m3 cache read through strides.
+    kv = torch.stack([k8.view(torch.uint8), v8.view(torch.uint8)], 1).view(torch.float8_e4m3fn)
+    assert np.array_equal(attention_c64(q, kv[:, 0], kv[:, 1], bt, sl, 16, 8), a)
