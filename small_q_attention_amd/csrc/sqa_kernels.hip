@@ -150,10 +150,11 @@ constexpr int kBufferFlags = 0x00020000;
 // Cache-policy operand of the K/V buffer loads: non-temporal (read once).
 constexpr int kStreamAux = 2;
 
-// K/V storage. Per page a lane holds K for token l%16, dims 32*kk + 8*(l/16)
-// + 0..7 (kk = 0..3), and V for tokens 4*(l/16) + 0..3, dims 8*(l%16) + 0..7:
-// the same dims and tokens whatever the element width, so Q and the output
-// mapping never change. expand() hands the MFMAs 16-bit elements.
+// K/V storage. Per page a lane holds K for token l%16 and V for tokens
+// 4*(l/16) + 0..3, dims 8*(l%16) + 0..7. The head dims of K fragment kk are
+// q_dims(kk, l/16) + 0..7 (Q is loaded with the same map, so the QK contraction
+// is unchanged); V and the output mapping are the same for every storage type.
+// expand() hands the MFMAs 16-bit elements.
 // One page of K and V in the query's 16-bit type (what the MFMAs take).
 struct PageVals {
   u4 k[4];
@@ -162,6 +163,9 @@ struct PageVals {
 
 struct KvNative {  // the query's 16-bit type
   static constexpr int kBytes = 2;
+  // One 16-byte load per fragment: dims 32*kk + 8*g.
+  static __device__ __forceinline__ int q_dims(int kk, int g) { return 32 * kk + 8 * g; }
+  static __device__ __forceinline__ unsigned k_lane_bytes(int g) { return 16 * g; }
   struct Regs {
     u4 k[4];
     u4 v[4];
@@ -188,16 +192,24 @@ struct KvNative {  // the query's 16-bit type
 
 struct KvFp8 {  // OCP e4m3 bytes, widened exactly to the query's type
   static constexpr int kBytes = 1;
+  // K rows are 128 bytes: two 16-byte loads per lane (64 bytes of a row per
+  // instruction, as for the 16-bit types; 8-byte loads used 32 bytes per row
+  // request and ran at 58% of peak instead of 78%). Load i holds dims
+  // 64*i + 16*g + 0..15, i.e. fragments kk = 2i, 2i+1.
+  static __device__ __forceinline__ int q_dims(int kk, int g) {
+    return 64 * (kk >> 1) + 16 * g + 8 * (kk & 1);
+  }
+  static __device__ __forceinline__ unsigned k_lane_bytes(int g) { return 16 * g; }
   struct Regs {
-    u2 k[4];
+    u4 k[2];
     u2 v[4];
   };
   static __device__ __forceinline__ void load(Regs& r, __amdgpu_buffer_rsrc_t kr,
                                               __amdgpu_buffer_rsrc_t vr, unsigned k_lane,
                                               unsigned v_lane, unsigned tok) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      r.k[kk] = __builtin_amdgcn_raw_buffer_load_b64(kr, k_lane + 32 * kk, 0, kStreamAux);
+    for (int i = 0; i < 2; ++i)
+      r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * i, 0, kStreamAux);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       r.v[e] = __builtin_amdgcn_raw_buffer_load_b64(vr, v_lane, e * tok, kStreamAux);
@@ -205,10 +217,12 @@ struct KvFp8 {  // OCP e4m3 bytes, widened exactly to the query's type
   template <typename E>
   static __device__ __forceinline__ void expand(const Regs& r, u4 (&k)[4], u4 (&v)[4]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      k[i] = E::widen_fp8(r.k[i]);
-      v[i] = E::widen_fp8(r.v[i]);
+    for (int i = 0; i < 2; ++i) {
+      k[2 * i] = E::widen_fp8(u2{r.k[i][0], r.k[i][1]});
+      k[2 * i + 1] = E::widen_fp8(u2{r.k[i][2], r.k[i][3]});
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = E::widen_fp8(r.v[i]);
   }
 };
 
@@ -541,10 +555,10 @@ void sqa_partial_kernel(PartialArgs a) {
     const int qi = real ? r / a.group : 0;
     const int gg = real ? r - qi * a.group : 0;
     const int hh = real ? kvh * a.group + gg : 0;
-    const _Float16* qp = a.q + ((size_t)(b * a.q_len + qi) * a.hq + hh) * kHeadDim + 8 * g16;
+    const _Float16* qp = a.q + ((size_t)(b * a.q_len + qi) * a.hq + hh) * kHeadDim;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const u4 x = *(const u4*)(qp + 32 * kk);
+      const u4 x = *(const u4*)(qp + KV::q_dims(kk, g16));
       qreg[nb][kk] = real ? x : u4{0u, 0u, 0u, 0u};
     }
     // Draft bits of the row: bit j = sees draft token j (the caller's mask, or
@@ -576,7 +590,7 @@ void sqa_partial_kernel(PartialArgs a) {
   // offsets below stay in one VGPR each for the whole loop.
   const int kvh_c = active ? kvh : 0;
   const unsigned tok_bytes = a.token_stride;
-  const unsigned k_lane = l16 * tok_bytes + kvh_c * a.head_stride + 8 * KV::kBytes * g16;
+  const unsigned k_lane = l16 * tok_bytes + kvh_c * a.head_stride + KV::k_lane_bytes(g16);
   const unsigned v_lane = 4 * g16 * tok_bytes + kvh_c * a.head_stride + 8 * KV::kBytes * l16;
   // pid < 0 gives a zero-length resource: the loads return zeros without
   // touching memory, so every slot refill below is unconditional and the
