@@ -80,7 +80,8 @@ def time_calls(torch, lib, tensors, plan, steps, warmup):
     q, k, v, bt, sl = tensors
     num_splits, pps = plan
     out = torch.empty_like(q)
-    nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], num_splits, pps)
+    nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], q.shape[3],
+                                 num_splits, pps)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     stream = torch.cuda.current_stream()
     handle = stream.cuda_stream
@@ -106,7 +107,8 @@ def _ramp_clocks(torch, lib, tensors, plan, seconds=0.25):
     warmup steps (the first calls of a process otherwise run up to ~10% slow)."""
     q, k, v, bt, sl = tensors
     out = torch.empty_like(q)
-    nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], plan[0], plan[1])
+    nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], q.shape[3],
+                                 plan[0], plan[1])
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     handle = torch.cuda.current_stream().cuda_stream
     t0 = time.perf_counter()
@@ -266,7 +268,7 @@ def main():
         qb, kb, vb = q.bfloat16(), k.bfloat16(), v.bfloat16()
         outb = torch.empty_like(qb)
         nbytes = _lib.workspace_bytes(case.batch, case.q_len, case.num_query_heads,
-                                      case.num_kv_heads, plan[0], plan[1])
+                                      case.num_kv_heads, case.head_dim, plan[0], plan[1])
         wsb = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
         handle = torch.cuda.current_stream().cuda_stream
 

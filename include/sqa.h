@@ -64,12 +64,12 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
 
 /*
  * Device workspace bytes sqa_paged_mtp_attention needs for a plan from
- * sqa_plan_splits (0 for a fixed plan with num_splits == 1). Replaces the
+ * sqa_plan_splits and a head_dim (0 for a fixed plan with num_splits == 1). Replaces the
  * per-call torch::empty of the partial buffers in the reference launchers
  * (csrc/small_q_attention_ext.cu:1102-1104).
  */
 size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv_heads,
-                           int num_splits, int pages_per_split);
+                           int head_dim, int num_splits, int pages_per_split);
 
 /*
  * Runs the op asynchronously on `stream` (a hipStream_t; NULL = default stream).
@@ -78,7 +78,8 @@ size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv
  * :1380-1390). num_splits/pages_per_split come from sqa_plan_splits
  * (pages_per_split 0: balanced plan, batch <= 256 and num_splits >= batch +
  * max(1, ceil(batch * max_pages * page_size / 16 / 2048))); max_pages is the
- * block_tables row length. `workspace` must hold
+ * block_tables row length. head_dim is 128 (the reference's), 64 or 256;
+ * 256 needs q_len * num_query_heads / num_kv_heads <= 32. `workspace` must hold
  * sqa_workspace_bytes(...) bytes (may be NULL when that is 0). Allocates
  * nothing and never synchronises.
  * `timing_events`: NULL, or an array of 3 hipEvent_t recorded on `stream`
@@ -98,12 +99,12 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
  * h at slot t of page p is k[p * page_stride + t * token_stride + h *
  * head_stride + d] (V alike from v). Strides must be multiples of 8 elements
  * and k, v 16-byte aligned.
- *   separate caches [P, 16, Hkv, 128] (the reference's): k = key_cache,
- *     v = value_cache, page_stride 16*Hkv*128, token_stride Hkv*128, head_stride 128
- *   interleaved NHD [P, 2, 16, Hkv, 128]: k = kv, v = kv + 16*Hkv*128,
- *     page_stride 2*16*Hkv*128, token_stride Hkv*128, head_stride 128
- *   interleaved HND [P, 2, Hkv, 16, 128]: k = kv, v = kv + 16*Hkv*128,
- *     page_stride 2*16*Hkv*128, token_stride 128, head_stride 16*128
+ *   separate caches [P, 16, Hkv, D] (the reference's, D = 128): k = key_cache,
+ *     v = value_cache, page_stride 16*Hkv*D, token_stride Hkv*D, head_stride D
+ *   interleaved NHD [P, 2, 16, Hkv, D]: k = kv, v = kv + 16*Hkv*D,
+ *     page_stride 2*16*Hkv*D, token_stride Hkv*D, head_stride D
+ *   interleaved HND [P, 2, Hkv, 16, D]: k = kv, v = kv + 16*Hkv*D,
+ *     page_stride 2*16*Hkv*D, token_stride D, head_stride 16*D
  */
 typedef struct sqa_kv_cache {
   const void* k;

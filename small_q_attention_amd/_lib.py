@@ -23,7 +23,7 @@ _C = ctypes
 _SIGNATURES = [
     ("sqa_plan_splits", _C.c_int,
      [_C.c_int] * 8 + [_C.POINTER(_C.c_int), _C.POINTER(_C.c_int)]),
-    ("sqa_workspace_bytes", _C.c_size_t, [_C.c_int] * 6),
+    ("sqa_workspace_bytes", _C.c_size_t, [_C.c_int] * 7),
     ("sqa_paged_mtp_attention", _C.c_int,
      [_C.c_void_p] * 7 + [_C.c_size_t] + [_C.c_int] * 5 + [_C.c_int64] + [_C.c_int] * 4
      + [_C.c_void_p, _C.c_void_p]),
@@ -107,10 +107,10 @@ def plan_splits(device_index: int, batch: int, q_len: int, num_query_heads: int,
 
 @functools.lru_cache(maxsize=4096)
 def workspace_bytes(batch: int, q_len: int, num_query_heads: int, num_kv_heads: int,
-                    num_splits: int, pages_per_split: int) -> int:
+                    head_dim: int, num_splits: int, pages_per_split: int) -> int:
     """Workspace of a plan from :func:`plan_splits` (``pages_per_split`` 0 = balanced)."""
-    return int(load().sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, num_splits,
-                                          pages_per_split))
+    return int(load().sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, head_dim,
+                                          num_splits, pages_per_split))
 
 
 def raw_stream(device_index: int) -> int:
@@ -198,8 +198,8 @@ def run(query, key_cache, value_cache, block_tables, seq_lens, num_splits: int,
     import torch
 
     out = torch.empty_like(query)
-    b, q_len, hq, _ = query.shape
-    nbytes = workspace_bytes(b, q_len, hq, key_cache.shape[2], num_splits, pages_per_split)
+    b, q_len, hq, d = query.shape
+    nbytes = workspace_bytes(b, q_len, hq, key_cache.shape[2], d, num_splits, pages_per_split)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=query.device) if nbytes else None
     stream = raw_stream(query.device.index)
     if query.dtype == torch.float16:

@@ -114,15 +114,15 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
 }
 
 size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv_heads,
-                           int num_splits, int pages_per_split) {
-  if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_query_heads <= 0 || num_splits <= 0 ||
-      pages_per_split < 0)
+                           int head_dim, int num_splits, int pages_per_split) {
+  if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_query_heads <= 0 || head_dim <= 0 ||
+      num_splits <= 0 || pages_per_split < 0)
     return 0;
   const bool balanced = sqa::is_balanced(pages_per_split);
   if (!balanced && num_splits == 1) return 0;
   const size_t rows = (size_t)q_len * (num_query_heads / num_kv_heads);
   const size_t items = (size_t)sqa::plan_slots(batch, num_splits, pages_per_split) * num_kv_heads * rows;
-  size_t bytes = items * (sqa::kHeadDim + 2) * sizeof(float);
+  size_t bytes = items * ((size_t)head_dim + 2) * sizeof(float);
   if (balanced) bytes += (size_t)batch * sizeof(sqa::SeqSplits);
   return bytes;
 }
@@ -146,8 +146,8 @@ int run_attention(const sqa_attention_args& a) {
     return fail(SQA_ERR_INVALID, "empty KV cache is not supported");
   if (num_query_heads % num_kv_heads != 0)
     return fail(SQA_ERR_INVALID, "num_query_heads must be divisible by num_kv_heads");
-  if (head_dim != sqa::kHeadDim)
-    return fail(SQA_ERR_UNSUPPORTED, "head_dim must be %d (got %d)", sqa::kHeadDim, head_dim);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(SQA_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256 (got %d)", head_dim);
   int page_shift = -1;
   for (int sh = 0; sh <= sqa::kMaxPageShift; ++sh)
     if (page_size == (sqa::kPageSize << sh)) page_shift = sh;
@@ -158,8 +158,10 @@ int run_attention(const sqa_attention_args& a) {
   if (kernel_pages > 0x7fffffffLL) return fail(SQA_ERR_INVALID, "block table too wide");
   const int group = num_query_heads / num_kv_heads;
   const long long rows = (long long)q_len * group;
-  if (rows > sqa::kMaxRows)
-    return fail(SQA_ERR_UNSUPPORTED, "q_len * group = %lld exceeds %d", rows, sqa::kMaxRows);
+  const int max_rows = head_dim == 256 ? sqa::kMaxRowsHd256 : sqa::kMaxRows;
+  if (rows > max_rows)
+    return fail(SQA_ERR_UNSUPPORTED, "q_len * group = %lld exceeds %d at head_dim %d", rows,
+                max_rows, head_dim);
   if (a.dtype != SQA_DTYPE_F16 && a.dtype != SQA_DTYPE_BF16)
     return fail(SQA_ERR_UNSUPPORTED, "dtype must be SQA_DTYPE_F16 or SQA_DTYPE_BF16 (got %d)",
                 a.dtype);
@@ -178,7 +180,7 @@ int run_attention(const sqa_attention_args& a) {
     return fail(SQA_ERR_INVALID, "cache base pointers must be 16-byte aligned");
   const long long extent =
       kv_bytes * ((long long)(sqa::kPageSize - 1) * ts + (long long)(num_kv_heads - 1) * hs +
-                  sqa::kHeadDim);
+                  head_dim);
   if (extent > 0x7fffffffLL)
     return fail(SQA_ERR_INVALID, "one page of the cache spans more than 2 GiB");
   if (a.draft_mask && (a.mask_words < (q_len + 31) / 32 || a.mask_words > 2))
@@ -209,8 +211,8 @@ int run_attention(const sqa_attention_args& a) {
   // balanced plan processes every page up to seq_lens (clamped to max_pages).
   if (sqa::plan_slots(batch, num_splits, pages_per_split) * num_kv_heads > 0x7fffffffLL)
     return fail(SQA_ERR_INVALID, "grid too large");
-  const size_t need = sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, num_splits,
-                                          pages_per_split);
+  const size_t need = sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, head_dim,
+                                          num_splits, pages_per_split);
   if (need > 0 && (!a.workspace || a.workspace_bytes < need))
     return fail(SQA_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
                 a.workspace ? a.workspace_bytes : (size_t)0);
@@ -232,7 +234,7 @@ int run_attention(const sqa_attention_args& a) {
       (size_t)sqa::plan_slots(batch, num_splits, pages_per_split) * num_kv_heads * rows;
   const bool merged = balanced || num_splits > 1;
   pa.part_o = merged ? (float*)workspace : nullptr;
-  pa.part_ml = merged ? (float*)workspace + items * sqa::kHeadDim : nullptr;
+  pa.part_ml = merged ? (float*)workspace + items * head_dim : nullptr;
   pa.seq_splits = balanced ? (sqa::SeqSplits*)(pa.part_ml + items * 2) : nullptr;
   pa.num_pages = num_pages;
   pa.page_stride = kv_bytes * ps;
@@ -245,6 +247,7 @@ int run_attention(const sqa_attention_args& a) {
   pa.hkv = num_kv_heads;
   pa.group = group;
   pa.rows = (int)rows;
+  pa.head_dim = head_dim;
   pa.bt_stride = max_pages;
   pa.page_shift = page_shift;
   pa.max_pages = (int)kernel_pages;
@@ -272,6 +275,7 @@ int run_attention(const sqa_attention_args& a) {
     ma.hkv = num_kv_heads;
     ma.group = group;
     ma.rows = (int)rows;
+    ma.head_dim = head_dim;
     ma.max_pages = (int)kernel_pages;
     ma.pages_per_split = pages_per_split;
     ma.num_splits = num_splits;

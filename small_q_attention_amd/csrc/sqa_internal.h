@@ -7,7 +7,8 @@
 
 namespace sqa {
 
-constexpr int kHeadDim = 128;   // contract: head_dim 128
+constexpr int kHeadDim = 128;   // the reference's head_dim; 64 and 256 are also built
+constexpr int kMaxRowsHd256 = 32;  // head_dim 256: accumulators of at most two 16-row blocks
 constexpr int kPageSize = 16;   // kernel page: 16 tokens (one MFMA tile of keys)
 constexpr int kMaxPageShift = 2;  // cache pages of 16 << shift tokens: 16, 32, 64
 constexpr int kMaxRows = 64;    // q_len * (Hq / Hkv) rows one work item holds
@@ -34,14 +35,14 @@ struct SeqSplits {
 // (sequence, split) = first slot of the sequence + split; sequences whose
 // pages fit one split are written straight to the output.
 struct PartialArgs {
-  const _Float16* q;          // [B, Q, Hq, 128]
+  const _Float16* q;          // [B, Q, Hq, head_dim]
   const _Float16* k;          // K of page 0, slot 0, kv head 0
   const _Float16* v;          // V of page 0, slot 0, kv head 0
   const int32_t* block_tables;  // [B, bt_stride] cache-page ids
   const int32_t* seq_lens;      // [B]
   const uint32_t* draft_mask;   // NULL (causal draft chain) or [B, Q, mask_words]
-  _Float16* out;              // [B, Q, Hq, 128]; written directly when num_splits == 1
-  float* part_o;              // [slots, Hkv, rows, 128] unnormalised sums
+  _Float16* out;              // [B, Q, Hq, head_dim]; written directly when num_splits == 1
+  float* part_o;              // [slots, Hkv, rows, head_dim] unnormalised sums
   float* part_ml;             // [slots, Hkv, rows, 2] (max in log2 units, sum)
   SeqSplits* seq_splits;      // [B] (balanced plan only)
   long long num_pages;        // pages in the cache pool; ids outside are clamped to 0
@@ -51,6 +52,7 @@ struct PartialArgs {
   unsigned page_extent;       // bytes from a kernel page's base that its K (or V) spans
   int mask_words;             // 32-bit words per draft-mask row (1 or 2)
   int batch, q_len, hq, hkv, group, rows;
+  int head_dim;               // 64, 128 or 256
   int bt_stride;              // block_tables row length (cache pages)
   int page_shift;             // cache page = 16 << page_shift tokens = 1 << page_shift kernel pages
   int max_pages;              // kernel pages a block-table row addresses (bt_stride << page_shift)
@@ -75,6 +77,7 @@ struct MergeArgs {
   const int32_t* seq_lens;
   _Float16* out;
   int batch, q_len, hq, hkv, group, rows;
+  int head_dim;
   int max_pages;  // kernel pages a block-table row addresses
   int pages_per_split, num_splits;
   float out_scale;

@@ -27,7 +27,9 @@
 //     them with one byte permute per half pair: output block mb covers dims
 //     d = 8*m + mb, m = 0..15.
 // Rows beyond q_len*group (q_len*group not a multiple of 16) carry zero Q and
-// are never stored.
+// are never stored. The figures above are for head dim 128; the kernels are
+// also built for 64 and 256 (HD), where the per-lane counts scale with HD
+// (Dims<HD>) and a ring slot holds a page of HD-wide rows.
 #include "sqa_internal.h"
 
 #include <math.h>
@@ -79,6 +81,18 @@ struct ElemF16 {
   static __device__ __forceinline__ unsigned pack2(float x, float y) {
     return __builtin_bit_cast(unsigned, h2{(_Float16)x, (_Float16)y});
   }
+  static __device__ __forceinline__ u2 pack4(const float (&x)[4]) {
+    return __builtin_bit_cast(u2, h4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2],
+                                     (_Float16)x[3]});
+  }
+  static __device__ __forceinline__ unsigned short pack1(float x) {
+    return __builtin_bit_cast(unsigned short, (_Float16)x);
+  }
+  // Four OCP e4m3 values (bytes of w, low first) -> four fp16 (exact).
+  static __device__ __forceinline__ u2 widen_fp8x4(unsigned w) {
+    return u2{__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, false)),
+              __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, true))};
+  }
   // Eight OCP e4m3 values (bytes of w, low first) -> eight fp16 (exact).
   static __device__ __forceinline__ u4 widen_fp8(u2 w) {
     return u4{__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0], 1.f, false)),
@@ -119,6 +133,16 @@ struct ElemBF16 {
     typedef __bf16 bb2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(unsigned, bb2{(__bf16)x, (__bf16)y});
   }
+  static __device__ __forceinline__ u2 pack4(const float (&x)[4]) {
+    return __builtin_bit_cast(u2, b4{(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]});
+  }
+  static __device__ __forceinline__ unsigned short pack1(float x) {
+    return __builtin_bit_cast(unsigned short, (__bf16)x);
+  }
+  static __device__ __forceinline__ u2 widen_fp8x4(unsigned w) {
+    return u2{__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, false)),
+              __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, true))};
+  }
   static __device__ __forceinline__ u4 widen_fp8(u2 w) {
     return u4{__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.f, false)),
               __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.f, true)),
@@ -150,49 +174,79 @@ constexpr int kBufferFlags = 0x00020000;
 // Cache-policy operand of the K/V buffer loads: non-temporal (read once).
 constexpr int kStreamAux = 2;
 
-// K/V storage. Per page a lane holds K for token l%16 and V for tokens
-// 4*(l/16) + 0..3, dims 8*(l%16) + 0..7. The head dims of K fragment kk are
-// q_dims(kk, l/16) + 0..7 (Q is loaded with the same map, so the QK contraction
-// is unchanged); V and the output mapping are the same for every storage type.
-// expand() hands the MFMAs 16-bit elements.
-// One page of K and V in the query's 16-bit type (what the MFMAs take).
-struct PageVals {
-  u4 k[4];
-  u4 v[4];
+// Per-lane shapes for head dim HD (64, 128 or 256): KK = HD/32 K fragments of
+// 8 dims, MB = HD/16 output dim blocks, VW = HD/32 dwords of V per token (HD/16
+// dims of one token in 16-bit elements), each lane owning HD/4 output dims.
+template <int HD>
+struct Dims {
+  static constexpr int KK = HD / 32;
+  static constexpr int MB = HD / 16;
+  static constexpr int VW = HD / 32;
 };
 
+// K/V storage. Per page a lane holds K for token l%16 and V for tokens
+// 4*(l/16) + 0..3, dims (HD/16)*(l%16) + 0..HD/16-1. The head dims of K
+// fragment kk are q_dims(kk, l/16) + 0..7 (Q is loaded with the same map, so
+// the QK contraction is unchanged); V and the output mapping are the same for
+// every storage type. expand() hands the MFMAs 16-bit elements.
+// One page of K and V in the query's 16-bit type (what the MFMAs take).
+template <int HD>
+struct PageVals {
+  u4 k[Dims<HD>::KK];
+  unsigned v[4][Dims<HD>::VW];
+};
+
+template <int HD>
 struct KvNative {  // the query's 16-bit type
   static constexpr int kBytes = 2;
+  static constexpr int KK = Dims<HD>::KK, VW = Dims<HD>::VW;
   // One 16-byte load per fragment: dims 32*kk + 8*g.
   static __device__ __forceinline__ int q_dims(int kk, int g) { return 32 * kk + 8 * g; }
   static __device__ __forceinline__ unsigned k_lane_bytes(int g) { return 16 * g; }
+  static __device__ __forceinline__ unsigned v_lane_bytes(int l16) { return 4 * VW * l16; }
   struct Regs {
-    u4 k[4];
-    u4 v[4];
+    u4 k[KK];
+    unsigned v[4][VW];
   };
   static __device__ __forceinline__ void load(Regs& r, __amdgpu_buffer_rsrc_t kr,
                                               __amdgpu_buffer_rsrc_t vr, unsigned k_lane,
                                               unsigned v_lane, unsigned tok) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+    for (int kk = 0; kk < KK; ++kk)
       r.k[kk] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * kk, 0, kStreamAux);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      r.v[e] = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane, e * tok, kStreamAux);
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (VW == 2) {
+        const u2 x = __builtin_amdgcn_raw_buffer_load_b64(vr, v_lane, e * tok, kStreamAux);
+        r.v[e][0] = x[0];
+        r.v[e][1] = x[1];
+      } else {
+#pragma unroll
+        for (int h = 0; h < VW / 4; ++h) {
+          const u4 x = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane + 16 * h, e * tok,
+                                                             kStreamAux);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) r.v[e][4 * h + i] = x[i];
+        }
+      }
+    }
   }
   template <typename E>
-  static __device__ __forceinline__ void expand(const Regs& r, u4 (&k)[4], u4 (&v)[4]) {
+  static __device__ __forceinline__ void expand(const Regs& r, PageVals<HD>& pg) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      k[i] = r.k[i];
-      v[i] = r.v[i];
-    }
+    for (int i = 0; i < KK; ++i) pg.k[i] = r.k[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int i = 0; i < VW; ++i) pg.v[e][i] = r.v[e][i];
   }
 };
 
+template <int HD>
 struct KvFp8 {  // OCP e4m3 bytes, widened exactly to the query's type
   static constexpr int kBytes = 1;
-  // K rows are 128 bytes: two 16-byte loads per lane (64 bytes of a row per
+  static constexpr int KK = Dims<HD>::KK, VW = Dims<HD>::VW;
+  // K rows are HD bytes: 16-byte loads per lane (64 bytes of a row per
   // instruction, as for the 16-bit types; 8-byte loads used 32 bytes per row
   // request and ran at 58% of peak instead of 78%). Load i holds dims
   // 64*i + 16*g + 0..15, i.e. fragments kk = 2i, 2i+1.
@@ -200,42 +254,60 @@ struct KvFp8 {  // OCP e4m3 bytes, widened exactly to the query's type
     return 64 * (kk >> 1) + 16 * g + 8 * (kk & 1);
   }
   static __device__ __forceinline__ unsigned k_lane_bytes(int g) { return 16 * g; }
+  static __device__ __forceinline__ unsigned v_lane_bytes(int l16) { return 2 * VW * l16; }
   struct Regs {
-    u4 k[2];
-    u2 v[4];
+    u4 k[KK / 2];
+    unsigned v[4][VW / 2];  // HD/16 e4m3 bytes per token
   };
   static __device__ __forceinline__ void load(Regs& r, __amdgpu_buffer_rsrc_t kr,
                                               __amdgpu_buffer_rsrc_t vr, unsigned k_lane,
                                               unsigned v_lane, unsigned tok) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < KK / 2; ++i)
       r.k[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * i, 0, kStreamAux);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      r.v[e] = __builtin_amdgcn_raw_buffer_load_b64(vr, v_lane, e * tok, kStreamAux);
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (VW == 2) {
+        r.v[e][0] = __builtin_amdgcn_raw_buffer_load_b32(vr, v_lane, e * tok, kStreamAux);
+      } else if constexpr (VW == 4) {
+        const u2 x = __builtin_amdgcn_raw_buffer_load_b64(vr, v_lane, e * tok, kStreamAux);
+        r.v[e][0] = x[0];
+        r.v[e][1] = x[1];
+      } else {
+        const u4 x = __builtin_amdgcn_raw_buffer_load_b128(vr, v_lane, e * tok, kStreamAux);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.v[e][i] = x[i];
+      }
+    }
   }
   template <typename E>
-  static __device__ __forceinline__ void expand(const Regs& r, u4 (&k)[4], u4 (&v)[4]) {
+  static __device__ __forceinline__ void expand(const Regs& r, PageVals<HD>& pg) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      k[2 * i] = E::widen_fp8(u2{r.k[i][0], r.k[i][1]});
-      k[2 * i + 1] = E::widen_fp8(u2{r.k[i][2], r.k[i][3]});
+    for (int i = 0; i < KK / 2; ++i) {
+      pg.k[2 * i] = E::widen_fp8(u2{r.k[i][0], r.k[i][1]});
+      pg.k[2 * i + 1] = E::widen_fp8(u2{r.k[i][2], r.k[i][3]});
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = E::widen_fp8(r.v[i]);
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int i = 0; i < VW / 2; ++i) {
+        const u2 w = E::widen_fp8x4(r.v[e][i]);
+        pg.v[e][2 * i] = w[0];
+        pg.v[e][2 * i + 1] = w[1];
+      }
   }
 };
 
-template <int NB>
+template <int NB, int HD>
 struct WaveState {
-  f4 acc[8][NB];   // O^T blocks: lane l holds dims 32*(l/16)+8*r+mb of row 16*nb+l%16
+  f4 acc[Dims<HD>::MB][NB];  // O^T blocks: lane l holds dims (HD/4)*(l/16)+(HD/16)*r+mb of row 16*nb+l%16
   float m[NB];     // reference max (log2 units, within kMaxLag of the true row max), same in all 4 lane groups
   float l[NB];     // partial row sum over this lane's tokens
 };
 
 // Padding of the LDS page-id table beyond the split's last page: covers the
 // ring's look-ahead (at most 2 * D + 1 entries past the end).
-constexpr int kIdPad = 32;
+constexpr int kIdPad = 64;
 
 __device__ __forceinline__ int clamp_page(int pid, long long num_pages) {
   return (pid >= 0 && (long long)pid < num_pages) ? pid : 0;
@@ -264,22 +336,23 @@ __device__ __forceinline__ unsigned pack_hi(unsigned a, unsigned b) {
 // Visibility on masked pages: token t < len is seen by a row when it lies
 // before the draft block (t < draft_base = len - q_len) or when bit
 // t - draft_base of the row's draft bits is set.
-template <int NB, typename E, typename KV>
-__device__ __forceinline__ void process_page(WaveState<NB>& st, const typename KV::Regs& raw,
+template <int NB, int HD, typename E, typename KV>
+__device__ __forceinline__ void process_page(WaveState<NB, HD>& st, const typename KV::Regs& raw,
                                              const u4* sm_q,
                                              int lane, const unsigned long long (&dbits)[NB],
                                              int draft_base, int tok0, int len, bool masked,
                                              float c) {
-  PageVals pg;
-  KV::template expand<E>(raw, pg.k, pg.v);
+  constexpr int KK = Dims<HD>::KK, MB = Dims<HD>::MB, VW = Dims<HD>::VW;
+  PageVals<HD> pg;
+  KV::template expand<E>(raw, pg);
   // Raw scores S^T[token][row] = K . Q^T for this page.
   f4 s[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     s[nb] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const u4 qf = sm_q[(nb * 4 + kk) * 64 + lane];
+    for (int kk = 0; kk < KK; ++kk) {
+      const u4 qf = sm_q[(nb * KK + kk) * 64 + lane];
       s[nb] = E::mma_qk(pg.k[kk], qf, s[nb]);
     }
   }
@@ -302,7 +375,10 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, const typename K
     // poison the product, so zero them.
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      if (tok0 + e >= len) pg.v[e] = u4{0u, 0u, 0u, 0u};
+      if (tok0 + e >= len) {
+#pragma unroll
+        for (int i = 0; i < VW; ++i) pg.v[e][i] = 0u;
+      }
     }
   }
 
@@ -323,7 +399,7 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, const typename K
       st.m[nb] = mn;
       st.l[nb] *= alpha;
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) st.acc[mb][nb] *= alpha;
+      for (int mb = 0; mb < MB; ++mb) st.acc[mb][nb] *= alpha;
     }
   }
 
@@ -341,7 +417,7 @@ __device__ __forceinline__ void process_page(WaveState<NB>& st, const typename K
   // O^T += V^T . P^T, one 16x16x16 MFMA per (dim block, row block). Dim block
   // mb takes half mb%2 of dword mb/2 from the four token rows this lane holds.
 #pragma unroll
-  for (int mb = 0; mb < 8; ++mb) {
+  for (int mb = 0; mb < MB; ++mb) {
     const int j = mb >> 1;
     const unsigned w0 = pg.v[0][j], w1 = pg.v[1][j], w2 = pg.v[2][j], w3 = pg.v[3][j];
     const u2 av = (mb & 1) == 0 ? u2{pack_lo(w0, w1), pack_lo(w2, w3)}
@@ -484,9 +560,10 @@ __device__ ItemRange balanced_item(const PartialArgs& a, int item, int* sm) {
 // dispatch neighbours. Each wave keeps its own softmax state and writes its
 // own partial (or, with a single split, the output). Every K/V byte is read by
 // one wave only, so the loads are non-temporal.
-template <int NB, int D, int WW, int WPE, typename E, typename KV>
+template <int NB, int D, int WW, int WPE, int HD, typename E, typename KV>
 __global__ __launch_bounds__(WW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void sqa_partial_kernel(PartialArgs a) {
+  constexpr int KK = Dims<HD>::KK, MB = Dims<HD>::MB;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g16 = lane >> 4;
@@ -543,7 +620,7 @@ void sqa_partial_kernel(PartialArgs a) {
   // Second: Q fragments, the rest of the split's page ids and the first D
   // pages, all in flight at once (Q and ids first, so waiting for them leaves
   // the page loads outstanding).
-  u4 qreg[NB][4];
+  u4 qreg[NB][KK];
   unsigned long long dbits[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -555,9 +632,9 @@ void sqa_partial_kernel(PartialArgs a) {
     const int qi = real ? r / a.group : 0;
     const int gg = real ? r - qi * a.group : 0;
     const int hh = real ? kvh * a.group + gg : 0;
-    const _Float16* qp = a.q + ((size_t)(b * a.q_len + qi) * a.hq + hh) * kHeadDim;
+    const _Float16* qp = a.q + ((size_t)(b * a.q_len + qi) * a.hq + hh) * HD;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < KK; ++kk) {
       const u4 x = *(const u4*)(qp + KV::q_dims(kk, g16));
       qreg[nb][kk] = real ? x : u4{0u, 0u, 0u, 0u};
     }
@@ -591,7 +668,7 @@ void sqa_partial_kernel(PartialArgs a) {
   const int kvh_c = active ? kvh : 0;
   const unsigned tok_bytes = a.token_stride;
   const unsigned k_lane = l16 * tok_bytes + kvh_c * a.head_stride + KV::k_lane_bytes(g16);
-  const unsigned v_lane = 4 * g16 * tok_bytes + kvh_c * a.head_stride + 8 * KV::kBytes * l16;
+  const unsigned v_lane = 4 * g16 * tok_bytes + kvh_c * a.head_stride + KV::v_lane_bytes(l16);
   // pid < 0 gives a zero-length resource: the loads return zeros without
   // touching memory, so every slot refill below is unconditional and the
   // compiler's wait counts stay exact (one page retires per step). K/V are
@@ -622,13 +699,13 @@ void sqa_partial_kernel(PartialArgs a) {
   // and the split's page ids: ids of [p_begin, p_end) clamped into the pool,
   // then -1 for the ring's look-ahead. Waves read ids back a step ahead of
   // use, so no page waits on a block-table load from memory.
-  __shared__ u4 sm_q[WW * NB * 4 * 64];
+  __shared__ u4 sm_q[WW * NB * KK * 64];
   __shared__ int sm_ids[kIdSlots * WW * 64];
-  u4* my_q = sm_q + wave * NB * 4 * 64;
+  u4* my_q = sm_q + wave * NB * KK * 64;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) my_q[(nb * 4 + kk) * 64 + lane] = qreg[nb][kk];
+    for (int kk = 0; kk < KK; ++kk) my_q[(nb * KK + kk) * 64 + lane] = qreg[nb][kk];
   }
 #pragma unroll
   for (int k = 0; k < kIdSlots; ++k) {
@@ -639,13 +716,13 @@ void sqa_partial_kernel(PartialArgs a) {
   // Pages holding a token >= mask_from (draft block or past the end) are masked.
   const int mask_from = len - a.q_len;
 
-  WaveState<NB> st;
+  WaveState<NB, HD> st;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     st.m[nb] = -INFINITY;
     st.l[nb] = 0.f;
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) st.acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < MB; ++mb) st.acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
   }
 
   __syncthreads();  // sm_q and sm_ids written
@@ -658,8 +735,8 @@ void sqa_partial_kernel(PartialArgs a) {
       if (ii < n_pages) {
         const int p = p_begin + ii;
         const bool masked = (p + 1) * kPageSize > mask_from;
-        process_page<NB, E, KV>(st, ring[j], my_q, lane, dbits, mask_from,
-                                p * kPageSize + 4 * g16, len, masked, a.scale_log2);
+        process_page<NB, HD, E, KV>(st, ring[j], my_q, lane, dbits, mask_from,
+                                    p * kPageSize + 4 * g16, len, masked, a.scale_log2);
       }
       const int pid = next_pid;
       next_pid = page_id(ii + D + 1);
@@ -672,38 +749,47 @@ void sqa_partial_kernel(PartialArgs a) {
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) st.l[nb] = xor_sum(st.l[nb]);
 
-  // Lane l owns dims 32*g16 + 8*rr + mb (rr = 0..3, mb = 0..7) of row
-  // 16*nb + l16.
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int r = nb * 16 + l16;
     if (r >= a.rows) continue;
     const int qi = r / a.group;
     const int gg = r - qi * a.group;
+    // Lane l owns dims (HD/4)*g16 + MB*rr + mb (rr = 0..3, mb < MB = HD/16)
+    // of row 16*nb + l16: MB contiguous dims per rr.
     if (direct) {
       const float inv = st.l[nb] > 0.f ? a.out_scale / st.l[nb] : 0.f;
-      _Float16* op =
-          a.out + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * kHeadDim + 32 * g16;
+      _Float16* op = a.out + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * HD +
+                     (HD / 4) * g16;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        float o[8];
+        if constexpr (MB == 4) {
+          float o[4];
 #pragma unroll
-        for (int mb = 0; mb < 8; ++mb) o[mb] = st.acc[mb][nb][rr] * inv;
-        *(u4*)(op + 8 * rr) = E::pack8(o);
+          for (int mb = 0; mb < 4; ++mb) o[mb] = st.acc[mb][nb][rr] * inv;
+          *(u2*)(op + MB * rr) = E::pack4(o);
+        } else {
+#pragma unroll
+          for (int h = 0; h < MB / 8; ++h) {
+            float o[8];
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb) o[mb] = st.acc[8 * h + mb][nb][rr] * inv;
+            *(u4*)(op + MB * rr + 8 * h) = E::pack8(o);
+          }
+        }
       }
     } else {
       const size_t pitem = ((size_t)(it.slot0 + split) * a.hkv + kvh) * a.rows + r;
-      float* op = a.part_o + pitem * kHeadDim + 32 * g16;
+      float* op = a.part_o + pitem * HD + (HD / 4) * g16;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        f4 lo, hi;
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          lo[mb] = st.acc[mb][nb][rr];
-          hi[mb] = st.acc[mb + 4][nb][rr];
+        for (int h = 0; h < MB / 4; ++h) {
+          f4 o;
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) o[mb] = st.acc[4 * h + mb][nb][rr];
+          *(f4*)(op + MB * rr + 4 * h) = o;
         }
-        *(f4*)(op + 8 * rr) = lo;
-        *(f4*)(op + 8 * rr + 4) = hi;
       }
       if (g16 == 0) {
         a.part_ml[pitem * 2 + 0] = st.m[nb];
@@ -717,12 +803,13 @@ void sqa_partial_kernel(PartialArgs a) {
 // M = max_s m_s; O = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M); splits
 // with l_s <= 0 are skipped and a row with no visible key is written as 0.
 // A 256-thread workgroup merges 4 / G output rows; each row gets G waves and
-// wave g of a row sums dims 2*lane, +1 over the splits s = g (mod G) with
+// wave g of a row sums dims HD/64 * lane + 0.. over the splits s = g (mod G) with
 // eight loads in flight. G = 1 (a wave per row) suits a few splits per row,
 // G = 4 spreads many splits over the workgroup; the G partial sums and the
 // global max meet in LDS.
-template <int G, typename E>
+template <int G, int HD, typename E>
 __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
+  constexpr int DL = HD / 64;  // output dims per lane
   constexpr int kRowsPerWg = 4 / G;
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -757,10 +844,10 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   const size_t stride = (size_t)a.hkv * a.rows;  // items between consecutive splits of this row
   const size_t first = ((size_t)slot0 * a.hkv + kvh) * a.rows + r;
   const float* ml = a.part_ml + first * 2;
-  const float* po = a.part_o + first * kHeadDim + 2 * lane;
+  const float* po = a.part_o + first * HD + DL * lane;
 
   __shared__ float sm_red[4];
-  __shared__ float sm_acc[4][2 * 64 + 1];
+  __shared__ float sm_acc[4][HD + 1];
 
   // 1. M over the splits that hold a positive sum.
   float mx = -INFINITY;
@@ -776,18 +863,34 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
     for (int g = 0; g < G; ++g) mx = fmaxf(mx, sm_red[slot * G + g]);
   }
 
-  // 2. Weighted sums over this wave's splits.
-  float acc0 = 0.f, acc1 = 0.f, den = 0.f;
+  // 2. Weighted sums over this wave's splits (DL dims per lane).
+  auto load_o = [&](size_t it, float (&o)[DL]) {
+    const float* src = po + it * HD;
+    if constexpr (DL == 1) {
+      o[0] = src[0];
+    } else if constexpr (DL == 2) {
+      const float2 x = *(const float2*)src;
+      o[0] = x.x;
+      o[1] = x.y;
+    } else {
+      const f4 x = *(const f4*)src;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = x[i];
+    }
+  };
+  float acc[DL], den = 0.f;
+#pragma unroll
+  for (int i = 0; i < DL; ++i) acc[i] = 0.f;
   if (mx != -INFINITY) {
     constexpr int kUnroll = 8;
     int s = grp;
     for (; s + (kUnroll - 1) * G < n_valid; s += kUnroll * G) {
-      float2 o[kUnroll];
+      float o[kUnroll][DL];
       float m[kUnroll], l[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const size_t it = (size_t)(s + u * G) * stride;
-        o[u] = *(const float2*)(po + it * kHeadDim);
+        load_o(it, o[u]);
         m[u] = ml[it * 2];
         l[u] = ml[it * 2 + 1];
       }
@@ -795,63 +898,100 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
       for (int u = 0; u < kUnroll; ++u) {
         const float w = l[u] > 0.f ? fast_exp2(m[u] - mx) : 0.f;
         den += w * l[u];
-        acc0 += w * o[u].x;
-        acc1 += w * o[u].y;
+#pragma unroll
+        for (int i = 0; i < DL; ++i) acc[i] += w * o[u][i];
       }
     }
     for (; s < n_valid; s += G) {
       const size_t it = (size_t)s * stride;
       const float l = ml[it * 2 + 1];
       const float w = l > 0.f ? fast_exp2(ml[it * 2] - mx) : 0.f;
-      const float2 o = *(const float2*)(po + it * kHeadDim);
+      float o[DL];
+      load_o(it, o);
       den += w * l;
-      acc0 += w * o.x;
-      acc1 += w * o.y;
+#pragma unroll
+      for (int i = 0; i < DL; ++i) acc[i] += w * o[i];
     }
   }
   if (G > 1) {
-    sm_acc[wv][2 * lane] = acc0;
-    sm_acc[wv][2 * lane + 1] = acc1;
-    if (lane == 0) sm_acc[wv][128] = den;
+#pragma unroll
+    for (int i = 0; i < DL; ++i) sm_acc[wv][DL * lane + i] = acc[i];
+    if (lane == 0) sm_acc[wv][HD] = den;
     __syncthreads();
     if (grp != 0) return;
-    acc0 = acc1 = den = 0.f;
+    den = 0.f;
+#pragma unroll
+    for (int i = 0; i < DL; ++i) acc[i] = 0.f;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      den += sm_acc[slot * G + g][128];
-      acc0 += sm_acc[slot * G + g][2 * lane];
-      acc1 += sm_acc[slot * G + g][2 * lane + 1];
+      den += sm_acc[slot * G + g][HD];
+#pragma unroll
+      for (int i = 0; i < DL; ++i) acc[i] += sm_acc[slot * G + g][DL * lane + i];
     }
   }
   if (skip) return;
   const float inv = den > 0.f ? a.out_scale / den : 0.f;
-  *(unsigned*)(a.out + (size_t)row * kHeadDim + 2 * lane) = E::pack2(acc0 * inv, acc1 * inv);
+  _Float16* dst = a.out + (size_t)row * HD + DL * lane;
+  if constexpr (DL == 1) {
+    *(unsigned short*)dst = E::pack1(acc[0] * inv);
+  } else if constexpr (DL == 2) {
+    *(unsigned*)dst = E::pack2(acc[0] * inv, acc[1] * inv);
+  } else {
+    const float o[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+    *(u2*)dst = E::pack4(o);
+  }
 }
 
-// Ring depth: 4 pages (3 at 64 rows, where the registers run out); fp8 pages
-// are half the bytes and half the registers, so twice as many stay in flight.
-template <typename E, typename KV>
+// Ring depth: the pages in flight per wave hold about 32 KiB of K and V, 4
+// pages of 16-bit elements at head dim 128 (3 at 64 rows, where the registers
+// run out), proportionally more pages when a page holds fewer bytes (e4m3
+// caches, head dim 64) and fewer at head dim 256, which holds at most 32 rows
+// (its accumulators double).
+template <int HD, typename E, typename KV>
+void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
+                       hipStream_t stream) {
+  constexpr int kScale = (2 / KV::kBytes) * 128;  // 32 KiB / (16 * HD * kBytes * 2) * 4
+  constexpr int D4 = 4 * kScale / HD, D3 = 3 * kScale / HD;
+  if (sh.row_blocks == 1) {
+    hipLaunchKernelGGL((sqa_partial_kernel<1, D4, 4, 1, HD, E, KV>), grid, block, 0, stream, a);
+  } else if (sh.row_blocks == 2) {
+    hipLaunchKernelGGL((sqa_partial_kernel<2, D4, 4, 1, HD, E, KV>), grid, block, 0, stream, a);
+  } else if constexpr (HD != 256) {
+    hipLaunchKernelGGL((sqa_partial_kernel<4, D3, 4, 1, HD, E, KV>), grid, block, 0, stream, a);
+  }
+}
+
+template <typename E, template <int> class KV>
 void launch_partial_as(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
                        hipStream_t stream) {
-  constexpr int R = KV::kBytes == 1 ? 2 : 1;
-  if (sh.row_blocks == 1) {
-    hipLaunchKernelGGL((sqa_partial_kernel<1, 4 * R, 4, 1, E, KV>), grid, block, 0, stream, a);
-  } else if (sh.row_blocks == 2) {
-    hipLaunchKernelGGL((sqa_partial_kernel<2, 4 * R, 4, 1, E, KV>), grid, block, 0, stream, a);
+  if (a.head_dim == 64)
+    launch_partial_hd<64, E, KV<64>>(a, sh, grid, block, stream);
+  else if (a.head_dim == 256)
+    launch_partial_hd<256, E, KV<256>>(a, sh, grid, block, stream);
+  else
+    launch_partial_hd<128, E, KV<128>>(a, sh, grid, block, stream);
+}
+
+template <int HD, typename E>
+void launch_merge_hd(const MergeArgs& a, int per_row, hipStream_t stream) {
+  const int total = a.batch * a.q_len * a.hq;
+  if (per_row <= 32) {
+    hipLaunchKernelGGL((sqa_merge_kernel<1, HD, E>), dim3((unsigned)((total + 3) / 4)), dim3(256),
+                       0, stream, a);
   } else {
-    hipLaunchKernelGGL((sqa_partial_kernel<4, 3 * R, 4, 1, E, KV>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((sqa_merge_kernel<4, HD, E>), dim3((unsigned)total), dim3(256), 0, stream,
+                       a);
   }
 }
 
 template <typename E>
 void launch_merge_as(const MergeArgs& a, int per_row, hipStream_t stream) {
-  const int total = a.batch * a.q_len * a.hq;
-  if (per_row <= 32) {
-    hipLaunchKernelGGL((sqa_merge_kernel<1, E>), dim3((unsigned)((total + 3) / 4)), dim3(256), 0,
-                       stream, a);
-  } else {
-    hipLaunchKernelGGL((sqa_merge_kernel<4, E>), dim3((unsigned)total), dim3(256), 0, stream, a);
-  }
+  if (a.head_dim == 64)
+    launch_merge_hd<64, E>(a, per_row, stream);
+  else if (a.head_dim == 256)
+    launch_merge_hd<256, E>(a, per_row, stream);
+  else
+    launch_merge_hd<128, E>(a, per_row, stream);
 }
 
 }  // namespace

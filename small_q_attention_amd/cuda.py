@@ -20,7 +20,9 @@ Deliberate contract differences:
 * ``q_len`` 16 is accepted (the reference allows 2, 4, 8): ``q_len * group``
   must be at most 64 rows.
 * ``page_size`` must be 16, 32 or 64 and ``head_dim`` 128 (the reference's
-  launchers take any page size, but every reference caller uses 16).
+  launchers take any page size, but every reference caller uses 16). The
+  native entry :func:`paged_mtp_attention` also takes head_dim 64 and 256
+  (at most 32 rows at 256).
 * ``chunk_keys=None`` selects the automatic split plan (from the CU count).
 * ``token_group`` (v5) is validated and otherwise ignored: every draft row
   already shares one K/V load.
@@ -35,6 +37,7 @@ from . import _lib
 
 SUPPORTED_Q_LENS = (2, 4, 8, 16)
 HEAD_DIM = 128
+HEAD_DIMS = (64, 128, 256)  # native entry
 PAGE_SIZE = 16
 SUPPORTED_PAGE_SIZES = (16, 32, 64)
 MAX_ROWS = 64
@@ -108,9 +111,11 @@ def _gpu_present(torch) -> bool:
 
 
 def _check_python_contract(tag, query, key_cache, value_cache, block_tables, seq_lens,
-                           gqa4: bool, allow_bf16: bool = False):
+                           gqa4: bool, allow_bf16: bool = False,
+                           head_dims: tuple = (HEAD_DIM,)):
     """The reference's Python-side checks (``cuda.py:65-77,85-95,138-150,197-211``).
-    ``allow_bf16`` (native entry only) also accepts Q/K/V all in bfloat16."""
+    ``allow_bf16`` and ``head_dims`` (native entry only) also accept Q/K/V all in
+    bfloat16 and the other head dims of this build."""
     import torch
 
     if not _gpu_present(torch):
@@ -134,8 +139,8 @@ def _check_python_contract(tag, query, key_cache, value_cache, block_tables, seq
             raise ValueError(f"{tag} requires FP16 Q/K/V" + (" (or all BF16)" if allow_bf16 else ""))
     if query.ndim < 2 or query.shape[1] not in SUPPORTED_Q_LENS:
         raise ValueError(f"{tag} supports q_len 2, 4, 8 or 16")
-    if query.shape[-1] != HEAD_DIM:
-        raise ValueError(f"{tag} supports head_dim 128")
+    if query.shape[-1] not in head_dims:
+        raise ValueError(f"{tag} supports head_dim " + ", ".join(map(str, head_dims)))
     if gqa4:
         if (key_cache.ndim < 3 or query.ndim < 3 or key_cache.shape[2] == 0
                 or query.shape[2] % key_cache.shape[2] != 0
@@ -175,8 +180,9 @@ def _check_launcher_contract(query, key_cache, value_cache, block_tables, seq_le
         raise RuntimeError("batch must be positive")
     if cache_page not in SUPPORTED_PAGE_SIZES:
         raise ValueError("this build supports page_size 16, 32 or 64")
-    if q_len * (hq // hkv) > MAX_ROWS:
-        raise ValueError("q_len * (Hq / Hkv) must be at most 64")
+    rows_cap = 32 if dim == 256 else MAX_ROWS
+    if q_len * (hq // hkv) > rows_cap:
+        raise ValueError(f"q_len * (Hq / Hkv) must be at most {rows_cap} at head_dim {dim}")
 
 
 def _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
@@ -221,11 +227,12 @@ def paged_mtp_attention(query, key_cache, value_cache, block_tables, seq_lens,
     """Native entry: automatic split plan, no host sync unless ``max_seq_len < 0``.
 
     ``max_seq_len`` > 0 promises every ``seq_lens[b] <= max_seq_len``; 0 plans
-    over the whole block-table row. Q, K and V may also all be bfloat16 (the
-    ``forward_vN`` names keep the reference's fp16-only contract).
+    over the whole block-table row. Q, K and V may also all be bfloat16, and
+    head_dim 64 or 256 (the ``forward_vN`` names keep the reference's fp16,
+    head_dim 128 contract).
     """
     _check_python_contract("sqa", query, key_cache, value_cache, block_tables, seq_lens, False,
-                           allow_bf16=True)
+                           allow_bf16=True, head_dims=HEAD_DIMS)
     if chunk_keys is not None and chunk_keys <= 0:
         raise ValueError("chunk_keys must be positive")
     _load()

@@ -7,7 +7,8 @@ The reference compares its kernels with four FlashInfer paths for the same op
 so code written against them runs here unchanged, within the contract of this
 build (fp16 or bf16 Q, K/V of the same type or OCP FP8 E4M3
 (``torch.float8_e4m3fn``, K/V scales folded into ``bmm1_scale``/``bmm2_scale``),
-head_dim 128, pages of 16, 32 or 64 tokens, ``q_len * Hq / Hkv <= 64``):
+head_dim 64, 128 or 256, pages of 16, 32 or 64 tokens, ``q_len * Hq / Hkv <= 64``,
+at most 32 at head_dim 256):
 
 * :func:`xqa_batch_decode_with_kv_cache` — block table + seq_lens, interleaved
   ``[P, 2, 16, Hkv, D]`` ("NHD") or ``[P, 2, Hkv, 16, D]`` ("HND") cache or a
@@ -36,7 +37,12 @@ from .masks import as_words
 
 PAGE_SIZE = 16  # tokens per kernel page; cache pages hold 16, 32 or 64
 PAGE_SIZES = (16, 32, 64)
-HEAD_DIM = 128
+HEAD_DIMS = (64, 128, 256)
+
+
+def max_rows(head_dim: int) -> int:
+    """Most query rows (``q_len * Hq / Hkv``) one kv head may carry at ``head_dim``."""
+    return 32 if head_dim == 256 else 64
 
 
 def _kv_views(kv_cache, kv_layout: str):
@@ -72,8 +78,9 @@ def _check_tensors(query, k, v, num_qo_heads: Optional[int] = None):
         raise ValueError("key and value caches must share the element type")
     if query.dim() != 3 or not query.is_contiguous():
         raise ValueError("query must be a contiguous [B * Q, Hq, D] tensor")
-    if query.shape[-1] != HEAD_DIM or k.shape[-1] != HEAD_DIM:
-        raise ValueError("this build supports head_dim 128")
+    if query.shape[-1] not in HEAD_DIMS or k.shape[-1] != query.shape[-1]:
+        raise ValueError("this build supports head_dim 64, 128 or 256, equal for query and "
+                         "kv_cache")
     if k.shape[1] not in PAGE_SIZES:
         raise ValueError("this build supports page_size 16, 32 or 64")
     if num_qo_heads is not None and query.shape[1] != num_qo_heads:
@@ -92,12 +99,14 @@ def _run(query, k, v, block_tables, seq_lens, max_seq_len: int, q_len: int, scal
     hq, hkv = query.shape[1], k.shape[2]
     if hkv == 0 or hq % hkv:
         raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
-    if q_len * (hq // hkv) > 64:
-        raise ValueError("q_len_per_req * (Hq / Hkv) must be at most 64")
+    d = query.shape[-1]
+    if q_len * (hq // hkv) > max_rows(d):
+        raise ValueError(f"q_len_per_req * (Hq / Hkv) must be at most {max_rows(d)} at "
+                         f"head_dim {d}")
     if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32:
         raise ValueError("block_tables and seq_lens must be int32")
     words = None if mask is None else as_words(mask, batch, q_len)
-    q4 = query.view(batch, q_len, hq, HEAD_DIM)
+    q4 = query.view(batch, q_len, hq, d)
     if out is None:
         out = torch.empty_like(query)
     elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
@@ -106,7 +115,7 @@ def _run(query, k, v, block_tables, seq_lens, max_seq_len: int, q_len: int, scal
         plan = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv, int(max_seq_len),
                                 block_tables.shape[1] * (k.shape[1] // PAGE_SIZE), 0)
     ns, pps = plan
-    need = _lib.workspace_bytes(batch, q_len, hq, hkv, ns, pps)
+    need = _lib.workspace_bytes(batch, q_len, hq, hkv, d, ns, pps)
     ws = None
     if need:
         if workspace_buffer is None:
@@ -117,7 +126,7 @@ def _run(query, k, v, block_tables, seq_lens, max_seq_len: int, q_len: int, scal
                 raise ValueError(f"workspace_buffer must be contiguous and hold at least {need} "
                                  f"bytes for this batch (has {have})")
             ws = workspace_buffer
-    _lib.launch_general(q4, out.view(batch, q_len, hq, HEAD_DIM), k, v, block_tables, seq_lens,
+    _lib.launch_general(q4, out.view(batch, q_len, hq, d), k, v, block_tables, seq_lens,
                         words, scale, out_scale, ns, pps, ws,
                         _lib.raw_stream(query.device.index))
     return out
@@ -227,8 +236,9 @@ class _PagedWrapper:
         if q_data_type not in ok or kv_data_type not in ok + fp8:
             raise ValueError("this build supports fp16 or bf16 query and KV "
                              "(KV also float8_e4m3fn)")
-        if head_dim != HEAD_DIM or page_size not in PAGE_SIZES:
-            raise ValueError("this build supports head_dim 128 and page_size 16, 32 or 64")
+        if head_dim not in HEAD_DIMS or page_size not in PAGE_SIZES:
+            raise ValueError("this build supports head_dim 64, 128 or 256 and page_size 16, 32 "
+                             "or 64")
         if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
             raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
         block_tables, seq_lens = csr_to_block_table(indptr, indices, last_page_len, page_size)
@@ -237,7 +247,7 @@ class _PagedWrapper:
         plan = _lib.plan_splits(block_tables.device.index or 0, batch, q_len, num_qo_heads,
                                 num_kv_heads, max(max_seq_len, 1),
                                 block_tables.shape[1] * (page_size // PAGE_SIZE), 0)
-        need = _lib.workspace_bytes(batch, q_len, num_qo_heads, num_kv_heads, *plan)
+        need = _lib.workspace_bytes(batch, q_len, num_qo_heads, num_kv_heads, head_dim, *plan)
         if need and self._workspace is not None:
             have = self._workspace.numel() * self._workspace.element_size()
             if have < need:
@@ -246,8 +256,8 @@ class _PagedWrapper:
         self._planned = dict(block_tables=block_tables, seq_lens=seq_lens, plan=plan,
                              q_len=q_len, hq=num_qo_heads, hkv=num_kv_heads,
                              max_seq_len=max_seq_len, mask_words=mask_words,
-                             page_size=page_size,
-                             scale=HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale))
+                             page_size=page_size, head_dim=head_dim,
+                             scale=head_dim ** -0.5 if sm_scale is None else float(sm_scale))
 
     def run(self, q, paged_kv_cache, *_unused, out=None, **_kw):
         if self._planned is None:
@@ -257,6 +267,9 @@ class _PagedWrapper:
         _check_tensors(q, k, v, p["hq"])
         if k.shape[2] != p["hkv"]:
             raise ValueError(f"kv_cache has {k.shape[2]} kv heads, plan() was given {p['hkv']}")
+        if q.shape[-1] != p["head_dim"]:
+            raise ValueError(f"query has head_dim {q.shape[-1]}, plan() was given "
+                             f"{p['head_dim']}")
         if k.shape[1] != p["page_size"]:
             raise ValueError(f"kv_cache pages hold {k.shape[1]} tokens, plan() was given "
                              f"{p['page_size']}")

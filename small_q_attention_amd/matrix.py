@@ -114,7 +114,8 @@ def measure_case(torch, variant, case, page_mode, chunk_keys, warmup, repeats, s
     max_seq = case["kv_len"] if variant not in ("v0", "v1") else 0
     ns, pps = _lib.plan_splits(0, c.batch, c.q_len, c.num_query_heads, c.num_kv_heads, max_seq,
                                bt.shape[1], plan_ck)
-    nbytes = _lib.workspace_bytes(c.batch, c.q_len, c.num_query_heads, c.num_kv_heads, ns, pps)
+    nbytes = _lib.workspace_bytes(c.batch, c.q_len, c.num_query_heads, c.num_kv_heads,
+                                  c.head_dim, ns, pps)
     ws = torch.empty(max(1, nbytes), dtype=torch.uint8, device="cuda")
     outs = [torch.empty_like(s[0]) for s in sets]
     stream = torch.cuda.current_stream().cuda_stream

@@ -48,15 +48,19 @@ def test_version_and_empty_error(lib):
 
 def test_workspace_bytes(lib):
     # Fixed plan: rows = q_len * group; items = B * Hkv * splits * rows; 130 floats each.
-    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 1, 2048) == 0
-    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 16, 128) == 16 * 8 * 16 * 32 * 130 * 4
-    assert lib.sqa_workspace_bytes(1, 2, 32, 8, 3, 4) == 1 * 8 * 3 * 8 * 130 * 4
-    assert lib.sqa_workspace_bytes(0, 2, 32, 8, 3, 4) == 0
+    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 128, 1, 2048) == 0
+    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 128, 16, 128) == 16 * 8 * 16 * 32 * 130 * 4
+    assert lib.sqa_workspace_bytes(1, 2, 32, 8, 128, 3, 4) == 1 * 8 * 3 * 8 * 130 * 4
+    assert lib.sqa_workspace_bytes(0, 2, 32, 8, 128, 3, 4) == 0
     # Balanced plan (pages_per_split 0): num_splits slots shared by the batch,
     # plus one (first slot, count) pair of int32 per sequence.
-    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 272, 0) == 272 * 8 * 32 * 130 * 4 + 16 * 8
-    assert lib.sqa_workspace_bytes(2, 2, 32, 8, 1, 0) == 1 * 8 * 8 * 130 * 4 + 2 * 8
-    assert lib.sqa_workspace_bytes(2, 2, 32, 8, 3, -1) == 0
+    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 128, 272, 0) == 272 * 8 * 32 * 130 * 4 + 16 * 8
+    assert lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 1, 0) == 1 * 8 * 8 * 130 * 4 + 2 * 8
+    assert lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 3, -1) == 0
+    # Other head dims: head_dim + 2 floats per item.
+    assert lib.sqa_workspace_bytes(1, 2, 32, 8, 64, 3, 4) == 1 * 8 * 3 * 8 * 66 * 4
+    assert lib.sqa_workspace_bytes(1, 2, 32, 8, 256, 3, 4) == 1 * 8 * 3 * 8 * 258 * 4
+    assert lib.sqa_workspace_bytes(1, 2, 32, 8, 0, 3, 4) == 0
 
 
 def _plan(lib, **kw):
@@ -106,7 +110,10 @@ def _call(lib, **kw):
     (dict(batch=0), SQA_ERR_INVALID, "positive"),
     (dict(num_pages=0), SQA_ERR_INVALID, "empty"),
     (dict(hkv=5), SQA_ERR_INVALID, "divisible"),
-    (dict(dim=64), SQA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(dim=96), SQA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(dim=512), SQA_ERR_UNSUPPORTED, "head_dim"),
+    # head_dim 256 holds at most 32 rows per kv head.
+    (dict(dim=256, q_len=16), SQA_ERR_UNSUPPORTED, "exceeds 32 at head_dim 256"),
     (dict(page=24), SQA_ERR_UNSUPPORTED, "page_size"),
     (dict(page=128), SQA_ERR_UNSUPPORTED, "page_size"),
     # 64-token pages: the balanced plan's slot bound counts 16-token pages.
@@ -161,7 +168,7 @@ def _general(lib, **kw):
     (dict(draft_mask=16, mask_words=3), SQA_ERR_INVALID, "draft_mask"),
     (dict(scale=0.0), SQA_ERR_INVALID, "scale"),
     (dict(out_scale=float("inf")), SQA_ERR_INVALID, "out_scale"),
-    (dict(head_dim=64), SQA_ERR_UNSUPPORTED, "head_dim"),
+    (dict(head_dim=32), SQA_ERR_UNSUPPORTED, "head_dim"),
     (dict(num_splits=2), SQA_ERR_WORKSPACE, "workspace"),
 ])
 def test_general_entry_rejects_bad_arguments_without_a_gpu(lib, kw, code, msg):

@@ -59,7 +59,7 @@ def test_wrappers_reject_unsupported_plans():
         with pytest.raises(ValueError, match=match):
             dec.plan(indptr, ids, last, 32, 8, 128, 16, **kw)
     with pytest.raises(ValueError, match="head_dim"):
-        dec.plan(indptr, ids, last, 32, 8, 64, 16)
+        dec.plan(indptr, ids, last, 32, 8, 96, 16)
     pre = fi.BatchPrefillWithPagedKVCacheWrapper(None, "HND")
     with pytest.raises(ValueError, match="same query length"):
         pre.plan(torch.tensor([0, 2, 5], dtype=torch.int32), indptr, ids, last, 32, 8, 128, 16)

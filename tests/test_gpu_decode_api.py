@@ -102,7 +102,7 @@ def test_draft_masks(q_len):
         ns, pps = _lib.plan_splits(0, B, q_len, 32, 8, max(lens), bt.shape[1], ck)
         out = torch.empty_like(q)
         words = torch.from_numpy(tree.numpy().view(np.int32)).cuda()
-        wsb = torch.empty(max(1, _lib.workspace_bytes(B, q_len, 32, 8, ns, pps)),
+        wsb = torch.empty(max(1, _lib.workspace_bytes(B, q_len, 32, 8, 128, ns, pps)),
                           dtype=torch.uint8, device="cuda")
         _lib.launch_general(q, out, nhd[:, 0], nhd[:, 1], bt, sl, words, 128 ** -0.5, 1.0, ns,
                             pps, wsb, torch.cuda.current_stream().cuda_stream)

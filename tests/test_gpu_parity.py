@@ -276,7 +276,7 @@ def test_c_abi_direct_with_caller_workspace():
     q, k, v, bt, sl = tensors
     ns, pps = _lib.plan_splits(0, 3, 4, 32, 8, 1500, bt.shape[1], 256)
     assert ns > 1
-    ws = torch.empty(_lib.workspace_bytes(3, 4, 32, 8, ns, pps), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(_lib.workspace_bytes(3, 4, 32, 8, 128, ns, pps), dtype=torch.uint8, device="cuda")
     out = torch.empty_like(q)
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     for e in evs:

@@ -270,6 +270,22 @@ def test_three_oracles_agree_at_contract_shape():
     np.testing.assert_allclose(loop, c64, atol=5e-6)
 
 
+@pytest.mark.parametrize("head_dim", [64, 256])
+def test_three_oracles_agree_at_other_head_dims(head_dim):
+    """The head dims the kernels also build: the restatements take D from the shapes,
+    and the default scale follows it (D^-1/2)."""
+    from small_q_attention_amd import inputs
+
+    case = inputs.Case(batch=2, q_len=4, seq_lens=[37, 6], seed=15, head_dim=head_dim)
+    q, kc, vc, bt, sl = inputs.make_inputs(case)
+    loop, vec = _all_oracles(q, kc, vc, bt, sl, 16, 8)
+    c64 = attention_c64(q, kc, vc, bt, sl, 16, 8)
+    np.testing.assert_allclose(vec, c64, atol=1e-12)
+    np.testing.assert_allclose(loop, c64, atol=5e-6)
+    explicit = attention_c64(q, kc, vc, bt, sl, 16, 8, scale=head_dim ** -0.5)
+    np.testing.assert_array_equal(explicit, c64)
+
+
 def test_c_oracle_rows_without_keys_are_zero_and_bad_ids_raise():
     q, kc, vc, bt, sl = _rand_case(14, batch=1, q_len=4, lens=(2,))
     out = attention_c64(q, kc, vc, bt, torch.tensor([2], dtype=torch.int32), 4, 2)
