@@ -31,7 +31,7 @@ extern "C" {
 #define SQA_OK 0
 #define SQA_ERR_INVALID 1     /* bad argument (shape, null pointer, ...) */
 #define SQA_ERR_UNSUPPORTED 2 /* outside the supported contract (head_dim, page size, rows) */
-#define SQA_ERR_WORKSPACE 3   /* workspace missing or too small */
+#define SQA_ERR_WORKSPACE 3   /* workspace missing, too small or not 16-byte aligned */
 #define SQA_ERR_HIP 4         /* HIP runtime error (launch, device query) */
 
 /* Element types of sqa_attention_args.dtype (query and output) and .kv_dtype
@@ -80,7 +80,7 @@ size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv
  * max(1, ceil(batch * max_pages * page_size / 16 / 2048))); max_pages is the
  * block_tables row length. head_dim is 128 (the reference's), 64 or 256;
  * 256 needs q_len * num_query_heads / num_kv_heads <= 32. `workspace` must hold
- * sqa_workspace_bytes(...) bytes (may be NULL when that is 0). Allocates
+ * sqa_workspace_bytes(...) bytes, 16-byte aligned (may be NULL when that is 0). Allocates
  * nothing and never synchronises.
  * `timing_events`: NULL, or an array of 3 hipEvent_t recorded on `stream`
  * before the partial kernel, between the two kernels and after the merge

@@ -99,7 +99,11 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
     }
     const long long splits = ceil_div(slots_target, batch);
     pps = ceil_div(pages, splits);
-    if (pps < sqa::kMinSplitPages) pps = sqa::kMinSplitPages;
+    // Each split writes rows x (head_dim + 2) floats per kv head for the merge;
+    // past 16 rows that rivals a 4-page split's K/V bytes, so splits start at
+    // 8 pages there (single-sequence batches of a few thousand tokens).
+    const long long min_pps = sh.row_blocks > 1 ? 2 * sqa::kMinSplitPages : sqa::kMinSplitPages;
+    if (pps < min_pps) pps = min_pps;
   }
   if (pps > pages) pps = pages;
   if (pps > sqa::kMaxSplitPages) pps = sqa::kMaxSplitPages;
@@ -216,6 +220,8 @@ int run_attention(const sqa_attention_args& a) {
   if (need > 0 && (!a.workspace || a.workspace_bytes < need))
     return fail(SQA_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
                 a.workspace ? a.workspace_bytes : (size_t)0);
+  if (need > 0 && (uintptr_t)a.workspace % 16)
+    return fail(SQA_ERR_WORKSPACE, "workspace must be 16-byte aligned");
 
   hipStream_t s = (hipStream_t)a.stream;
   hipEvent_t* ev = (hipEvent_t*)a.timing_events;

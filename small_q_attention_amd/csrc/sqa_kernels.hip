@@ -578,11 +578,26 @@ void sqa_partial_kernel(PartialArgs a) {
   // the barrier.
   const bool active = kvh < a.hkv;
 
-  // Start-up is two memory round trips. First: the work item (fixed plan:
-  // the sequence length, with the ids of the split's first D pages loaded
-  // alongside; balanced plan: all seq_lens and a workgroup scan).
+  // Start-up. First: the work item (fixed plan: the sequence length, with the
+  // ids of the split's first D pages loaded alongside; balanced plan: all
+  // seq_lens and a workgroup scan, then those ids).
   __shared__ int sm_plan[16];
   const bool balanced = is_balanced(a.pages_per_split);
+  // Ids of the split's first D pages (index clamped into the block-table row;
+  // ids past the split are never used). A fixed plan's page range follows from
+  // blockIdx alone, so they are issued before the sequence length is read and
+  // both arrive in one round trip.
+  int first_id[D];
+  auto load_first_ids = [&](int seq, int p0) {
+    const int32_t* row = a.block_tables + (size_t)seq * a.bt_stride;
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+      first_id[j] = row[min(max(p0 + j, 0), a.max_pages - 1) >> a.page_shift];
+  };
+  if (!balanced) {
+    const int seq = item / a.num_splits;
+    load_first_ids(seq, (item - seq * a.num_splits) * a.pages_per_split);
+  }
   ItemRange it = balanced ? balanced_item<WW * 64>(a, item, sm_plan) : fixed_item(a, item);
   // The work item is the same for the whole workgroup; saying so keeps it (and
   // the buffer-resource addresses built from it) in scalar registers.
@@ -602,13 +617,7 @@ void sqa_partial_kernel(PartialArgs a) {
   const int32_t* bt_row = a.block_tables + (size_t)b * a.bt_stride;
   const int shift = a.page_shift;
   const int sub_mask = (1 << shift) - 1;
-  // Ids of the split's first D pages (index clamped into the block-table row;
-  // ids past the split are never used), issued before the exits below so the
-  // fixed plan loads them together with the sequence length.
-  int first_id[D];
-#pragma unroll
-  for (int j = 0; j < D; ++j)
-    first_id[j] = bt_row[min(max(p_begin + j, 0), a.max_pages - 1) >> shift];
+  if (balanced) load_first_ids(b, p_begin);
   if (it.b < 0) return;                           // uniform: no work item
   if (p_begin >= p_end && !single) return;        // uniform; never merged
   const int n_split = p_end > p_begin ? p_end - p_begin : 0;
@@ -640,16 +649,20 @@ void sqa_partial_kernel(PartialArgs a) {
     }
     // Draft bits of the row: bit j = sees draft token j (the caller's mask, or
     // the causal chain j <= qi).
-    unsigned long long bits;
-    if (a.draft_mask != nullptr) {
-      const uint32_t* mp = a.draft_mask + (size_t)(b * a.q_len + qi) * a.mask_words;
-      const unsigned long long lo = mp[0];
-      const unsigned long long hi = a.mask_words > 1 ? mp[1] : 0u;
-      bits = lo | (hi << 32);
-    } else {
-      bits = qi >= 63 ? ~0ull : (2ull << qi) - 1ull;
-    }
-    dbits[nb] = real ? bits : 0ull;
+    // Both words are loaded unconditionally (without a mask: from seq_lens,
+    // never used), so no branch makes the compiler wait for them before the
+    // page loads below are issued.
+    const bool has_mask = a.draft_mask != nullptr;
+    const uint32_t* mp = has_mask ? a.draft_mask + (size_t)(b * a.q_len + qi) * a.mask_words
+                                  : (const uint32_t*)a.seq_lens;
+    const unsigned long long lo = mp[0];
+    const unsigned long long hi = mp[a.mask_words > 1 ? 1 : 0];
+    const unsigned long long causal = qi >= 63 ? ~0ull : (2ull << qi) - 1ull;
+    // Selections by bit masks, not by branches on loaded values.
+    const unsigned long long use_mask = 0ull - (unsigned long long)(has_mask && real);
+    const unsigned long long use_hi = 0ull - (unsigned long long)(a.mask_words > 1);
+    const unsigned long long use_causal = 0ull - (unsigned long long)(!has_mask && real);
+    dbits[nb] = ((lo | ((hi << 32) & use_hi)) & use_mask) | (causal & use_causal);
   }
   static_assert(2 * D + 1 <= kIdPad, "page-id table padding must cover the ring's look-ahead");
   constexpr int kIdSlots = (kMaxSplitPages + kIdPad + WW * 64 - 1) / (WW * 64);
@@ -802,23 +815,28 @@ void sqa_partial_kernel(PartialArgs a) {
 // Log-sum-exp merge of split partials (reference: csrc/small_q_attention_ext.cu:339-366):
 // M = max_s m_s; O = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M); splits
 // with l_s <= 0 are skipped and a row with no visible key is written as 0.
-// A 256-thread workgroup merges 4 / G output rows; each row gets G waves and
-// wave g of a row sums dims HD/64 * lane + 0.. over the splits s = g (mod G) with
-// eight loads in flight. G = 1 (a wave per row) suits a few splits per row,
-// G = 4 spreads many splits over the workgroup; the G partial sums and the
-// global max meet in LDS.
-template <int G, int HD, typename E>
+//
+// One pass, every load of a round in flight at once: TPR threads serve one
+// output row; thread t owns 4 dims (chunk t % (HD/4)) and the splits
+// s = g, g + SG, ... of its split group g = t / (HD/4) (SG = TPR / (HD/4)
+// groups), U splits per round. Each group keeps a running max and rescales its
+// sums when the max grows (as the online softmax does), so no pass over the
+// maxima precedes the sums; the SG groups then meet by shuffles (TPR = 64, one
+// wave per row) or in LDS (TPR = 256, a workgroup per row for many splits).
+template <int TPR, int HD, typename E>
 __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
-  constexpr int DL = HD / 64;  // output dims per lane
-  constexpr int kRowsPerWg = 4 / G;
+  constexpr int CH = HD / 4;       // 4-dim chunks of a row
+  constexpr int SG = TPR / CH;     // split groups of a row
+  constexpr int RPW = 256 / TPR;   // rows per workgroup
+  constexpr int U = 8;             // splits per thread per round
+  static_assert(SG >= 1 && TPR % CH == 0, "a row's threads must cover its dims");
   const int t = threadIdx.x;
-  const int lane = t & 63;
-  const int wv = t >> 6;
-  const int slot = wv / G;  // row slot of this wave inside the workgroup
-  const int grp = wv % G;   // split group of this wave
-  const int row = blockIdx.x * kRowsPerWg + slot;
+  const int tr = t % TPR;
+  const int c = tr % CH;
+  const int g = tr / CH;
+  const int row = blockIdx.x * RPW + t / TPR;
   const int total = a.batch * a.q_len * a.hq;
-  const bool live = row < total;  // uniform per wave; every wave reaches the barriers
+  const bool live = row < total;  // uniform per row
   const int rowc = live ? row : 0;
   const int h = rowc % a.hq;
   const int qi = (rowc / a.hq) % a.q_len;
@@ -844,102 +862,77 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   const size_t stride = (size_t)a.hkv * a.rows;  // items between consecutive splits of this row
   const size_t first = ((size_t)slot0 * a.hkv + kvh) * a.rows + r;
   const float* ml = a.part_ml + first * 2;
-  const float* po = a.part_o + first * HD + DL * lane;
+  const float* po = a.part_o + first * HD + 4 * c;
 
-  __shared__ float sm_red[4];
-  __shared__ float sm_acc[4][HD + 1];
-
-  // 1. M over the splits that hold a positive sum.
-  float mx = -INFINITY;
-  for (int s = grp * 64 + lane; s < n_valid; s += G * 64) {
-    const float ls = ml[(size_t)s * stride * 2 + 1];
-    if (ls > 0.f) mx = fmaxf(mx, ml[(size_t)s * stride * 2]);
-  }
-  mx = wave_max(mx);
-  if (G > 1) {
-    if (lane == 0) sm_red[wv] = mx;
-    __syncthreads();
+  float mt = -INFINITY, den = 0.f;
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = g; s0 < n_valid; s0 += U * SG) {
+    f4 o[U];
+    float m[U], l[U];
 #pragma unroll
-    for (int g = 0; g < G; ++g) mx = fmaxf(mx, sm_red[slot * G + g]);
-  }
-
-  // 2. Weighted sums over this wave's splits (DL dims per lane).
-  auto load_o = [&](size_t it, float (&o)[DL]) {
-    const float* src = po + it * HD;
-    if constexpr (DL == 1) {
-      o[0] = src[0];
-    } else if constexpr (DL == 2) {
-      const float2 x = *(const float2*)src;
-      o[0] = x.x;
-      o[1] = x.y;
-    } else {
-      const f4 x = *(const f4*)src;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = x[i];
+    for (int u = 0; u < U; ++u) {
+      // Loads stay unconditional (past the last split: split s0 again, weight 0).
+      const int s = s0 + u * SG;
+      const size_t it = (size_t)(s < n_valid ? s : s0) * stride;
+      o[u] = *(const f4*)(po + it * HD);
+      m[u] = ml[it * 2];
+      l[u] = s < n_valid ? ml[it * 2 + 1] : 0.f;
     }
-  };
-  float acc[DL], den = 0.f;
+    float cm = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < DL; ++i) acc[i] = 0.f;
-  if (mx != -INFINITY) {
-    constexpr int kUnroll = 8;
-    int s = grp;
-    for (; s + (kUnroll - 1) * G < n_valid; s += kUnroll * G) {
-      float o[kUnroll][DL];
-      float m[kUnroll], l[kUnroll];
+    for (int u = 0; u < U; ++u) cm = l[u] > 0.f ? fmaxf(cm, m[u]) : cm;
+    const float nm = fmaxf(mt, cm);
+    if (nm != -INFINITY) {
+      const float sc = mt == -INFINITY ? 0.f : fast_exp2(mt - nm);
+      den *= sc;
+      acc *= sc;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const size_t it = (size_t)(s + u * G) * stride;
-        load_o(it, o[u]);
-        m[u] = ml[it * 2];
-        l[u] = ml[it * 2 + 1];
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const float w = l[u] > 0.f ? fast_exp2(m[u] - mx) : 0.f;
+      for (int u = 0; u < U; ++u) {
+        const float w = l[u] > 0.f ? fast_exp2(m[u] - nm) : 0.f;
         den += w * l[u];
-#pragma unroll
-        for (int i = 0; i < DL; ++i) acc[i] += w * o[u][i];
+        acc += w * o[u];
       }
-    }
-    for (; s < n_valid; s += G) {
-      const size_t it = (size_t)s * stride;
-      const float l = ml[it * 2 + 1];
-      const float w = l > 0.f ? fast_exp2(ml[it * 2] - mx) : 0.f;
-      float o[DL];
-      load_o(it, o);
-      den += w * l;
-#pragma unroll
-      for (int i = 0; i < DL; ++i) acc[i] += w * o[i];
+      mt = nm;
     }
   }
-  if (G > 1) {
+
+  // Combine the SG groups of the row.
+  auto combine = [&](float mo, float dn, f4 ao) {
+    const float nm = fmaxf(mt, mo);
+    if (nm == -INFINITY) return;
+    const float sa = mt == -INFINITY ? 0.f : fast_exp2(mt - nm);
+    const float so = mo == -INFINITY ? 0.f : fast_exp2(mo - nm);
+    den = den * sa + dn * so;
+    acc = acc * sa + ao * so;
+    mt = nm;
+  };
+  if constexpr (SG > 1 && TPR == 64) {
 #pragma unroll
-    for (int i = 0; i < DL; ++i) sm_acc[wv][DL * lane + i] = acc[i];
-    if (lane == 0) sm_acc[wv][HD] = den;
+    for (int off = CH; off < 64; off <<= 1) {
+      const float mo = __shfl_xor(mt, off), dn = __shfl_xor(den, off);
+      const f4 ao = {__shfl_xor(acc[0], off), __shfl_xor(acc[1], off), __shfl_xor(acc[2], off),
+                     __shfl_xor(acc[3], off)};
+      combine(mo, dn, ao);
+    }
+  } else if constexpr (SG > 1) {
+    static_assert(RPW == 1, "LDS combine serves one row per workgroup");
+    __shared__ f4 sm_acc[SG][CH];
+    __shared__ float sm_m[SG], sm_d[SG];
+    if (skip) return;  // uniform over the workgroup (one row)
+    sm_acc[g][c] = acc;
+    if (c == 0) {
+      sm_m[g] = mt;
+      sm_d[g] = den;
+    }
     __syncthreads();
-    if (grp != 0) return;
-    den = 0.f;
+    if (g != 0) return;
 #pragma unroll
-    for (int i = 0; i < DL; ++i) acc[i] = 0.f;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      den += sm_acc[slot * G + g][HD];
-#pragma unroll
-      for (int i = 0; i < DL; ++i) acc[i] += sm_acc[slot * G + g][DL * lane + i];
-    }
+    for (int o = 1; o < SG; ++o) combine(sm_m[o], sm_d[o], sm_acc[o][c]);
   }
-  if (skip) return;
+  if (skip || g != 0) return;
   const float inv = den > 0.f ? a.out_scale / den : 0.f;
-  _Float16* dst = a.out + (size_t)row * HD + DL * lane;
-  if constexpr (DL == 1) {
-    *(unsigned short*)dst = E::pack1(acc[0] * inv);
-  } else if constexpr (DL == 2) {
-    *(unsigned*)dst = E::pack2(acc[0] * inv, acc[1] * inv);
-  } else {
-    const float o[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
-    *(u2*)dst = E::pack4(o);
-  }
+  const float out[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+  *(u2*)(a.out + (size_t)row * HD + 4 * c) = E::pack4(out);
 }
 
 // Ring depth: the pages in flight per wave hold about 32 KiB of K and V, 4
@@ -974,13 +967,16 @@ void launch_partial_as(const PartialArgs& a, const LaunchShape& sh, dim3 grid, d
 
 template <int HD, typename E>
 void launch_merge_hd(const MergeArgs& a, int per_row, hipStream_t stream) {
+  // A wave per row while its split groups take all of the row's splits in two
+  // rounds of loads; a workgroup per row beyond that.
+  constexpr int kSplitsPerWaveRound = 8 * (64 / (HD / 4));
   const int total = a.batch * a.q_len * a.hq;
-  if (per_row <= 32) {
-    hipLaunchKernelGGL((sqa_merge_kernel<1, HD, E>), dim3((unsigned)((total + 3) / 4)), dim3(256),
-                       0, stream, a);
+  if (per_row <= 2 * kSplitsPerWaveRound) {
+    hipLaunchKernelGGL((sqa_merge_kernel<64, HD, E>), dim3((unsigned)((total + 3) / 4)),
+                       dim3(256), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((sqa_merge_kernel<4, HD, E>), dim3((unsigned)total), dim3(256), 0, stream,
-                       a);
+    hipLaunchKernelGGL((sqa_merge_kernel<256, HD, E>), dim3((unsigned)total), dim3(256), 0,
+                       stream, a);
   }
 }
 
@@ -1016,9 +1012,8 @@ hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream) {
-  // A wave per row while the splits per row fit one pass of eight loads per
-  // lane group; four waves per row beyond that. The balanced plan's split
-  // count per sequence is known only on the device: use the batch average.
+  // The balanced plan's split count per sequence is known only on the
+  // device: use the batch average.
   const int per_row = is_balanced(a.pages_per_split)
                           ? (a.num_splits - a.batch + a.batch - 1) / a.batch
                           : a.num_splits;

@@ -132,6 +132,7 @@ def _call(lib, **kw):
     (dict(pps=0, batch=2, splits=3, ws=None), SQA_ERR_WORKSPACE, "workspace"),
     (dict(splits=2, ws=None), SQA_ERR_WORKSPACE, "workspace"),
     (dict(splits=2, ws=16, ws_bytes=100), SQA_ERR_WORKSPACE, "workspace"),
+    (dict(splits=2, ws=24, ws_bytes=1 << 40), SQA_ERR_WORKSPACE, "16-byte aligned"),
     (dict(k=24), SQA_ERR_INVALID, "16-byte aligned"),
 ])
 def test_launch_rejects_bad_arguments_without_a_gpu(lib, kw, code, msg):
