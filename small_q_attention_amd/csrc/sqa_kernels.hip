@@ -713,7 +713,7 @@ void sqa_partial_kernel(PartialArgs a) {
   // then -1 for the ring's look-ahead. Waves read ids back a step ahead of
   // use, so no page waits on a block-table load from memory.
   __shared__ u4 sm_q[WW * NB * KK * 64];
-  __shared__ float sm_stage[WW * 16 * (HD / 2 + 4)];
+  __shared__ float sm_stage[WW * 16 * (HD + 4)];
   __shared__ int sm_ids[kIdSlots * WW * 64];
   u4* my_q = sm_q + wave * NB * KK * 64;
 #pragma unroll
@@ -763,15 +763,14 @@ void sqa_partial_kernel(PartialArgs a) {
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) st.l[nb] = xor_sum(st.l[nb]);
 
-  // Results leave through LDS, half a 16-row block at a time: the lanes that
-  // hold dims [k HD/2, (k + 1) HD/2) of the block's rows (lane l: dims
-  // (HD/4) (l/16) + (HD/16) rr + mb of row l % 16) write them row-major, then
-  // every lane stores 16 contiguous values' worth of a row. Each store
-  // instruction then writes runs of HD/2 values instead of 64 scattered
-  // 16-byte pieces, which ran at a quarter of the store rate (the epilogue of
-  // a 64-row wave took 5 us).
-  constexpr int kStageRow = HD / 2 + 4;  // floats per staged row; the pad spreads rows over banks
-  constexpr int CPR = HD / 8;            // 4-value chunks per half row
+  // Results leave through LDS one 16-row block at a time: every lane writes
+  // its dims (HD/4) (l/16) + (HD/16) rr + mb of row l % 16 row-major, then
+  // reads back 4 contiguous values of a row, so a store instruction writes
+  // whole rows (1 KiB runs of partial sums) instead of 64 scattered 16-byte
+  // pieces, which ran at a quarter of the store rate (the epilogue of a
+  // 64-row wave took 5 us).
+  constexpr int kStageRow = HD + 4;  // floats per staged row; the pad spreads rows over banks
+  constexpr int CPR = HD / 4;        // 4-value chunks per row
   float* stage = sm_stage + wave * 16 * kStageRow;
   const size_t item0 = ((size_t)(it.slot0 + split) * a.hkv + kvh) * a.rows;
 #pragma unroll
@@ -780,60 +779,56 @@ void sqa_partial_kernel(PartialArgs a) {
     if (rb <= 0) break;
     const float inv = st.l[nb] > 0.f ? a.out_scale / st.l[nb] : 0.f;
     const float sc = direct ? inv : 1.f;
+    if (l16 < rb) {
+      float* dst = stage + l16 * kStageRow + (HD / 4) * g16;
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      if ((g16 >> 1) == k && l16 < rb) {
-        float* dst = stage + l16 * kStageRow + (HD / 4) * (g16 & 1);
+      for (int rr = 0; rr < 4; ++rr) {
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
+        for (int h = 0; h < MB / 4; ++h) {
+          f4 o;
 #pragma unroll
-          for (int h = 0; h < MB / 4; ++h) {
-            f4 o;
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) o[mb] = st.acc[4 * h + mb][nb][rr] * sc;
-            *(f4*)(dst + MB * rr + 4 * h) = o;
-          }
-        }
-      }
-      // The staging rows are this wave's own: LDS keeps a wave's accesses in
-      // order, the fence keeps the compiler from moving them. All reads are
-      // issued before the first store, so the block pays one LDS latency.
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      f4 v[CPR / 4];
-#pragma unroll
-      for (int i = 0; i < CPR / 4; ++i) {
-        const int e = i * 64 + lane;  // row e / CPR (< 16), chunk e % CPR
-        v[i] = *(const f4*)(stage + (e / CPR) * kStageRow + 4 * (e % CPR));
-      }
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      if (direct) {
-#pragma unroll
-        for (int i = 0; i < CPR / 4; ++i) {
-          const int e = i * 64 + lane;
-          const int r = 16 * nb + e / CPR;
-          if (e / CPR < rb) {
-            const int qi = r / a.group;
-            const int gg = r - qi * a.group;
-            _Float16* op = a.out + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * HD +
-                           k * (HD / 2) + 4 * (e % CPR);
-            const float o[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
-            *(u2*)op = E::pack4(o);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < CPR / 4; ++i) {
-          const int e = i * 64 + lane;
-          if (e / CPR < rb)
-            *(f4*)(a.part_o + (item0 + 16 * nb + e / CPR) * HD + k * (HD / 2) + 4 * (e % CPR)) =
-                v[i];
+          for (int mb = 0; mb < 4; ++mb) o[mb] = st.acc[4 * h + mb][nb][rr] * sc;
+          *(f4*)(dst + MB * rr + 4 * h) = o;
         }
       }
     }
-    if (!direct && g16 == 0 && l16 < rb) {
-      const size_t pitem = item0 + 16 * nb + l16;
-      a.part_ml[pitem * 2 + 0] = st.m[nb];
-      a.part_ml[pitem * 2 + 1] = st.l[nb];
+    // The staging rows are this wave's own: LDS keeps a wave's accesses in
+    // order, the fences keep the compiler from moving them. All reads are
+    // issued before the first store, so the block pays one LDS latency.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    f4 v[CPR / 4];
+#pragma unroll
+    for (int i = 0; i < CPR / 4; ++i) {
+      const int e = i * 64 + lane;  // row e / CPR (< 16), chunk e % CPR
+      v[i] = *(const f4*)(stage + (e / CPR) * kStageRow + 4 * (e % CPR));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (direct) {
+#pragma unroll
+      for (int i = 0; i < CPR / 4; ++i) {
+        const int e = i * 64 + lane;
+        const int r = 16 * nb + e / CPR;
+        if (e / CPR < rb) {
+          const int qi = r / a.group;
+          const int gg = r - qi * a.group;
+          _Float16* op = a.out + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * HD +
+                         4 * (e % CPR);
+          const float o[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
+          *(u2*)op = E::pack4(o);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < CPR / 4; ++i) {
+        const int e = i * 64 + lane;
+        if (e / CPR < rb)
+          *(f4*)(a.part_o + (item0 + 16 * nb + e / CPR) * HD + 4 * (e % CPR)) = v[i];
+      }
+      if (g16 == 0 && l16 < rb) {
+        const size_t pitem = item0 + 16 * nb + l16;
+        a.part_ml[pitem * 2 + 0] = st.m[nb];
+        a.part_ml[pitem * 2 + 1] = st.l[nb];
+      }
     }
   }
 }
