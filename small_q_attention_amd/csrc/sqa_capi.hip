@@ -203,6 +203,8 @@ int run_attention(const sqa_attention_args& a) {
     if (batch > sqa::kMaxBalancedBatch)
       return fail(SQA_ERR_INVALID, "balanced plan (pages_per_split 0) needs batch <= %d, got %d",
                   sqa::kMaxBalancedBatch, batch);
+    if (kernel_pages >= (1LL << 24))
+      return fail(SQA_ERR_INVALID, "balanced plan needs block-table rows under 2^28 tokens");
     const long long cap = ceil_div((long long)batch * kernel_pages, sqa::kMaxSplitPages);
     if ((long long)num_splits - batch < (cap > 1 ? cap : 1))
       return fail(SQA_ERR_INVALID,

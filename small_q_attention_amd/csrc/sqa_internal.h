@@ -14,7 +14,7 @@ constexpr int kMaxPageShift = 2;  // cache pages of 16 << shift tokens: 16, 32, 
 constexpr int kMaxRows = 64;    // q_len * (Hq / Hkv) rows one work item holds
 constexpr int kMaxSplitPages = 2048;  // pages one split may own (LDS page-id table)
 constexpr int kMinSplitPages = 4;     // fewest pages the automatic plans give a split
-constexpr int kMaxBalancedBatch = 256;  // balanced plan: one sequence per thread of a workgroup
+constexpr int kMaxBalancedBatch = 256;  // balanced plan: four sequences per lane of one wave
 
 // Per-sequence split layout of the balanced plan, written by the partial
 // kernel for the merge kernel: first slot and number of splits.

@@ -430,40 +430,6 @@ __device__ __forceinline__ void process_page(WaveState<NB, HD>& st, const typena
   }
 }
 
-// Block-wide sum and exclusive scan over NT threads (sm: NT / 64 ints). Both
-// end with a barrier, so sm can be reused right after.
-template <int NT>
-__device__ __forceinline__ int block_sum(int v, int* sm) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  if (lane == 0) sm[wave] = v;
-  __syncthreads();
-  int total = 0;
-#pragma unroll
-  for (int w = 0; w < NT / 64; ++w) total += sm[w];
-  __syncthreads();
-  return total;
-}
-
-template <int NT>
-__device__ __forceinline__ int block_exclusive_scan(int v, int* sm) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  if (lane == 63) sm[wave] = x;
-  __syncthreads();
-  int off = 0;
-#pragma unroll
-  for (int w = 0; w < NT / 64; ++w) off += w < wave ? sm[w] : 0;
-  __syncthreads();
-  return off + x - v;
-}
-
 // The page range one workgroup owns and where its sequence's result goes.
 struct ItemRange {
   int b;        // sequence (-1: no work item for this workgroup)
@@ -489,66 +455,114 @@ __device__ __forceinline__ ItemRange fixed_item(const PartialArgs& a, int item) 
   return r;
 }
 
-// Balanced plan (all NT threads call it; batch <= NT). num_splits = T +
-// batch slots, T = the work items one wave of resident workgroups holds.
-// Thread t takes sequence t and the workgroup picks one split size for the
-// batch: the smallest in [ceil(total / T), ceil(total / (T - batch))] (clamped
-// to [kMinSplitPages, kMaxSplitPages]) whose per-sequence split counts sum to
-// at most T (bisection over block sums), so no workgroup waits for a second
-// wave; the lower end alone always fits the T + batch slots. A scan of the
-// split counts then gives each sequence its first slot; the thread whose
-// sequence holds `item` publishes it. Workgroup 0 also stores every sequence's
-// (first slot, split count) for the merge kernel. Every workgroup computes the
-// same plan from the same seq_lens.
-template <int NT>
-__device__ ItemRange balanced_item(const PartialArgs& a, int item, int* sm) {
-  const int t = threadIdx.x;
-  if (t < 6) sm[8 + t] = t == 0 ? -1 : 0;  // defaults: no work item
-  int len = 0, pages = 0;
-  if (t < a.batch) {
-    len = max(a.seq_lens[t], 0);
-    pages = min((len + kPageSize - 1) / kPageSize, a.max_pages);
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ int wave_inclusive_scan_int(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(v, o);
+    if (lane >= o) v += y;
   }
-  const int total = block_sum<NT>(pages, sm);
+  return v;
+}
+
+// Balanced plan (batch <= kMaxBalancedBatch = 4 x 64). num_splits = T + batch
+// slots, T = the work items one wave of resident workgroups holds. Every wave
+// derives the same plan on its own, with wave reductions only (no LDS, no
+// barrier): lane l takes sequences l, l + 64, l + 128, l + 192, and the wave
+// picks one split size for the batch: the smallest in [ceil(total / T),
+// ceil(total / (T - batch))] (clamped to [kMinSplitPages, kMaxSplitPages])
+// whose per-sequence split counts sum to at most T (bisection), so no
+// workgroup waits for a second wave; the lower end alone always fits the
+// T + batch slots. A scan of the split counts gives each sequence its first
+// slot, and the lane whose sequence holds `item` hands its range to the wave.
+// Wave 0 of workgroup 0 also stores every sequence's (first slot, split
+// count) for the merge kernel. Every workgroup computes the same plan from the
+// same seq_lens.
+__device__ ItemRange balanced_item(const PartialArgs& a, int item) {
+  constexpr int K = kMaxBalancedBatch / 64;
+  const int lane = threadIdx.x & 63;
+  const int groups = (a.batch + 63) / 64;  // uniform; groups of 64 sequences in use
+  int len[K], pages[K];
+  int total = 0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int sq = 64 * k + lane;
+    len[k] = k < groups && sq < a.batch ? max(a.seq_lens[min(sq, a.batch - 1)], 0) : 0;
+    pages[k] = min((len[k] + kPageSize - 1) / kPageSize, a.max_pages);
+    total += pages[k];
+  }
+  total = wave_sum_int(total);
+  // ceil(n / size) for a uniform size: float reciprocal, then one correction
+  // each way (n < 2^24, so the estimate is off by at most one).
+  auto ceil_div_u = [](int n, int size, float inv) {
+    int q = (int)((float)n * inv);
+    q += (q + 1) * size <= n ? 1 : 0;
+    q -= q * size > n ? 1 : 0;
+    return q + (q * size < n ? 1 : 0);
+  };
+  auto count_splits = [&](int size) {
+    const float inv = 1.f / (float)size;
+    int n = 0;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (k < groups) n += ceil_div_u(pages[k], size, inv);
+    return wave_sum_int(n);
+  };
   const int target = a.num_splits - a.batch;
   const int lo = min(max((total + target - 1) / target, kMinSplitPages), kMaxSplitPages);
   int hi = lo;
   if (target > a.batch)
     hi = min(max((total + target - a.batch - 1) / (target - a.batch), lo), kMaxSplitPages);
   int pps = lo;
-  if (hi > lo && block_sum<NT>((pages + lo - 1) / lo, sm) > target) {
+  if (hi > lo && count_splits(lo) > target) {
     int l = lo + 1, h = hi;  // uniform bisection: smallest size in (lo, hi] that fits
     while (l < h) {
       const int mid = (l + h) >> 1;
-      if (block_sum<NT>((pages + mid - 1) / mid, sm) <= target)
+      if (count_splits(mid) <= target)
         h = mid;
       else
         l = mid + 1;
     }
     pps = h;
   }
-  const int splits = (pages + pps - 1) / pps;
-  const int first = block_exclusive_scan<NT>(splits, sm);
-  if (t < a.batch) {
-    if (blockIdx.x == 0) a.seq_splits[t] = SeqSplits{first, splits};
-    if (item >= first && item < first + splits) {
-      sm[8] = t;
-      sm[9] = item - first;
-      sm[10] = len;
-      sm[11] = pages;
-      sm[12] = first;
-      sm[13] = splits;
-    }
-  }
-  __syncthreads();
   ItemRange r;
-  r.b = sm[8];
-  r.split = sm[9];
-  r.len = sm[10];
-  r.p_begin = r.split * pps;
-  r.p_end = min(r.p_begin + pps, sm[11]);
-  r.slot0 = sm[12];
-  r.n_valid = sm[13];
+  r.b = -1;  // no work item unless a sequence holds `item`
+  r.split = 0;
+  r.len = 0;
+  r.p_begin = 0;
+  r.p_end = 0;
+  r.slot0 = 0;
+  r.n_valid = 0;
+  int base = 0;  // slots of the sequences before this group of 64
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    if (k >= groups) break;
+    const int splits = (pages[k] + pps - 1) / pps;
+    const int incl = wave_inclusive_scan_int(splits);
+    const int first = base + incl - splits;
+    const int sq = 64 * k + lane;
+    if (blockIdx.x == 0 && threadIdx.x < 64 && sq < a.batch)
+      a.seq_splits[sq] = SeqSplits{first, splits};
+    const bool mine = sq < a.batch && item >= first && item < first + splits;
+    const unsigned long long hit = __ballot(mine);
+    if (hit) {
+      const int src = __builtin_ctzll(hit);
+      r.b = 64 * k + src;
+      r.split = item - __shfl(first, src);
+      r.len = __shfl(len[k], src);
+      r.slot0 = __shfl(first, src);
+      r.n_valid = __shfl(splits, src);
+      r.p_begin = r.split * pps;
+      r.p_end = min(r.p_begin + pps, __shfl(pages[k], src));
+    }
+    base += __shfl(incl, 63);
+  }
   return r;
 }
 
@@ -581,7 +595,6 @@ void sqa_partial_kernel(PartialArgs a) {
   // Start-up. First: the work item (fixed plan: the sequence length, with the
   // ids of the split's first D pages loaded alongside; balanced plan: all
   // seq_lens and a workgroup scan, then those ids).
-  __shared__ int sm_plan[16];
   const bool balanced = is_balanced(a.pages_per_split);
   // Ids of the split's first D pages (index clamped into the block-table row;
   // ids past the split are never used). A fixed plan's page range follows from
@@ -598,7 +611,7 @@ void sqa_partial_kernel(PartialArgs a) {
     const int seq = item / a.num_splits;
     load_first_ids(seq, (item - seq * a.num_splits) * a.pages_per_split);
   }
-  ItemRange it = balanced ? balanced_item<WW * 64>(a, item, sm_plan) : fixed_item(a, item);
+  ItemRange it = balanced ? balanced_item(a, item) : fixed_item(a, item);
   // The work item is the same for the whole workgroup; saying so keeps it (and
   // the buffer-resource addresses built from it) in scalar registers.
   it.b = __builtin_amdgcn_readfirstlane(it.b);

@@ -132,7 +132,7 @@ def test_balanced_plan_on_a_skewed_batch(q_len):
 
 
 def test_balanced_plan_at_the_batch_limit():
-    """256 sequences (the balanced plan's limit; one per thread of the plan scan)
+    """256 sequences (the balanced plan's limit; four per lane of the plan's wave)
     and 257 (fixed plan), on a block table wide enough that the 2048-page split cap
     sets the slot count."""
     for batch in (256, 257):
