@@ -80,7 +80,9 @@ size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv
  * max(1, ceil(batch * max_pages * page_size / 16 / 2048))); max_pages is the
  * block_tables row length. head_dim is 128 (the reference's), 64 or 256;
  * 256 needs q_len * num_query_heads / num_kv_heads <= 32. `workspace` must hold
- * sqa_workspace_bytes(...) bytes, 16-byte aligned (may be NULL when that is 0). Allocates
+ * sqa_workspace_bytes(...) bytes, 16-byte aligned (may be NULL when that is 0). query
+ * and the caches must be 16-byte aligned, output 8-byte, block_tables and seq_lens
+ * 4-byte (SQA_ERR_INVALID otherwise). Allocates
  * nothing and never synchronises.
  * `timing_events`: NULL, or an array of 3 hipEvent_t recorded on `stream`
  * before the partial kernel, between the two kernels and after the merge

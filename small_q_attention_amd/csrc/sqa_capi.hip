@@ -182,6 +182,11 @@ int run_attention(const sqa_attention_args& a) {
     return fail(SQA_ERR_INVALID, "cache strides must be non-negative multiples of 8 elements");
   if (((uintptr_t)a.kv.k | (uintptr_t)a.kv.v) % 16)
     return fail(SQA_ERR_INVALID, "cache base pointers must be 16-byte aligned");
+  // Q rows are read 16 bytes at a time, outputs written 8 bytes at a time.
+  if ((uintptr_t)a.query % 16 || (uintptr_t)a.output % 8)
+    return fail(SQA_ERR_INVALID, "query must be 16-byte and output 8-byte aligned");
+  if (((uintptr_t)a.block_tables | (uintptr_t)a.seq_lens | (uintptr_t)a.draft_mask) % 4)
+    return fail(SQA_ERR_INVALID, "block_tables, seq_lens and draft_mask must be 4-byte aligned");
   const long long extent =
       kv_bytes * ((long long)(sqa::kPageSize - 1) * ts + (long long)(num_kv_heads - 1) * hs +
                   head_dim);

@@ -134,6 +134,10 @@ def _call(lib, **kw):
     (dict(splits=2, ws=16, ws_bytes=100), SQA_ERR_WORKSPACE, "workspace"),
     (dict(splits=2, ws=24, ws_bytes=1 << 40), SQA_ERR_WORKSPACE, "16-byte aligned"),
     (dict(k=24), SQA_ERR_INVALID, "16-byte aligned"),
+    (dict(q=24), SQA_ERR_INVALID, "query must be 16-byte"),
+    (dict(out=20), SQA_ERR_INVALID, "output 8-byte aligned"),
+    (dict(bt=18), SQA_ERR_INVALID, "4-byte aligned"),
+    (dict(sl=17), SQA_ERR_INVALID, "4-byte aligned"),
 ])
 def test_launch_rejects_bad_arguments_without_a_gpu(lib, kw, code, msg):
     # Validation runs before any HIP call, so these pointers are never touched.
