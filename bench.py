@@ -146,6 +146,17 @@ def cpu_baseline(torch, tensors, case, target_s):
         kv_done += int(case.seq_lens[b]) * case.num_kv_heads * case.head_dim * 4
         done += 1
     per_seq_s = elapsed / done
+    # cfg1 (B1 q_len2 KV1024, the reference's CPU-runnable case) in full, best of 3.
+    from small_q_attention_amd import inputs
+
+    c1 = inputs.baseline_configs()["cfg1"]
+    q1, k1, v1, bt1, sl1 = inputs.make_inputs(c1)
+    q1, k1, v1 = q1.float(), k1.float(), v1.float()
+    cfg1_s = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.paged_mtp_attention_reference(q1, k1, v1, bt1, sl1, c1.page_size, c1.num_kv_heads)
+        cfg1_s.append(time.perf_counter() - t0)
     return {
         "value": round(kv_done / elapsed / 1e9, 4),
         "unit": "GB/s (KV bytes / CPU time)",
@@ -155,6 +166,7 @@ def cpu_baseline(torch, tensors, case, target_s):
         "sample": (f"{done} of {case.batch} sequences of the workload (full KV length "
                    f"{case.seq_lens[0]}, all {case.num_query_heads} heads), fp32 on .float() "
                    f"copies; us_per_call extrapolates to the whole batch"),
+        "cfg1_us_per_call": round(min(cfg1_s) * 1e6, 1),
         "cpu_model": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
     }
@@ -327,7 +339,7 @@ def main():
         others = {}
         del tensors, q, k, v, bt, sl, out
         torch.cuda.empty_cache()
-        for name in ("cfg2", "cfg5"):
+        for name in ("cfg1", "cfg2", "cfg5"):
             c = inputs.baseline_configs()[name]
             t = inputs.make_inputs(c, device="cuda", gen_device="cuda")
             pl = _lib.plan_splits(0, c.batch, c.q_len, c.num_query_heads, c.num_kv_heads,
