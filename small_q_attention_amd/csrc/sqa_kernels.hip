@@ -594,7 +594,7 @@ void sqa_partial_kernel(PartialArgs a) {
 
   // Start-up. First: the work item (fixed plan: the sequence length, with the
   // ids of the split's first D pages loaded alongside; balanced plan: all
-  // seq_lens and a workgroup scan, then those ids).
+  // seq_lens and the plan's wave reductions, then those ids).
   const bool balanced = is_balanced(a.pages_per_split);
   // Ids of the split's first D pages (index clamped into the block-table row;
   // ids past the split are never used). A fixed plan's page range follows from
@@ -661,10 +661,9 @@ void sqa_partial_kernel(PartialArgs a) {
       qreg[nb][kk] = real ? x : u4{0u, 0u, 0u, 0u};
     }
     // Draft bits of the row: bit j = sees draft token j (the caller's mask, or
-    // the causal chain j <= qi).
-    // Both words are loaded unconditionally (without a mask: from seq_lens,
-    // never used), so no branch makes the compiler wait for them before the
-    // page loads below are issued.
+    // the causal chain j <= qi). Both mask words are loaded unconditionally
+    // (without a mask: from seq_lens, never used), so no branch makes the
+    // compiler wait for them before the page loads below are issued.
     const bool has_mask = a.draft_mask != nullptr;
     const uint32_t* mp = has_mask ? a.draft_mask + (size_t)(b * a.q_len + qi) * a.mask_words
                                   : (const uint32_t*)a.seq_lens;
@@ -724,7 +723,8 @@ void sqa_partial_kernel(PartialArgs a) {
   // B-operand layout; each lane stores exactly the fragments it reads back),
   // and the split's page ids: ids of [p_begin, p_end) clamped into the pool,
   // then -1 for the ring's look-ahead. Waves read ids back a step ahead of
-  // use, so no page waits on a block-table load from memory.
+  // use, so no page waits on a block-table load from memory. sm_stage holds
+  // each wave's results on their way out (the epilogue below).
   __shared__ u4 sm_q[WW * NB * KK * 64];
   __shared__ float sm_stage[WW * 16 * (HD + 4)];
   __shared__ int sm_ids[kIdSlots * WW * 64];
