@@ -152,6 +152,32 @@ def test_balanced_plan_at_the_batch_limit():
         assert_parity(out, _oracle(tensors), label=f"B{batch}")
 
 
+@pytest.mark.parametrize("hq,hkv,q_len", [
+    (8, 8, 4),    # group 1 (MHA)
+    (16, 2, 8),   # group 8, one head group with two idle waves
+    (32, 1, 2),   # group 32 (MQA): 64 rows on one kv head
+    (12, 6, 8),   # second head group with two idle waves
+    (24, 3, 4),   # group 8, three kv heads
+])
+def test_other_head_counts(hq, hkv, q_len):
+    """Head layouts beyond the reference's 32/8 on the native entry: the row map
+    r = qi * group + g, kv heads that leave waves of a workgroup idle, and all three
+    plans (balanced, fixed, single split)."""
+    lens = [1, 700, 33, 2900]
+    case = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=hq * 10 + hkv,
+                       num_query_heads=hq, num_kv_heads=hkv)
+    tensors = _to_gpu(inputs.make_inputs(case))
+    ref = _oracle(tensors, hkv=hkv)
+    for ck in (None, 256, 1 << 20):
+        out = sqa.paged_mtp_attention(*tensors, 16, max(lens), chunk_keys=ck)
+        assert_parity(out, ref, label=f"hq{hq} hkv{hkv} q{q_len} ck{ck}")
+    one = _to_gpu(inputs.make_inputs(inputs.Case(batch=1, q_len=q_len, seq_lens=[5000],
+                                                 seed=7, num_query_heads=hq,
+                                                 num_kv_heads=hkv)))
+    assert_parity(sqa.paged_mtp_attention(*one, 16), _oracle(one, hkv=hkv),
+                  label=f"hq{hq} hkv{hkv} B1")
+
+
 def test_rows_without_visible_keys_are_zero():
     """seq_len < q_len: rows qi < q_len - seq_len see nothing and are written as 0
     (reference v2-v5 merge, csrc/small_q_attention_ext.cu:365); seq_len 0 gives 0."""
