@@ -6,8 +6,9 @@
  * Tensor contract (reference: /root/reference/csrc/small_q_attention_ext.cu:976-1002,
  * /root/reference/src/small_q_attention/cuda.py:61-78):
  *   query        [batch, q_len, num_query_heads, 128]  fp16, contiguous, device
+ *                (head_dim 64 and 256 are also built; 128 is the reference's)
  *   key_cache    [num_pages, page_size, num_kv_heads, 128]  fp16, contiguous, device;
- *                page_size 16 (the reference's), 32 or 64
+ *                page_size 16 (the reference's), 32, 64, 128 or 256
  *   value_cache  same shape as key_cache
  *   block_tables [batch, max_pages] int32, device
  *   seq_lens     [batch] int32, device; KV length including the q_len draft tokens

@@ -156,7 +156,8 @@ int run_attention(const sqa_attention_args& a) {
   for (int sh = 0; sh <= sqa::kMaxPageShift; ++sh)
     if (page_size == (sqa::kPageSize << sh)) page_shift = sh;
   if (page_shift < 0)
-    return fail(SQA_ERR_UNSUPPORTED, "page_size must be 16, 32 or 64 (got %d)", page_size);
+    return fail(SQA_ERR_UNSUPPORTED, "page_size must be 16, 32, 64, 128 or 256 (got %d)",
+                page_size);
   // The kernels work in 16-token pages; a cache page is 1 << page_shift of them.
   const long long kernel_pages = (long long)max_pages << page_shift;
   if (kernel_pages > 0x7fffffffLL) return fail(SQA_ERR_INVALID, "block table too wide");

@@ -10,7 +10,7 @@ namespace sqa {
 constexpr int kHeadDim = 128;   // the reference's head_dim; 64 and 256 are also built
 constexpr int kMaxRowsHd256 = 32;  // head_dim 256: accumulators of at most two 16-row blocks
 constexpr int kPageSize = 16;   // kernel page: 16 tokens (one MFMA tile of keys)
-constexpr int kMaxPageShift = 2;  // cache pages of 16 << shift tokens: 16, 32, 64
+constexpr int kMaxPageShift = 4;  // cache pages of 16 << shift tokens: 16 .. 256
 constexpr int kMaxRows = 64;    // q_len * (Hq / Hkv) rows one work item holds
 constexpr int kMaxSplitPages = 2048;  // pages one split may own (LDS page-id table)
 constexpr int kMinSplitPages = 4;     // fewest pages the automatic plans give a split

@@ -19,7 +19,7 @@ non-contiguous, not fp16, an unsupported ``q_len`` or ``head_dim``
 Deliberate contract differences:
 * ``q_len`` 16 is accepted (the reference allows 2, 4, 8): ``q_len * group``
   must be at most 64 rows.
-* ``page_size`` must be 16, 32 or 64 and ``head_dim`` 128 (the reference's
+* ``page_size`` must be 16, 32, 64, 128 or 256 and ``head_dim`` 128 (the reference's
   launchers take any page size, but every reference caller uses 16). The
   native entry :func:`paged_mtp_attention` also takes head_dim 64 and 256
   (at most 32 rows at 256).
@@ -39,7 +39,7 @@ SUPPORTED_Q_LENS = (2, 4, 8, 16)
 HEAD_DIM = 128
 HEAD_DIMS = (64, 128, 256)  # native entry
 PAGE_SIZE = 16
-SUPPORTED_PAGE_SIZES = (16, 32, 64)
+SUPPORTED_PAGE_SIZES = (16, 32, 64, 128, 256)
 MAX_ROWS = 64
 
 
@@ -179,7 +179,7 @@ def _check_launcher_contract(query, key_cache, value_cache, block_tables, seq_le
     if batch == 0:
         raise RuntimeError("batch must be positive")
     if cache_page not in SUPPORTED_PAGE_SIZES:
-        raise ValueError("this build supports page_size 16, 32 or 64")
+        raise ValueError("this build supports page_size 16, 32, 64, 128 or 256")
     rows_cap = 32 if dim == 256 else MAX_ROWS
     if q_len * (hq // hkv) > rows_cap:
         raise ValueError(f"q_len * (Hq / Hkv) must be at most {rows_cap} at head_dim {dim}")

@@ -7,7 +7,7 @@ The reference compares its kernels with four FlashInfer paths for the same op
 so code written against them runs here unchanged, within the contract of this
 build (fp16 or bf16 Q, K/V of the same type or OCP FP8 E4M3
 (``torch.float8_e4m3fn``, K/V scales folded into ``bmm1_scale``/``bmm2_scale``),
-head_dim 64, 128 or 256, pages of 16, 32 or 64 tokens, ``q_len * Hq / Hkv <= 64``,
+head_dim 64, 128 or 256, pages of 16 to 256 tokens, ``q_len * Hq / Hkv <= 64``,
 at most 32 at head_dim 256):
 
 * :func:`xqa_batch_decode_with_kv_cache` — block table + seq_lens, interleaved
@@ -35,8 +35,8 @@ from typing import Optional
 from . import _lib
 from .masks import as_words
 
-PAGE_SIZE = 16  # tokens per kernel page; cache pages hold 16, 32 or 64
-PAGE_SIZES = (16, 32, 64)
+PAGE_SIZE = 16  # tokens per kernel page; cache pages hold 16 << k of them
+PAGE_SIZES = (16, 32, 64, 128, 256)
 HEAD_DIMS = (64, 128, 256)
 
 
@@ -82,7 +82,7 @@ def _check_tensors(query, k, v, num_qo_heads: Optional[int] = None):
         raise ValueError("this build supports head_dim 64, 128 or 256, equal for query and "
                          "kv_cache")
     if k.shape[1] not in PAGE_SIZES:
-        raise ValueError("this build supports page_size 16, 32 or 64")
+        raise ValueError("this build supports page_size 16, 32, 64, 128 or 256")
     if num_qo_heads is not None and query.shape[1] != num_qo_heads:
         raise ValueError(f"query has {query.shape[1]} heads, plan() was given {num_qo_heads}")
 
@@ -237,8 +237,8 @@ class _PagedWrapper:
             raise ValueError("this build supports fp16 or bf16 query and KV "
                              "(KV also float8_e4m3fn)")
         if head_dim not in HEAD_DIMS or page_size not in PAGE_SIZES:
-            raise ValueError("this build supports head_dim 64, 128 or 256 and page_size 16, 32 "
-                             "or 64")
+            raise ValueError("this build supports head_dim 64, 128 or 256 and page_size 16, 32, "
+                             "64, 128 or 256")
         if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
             raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
         block_tables, seq_lens = csr_to_block_table(indptr, indices, last_page_len, page_size)

@@ -115,7 +115,7 @@ def _call(lib, **kw):
     # head_dim 256 holds at most 32 rows per kv head.
     (dict(dim=256, q_len=16), SQA_ERR_UNSUPPORTED, "exceeds 32 at head_dim 256"),
     (dict(page=24), SQA_ERR_UNSUPPORTED, "page_size"),
-    (dict(page=128), SQA_ERR_UNSUPPORTED, "page_size"),
+    (dict(page=512), SQA_ERR_UNSUPPORTED, "page_size"),
     # 64-token pages: the balanced plan's slot bound counts 16-token pages.
     (dict(pps=0, batch=4, splits=7, max_pages=513, page=64, ws=16, ws_bytes=1 << 40),
      SQA_ERR_INVALID, "num_splits >= batch + 5"),

@@ -260,10 +260,10 @@ def _as_16_token_pages(k, v, bt, page):
     return k16, v16, bt16
 
 
-@pytest.mark.parametrize("page", [32, 64])
+@pytest.mark.parametrize("page", [32, 64, 128, 256])
 @pytest.mark.parametrize("q_len", [2, 8, 16])
 def test_larger_cache_pages(page, q_len):
-    """32- and 64-token cache pages through the reference boundary and the
+    """32- to 256-token cache pages through the reference boundary and the
     FlashInfer-shaped calls: parity with the oracle, and the same bits as the same
     memory addressed as 16-token pages."""
     lens = [1, q_len, page - 1, page, page + 1, 700, 5000]
