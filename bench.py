@@ -224,7 +224,7 @@ def main():
     tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
     q, k, v, bt, sl = tensors
     plan = _lib.plan_splits(0, case.batch, case.q_len, case.num_query_heads, case.num_kv_heads,
-                            case.max_seq_len, bt.shape[1], 0)
+                            case.head_dim, case.max_seq_len, bt.shape[1], 0)
     _ramp_clocks(torch, _lib, tensors, plan)
     ms, part_ms, merge_ms, out = time_calls(torch, _lib, tensors, plan, args.steps, args.warmup)
     if not torch.isfinite(out).all():
@@ -274,7 +274,7 @@ def main():
             qx = torch.randn(case.batch, ql, case.num_query_heads, case.head_dim,
                              generator=g, device="cuda", dtype=torch.float16)
             planx = _lib.plan_splits(0, case.batch, ql, case.num_query_heads, case.num_kv_heads,
-                                     case.max_seq_len, bt.shape[1], 0)
+                                     case.head_dim, case.max_seq_len, bt.shape[1], 0)
             msx, px, mx, _ = time_calls(torch, _lib, (qx, k, v, bt, sl), planx, args.steps,
                                         args.warmup)
             extra[f"q{ql}"] = {"us_per_call": round(msx * 1e3, 2),
@@ -343,7 +343,7 @@ def main():
             c = inputs.baseline_configs()[name]
             t = inputs.make_inputs(c, device="cuda", gen_device="cuda")
             pl = _lib.plan_splits(0, c.batch, c.q_len, c.num_query_heads, c.num_kv_heads,
-                                  c.max_seq_len, t[3].shape[1], 0)
+                                  c.head_dim, c.max_seq_len, t[3].shape[1], 0)
             _ramp_clocks(torch, _lib, t, pl, seconds=0.1)
             msx, px, mx, _ = time_calls(torch, _lib, t, pl, args.steps, args.warmup)
             kb = inputs.kv_bytes(c.seq_lens, c.num_kv_heads, c.head_dim)

@@ -57,11 +57,13 @@ extern "C" {
  * max_pages: 16-token pages a block-table row addresses (block_tables columns
  * x page_size / 16); num_splits and pages_per_split count 16-token pages too.
  * max_seq_len <= 0 means "unknown": a fixed plan covers max_pages * 16 tokens.
+ * head_dim: as passed to the attention call (it sets the kernel's heads per
+ * workgroup, hence the split count of the automatic plans).
  * Writes *num_splits >= 1 and *pages_per_split >= 0.
  */
 int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int num_kv_heads,
-                    int max_seq_len, int max_pages, int chunk_keys, int* num_splits,
-                    int* pages_per_split);
+                    int head_dim, int max_seq_len, int max_pages, int chunk_keys,
+                    int* num_splits, int* pages_per_split);
 
 /*
  * Device workspace bytes sqa_paged_mtp_attention needs for a plan from

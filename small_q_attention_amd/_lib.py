@@ -22,7 +22,7 @@ SQA_OK = 0
 _C = ctypes
 _SIGNATURES = [
     ("sqa_plan_splits", _C.c_int,
-     [_C.c_int] * 8 + [_C.POINTER(_C.c_int), _C.POINTER(_C.c_int)]),
+     [_C.c_int] * 9 + [_C.POINTER(_C.c_int), _C.POINTER(_C.c_int)]),
     ("sqa_workspace_bytes", _C.c_size_t, [_C.c_int] * 7),
     ("sqa_paged_mtp_attention", _C.c_int,
      [_C.c_void_p] * 7 + [_C.c_size_t] + [_C.c_int] * 5 + [_C.c_int64] + [_C.c_int] * 4
@@ -93,13 +93,15 @@ def last_error(lib) -> str:
 
 @functools.lru_cache(maxsize=4096)
 def plan_splits(device_index: int, batch: int, q_len: int, num_query_heads: int,
-                num_kv_heads: int, max_seq_len: int, max_pages: int, chunk_keys: int):
+                num_kv_heads: int, head_dim: int, max_seq_len: int, max_pages: int,
+                chunk_keys: int):
     """``sqa_plan_splits`` -> ``(num_splits, pages_per_split)``; memoised (the plan is a
     pure function of its arguments and the device's CU count)."""
     lib = load()
     ns, pps = ctypes.c_int(0), ctypes.c_int(0)
     rc = lib.sqa_plan_splits(device_index, batch, q_len, num_query_heads, num_kv_heads,
-                             max_seq_len, max_pages, chunk_keys, ctypes.byref(ns), ctypes.byref(pps))
+                             head_dim, max_seq_len, max_pages, chunk_keys, ctypes.byref(ns),
+                             ctypes.byref(pps))
     if rc != SQA_OK:
         raise RuntimeError(f"sqa_plan_splits failed: {last_error(lib)}")
     return ns.value, pps.value

@@ -62,8 +62,8 @@ int sqa_device_cu_count(int device) {
 }
 
 int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int num_kv_heads,
-                    int max_seq_len, int max_pages, int chunk_keys, int* num_splits,
-                    int* pages_per_split) {
+                    int head_dim, int max_seq_len, int max_pages, int chunk_keys,
+                    int* num_splits, int* pages_per_split) {
   if (!num_splits || !pages_per_split) return fail(SQA_ERR_INVALID, "null output pointer");
   if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_query_heads <= 0 || max_pages <= 0)
     return fail(SQA_ERR_INVALID, "batch, q_len, heads and max_pages must be positive");
@@ -80,7 +80,8 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
     int cus = sqa_device_cu_count(device);
     if (cus <= 0) return SQA_ERR_HIP;
     // One wave of resident workgroups over the whole chip.
-    const sqa::LaunchShape sh = sqa::launch_shape(q_len * (num_query_heads / num_kv_heads));
+    const sqa::LaunchShape sh =
+        sqa::launch_shape(q_len * (num_query_heads / num_kv_heads), num_kv_heads, head_dim);
     const long long head_groups = (num_kv_heads + sh.heads - 1) / sh.heads;
     const long long slots_target = ceil_div((long long)cus * sh.wg_per_cu, head_groups);
     if (batch > 1 && batch <= sqa::kMaxBalancedBatch) {

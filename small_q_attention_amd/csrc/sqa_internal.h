@@ -85,8 +85,8 @@ struct MergeArgs {
 };
 
 // Launch shape of the partial kernel for a given number of query rows per kv
-// head. A workgroup serves `heads` kv heads of one (sequence, split), one wave
-// per head holding all of its rows; all waves walk the same pages, so the
+// head. A workgroup serves `heads` kv heads of one (sequence, split), `hpw`
+// heads per wave holding all of their rows; all waves walk the same pages, so the
 // heads' slices of a page are read together (>= 4 heads keeps HBM accesses at
 // >= 1 KiB contiguous). `wg_per_cu` workgroups are resident per CU, which sets
 // the split count of the automatic plans.
@@ -99,14 +99,24 @@ struct MergeArgs {
 // one would have used.
 struct LaunchShape {
   int row_blocks;  // 16-row blocks per wave (1, 2 or 4)
-  int heads;       // kv heads per workgroup (one wave each)
+  int heads;       // kv heads per workgroup
+  int hpw;         // kv heads per wave (2: both halves of a 16-row block)
   int wg_per_cu;   // resident workgroups per CU
+  int waves() const { return heads / hpw; }
 };
 
-inline LaunchShape launch_shape(int rows) {
-  if (rows <= 16) return {1, 4, 1};
-  if (rows <= 32) return {2, 4, 1};
-  return {4, 4, 1};
+// At head dim 64 with up to 8 rows per kv head (q_len 2 at GQA 4) a wave holds
+// two kv heads in its one 16-row block: no padding rows, and the per-page
+// work (page id, buffer resources, softmax over 16 rows) is spread over twice
+// the bytes (a head's page is 4 KiB there); cfg3 lengths, q_len 2: 168.5 ->
+// 160.6 us. At head dim 128 the same shape ran 1-12% slower (half the pages
+// per work item, twice the partials) and keeps one head per wave. Needs
+// Hkv % 8 == 0.
+inline LaunchShape launch_shape(int rows, int hkv, int head_dim) {
+  if (rows <= 8 && hkv % 8 == 0 && head_dim == 64) return {1, 8, 2, 1};
+  if (rows <= 16) return {1, 4, 1, 1};
+  if (rows <= 32) return {2, 4, 1, 1};
+  return {4, 4, 1, 1};
 }
 
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream);

@@ -336,24 +336,38 @@ __device__ __forceinline__ unsigned pack_hi(unsigned a, unsigned b) {
 // Visibility on masked pages: token t < len is seen by a row when it lies
 // before the draft block (t < draft_base = len - q_len) or when bit
 // t - draft_base of the row's draft bits is set.
-template <int NB, int HD, typename E, typename KV>
-__device__ __forceinline__ void process_page(WaveState<NB, HD>& st, const typename KV::Regs& raw,
-                                             const u4* sm_q,
-                                             int lane, const unsigned long long (&dbits)[NB],
+// HPW = 2 (one 16-row block, rows 0-7 of kv head 0 of the wave and rows 8-15
+// of head 1): the QK and PV products run once per head over all 16 rows; each
+// lane keeps the scores of its own row's head (`upper`: row >= 8), and each
+// head's PV product gets the probabilities of its own rows only, so both land
+// in the one set of accumulators.
+template <int NB, int HD, typename E, typename KV, int HPW>
+__device__ __forceinline__ void process_page(WaveState<NB, HD>& st,
+                                             const typename KV::Regs (&raw)[HPW],
+                                             const u4* sm_q, int lane, bool upper,
+                                             const unsigned long long (&dbits)[NB],
                                              int draft_base, int tok0, int len, bool masked,
                                              float c) {
   constexpr int KK = Dims<HD>::KK, MB = Dims<HD>::MB, VW = Dims<HD>::VW;
-  PageVals<HD> pg;
-  KV::template expand<E>(raw, pg);
+  static_assert(HPW == 1 || NB == 1, "two heads per wave share one 16-row block");
+  PageVals<HD> pg[HPW];
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) KV::template expand<E>(raw[h], pg[h]);
   // Raw scores S^T[token][row] = K . Q^T for this page.
   f4 s[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     s[nb] = f4{0.f, 0.f, 0.f, 0.f};
+    f4 s1 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const u4 qf = sm_q[(nb * KK + kk) * 64 + lane];
-      s[nb] = E::mma_qk(pg.k[kk], qf, s[nb]);
+      s[nb] = E::mma_qk(pg[0].k[kk], qf, s[nb]);
+      if constexpr (HPW == 2) s1 = E::mma_qk(pg[HPW - 1].k[kk], qf, s1);
+    }
+    if constexpr (HPW == 2) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[nb][e] = upper ? s1[e] : s[nb][e];
     }
   }
   if (masked) {
@@ -377,7 +391,9 @@ __device__ __forceinline__ void process_page(WaveState<NB, HD>& st, const typena
     for (int e = 0; e < 4; ++e) {
       if (tok0 + e >= len) {
 #pragma unroll
-        for (int i = 0; i < VW; ++i) pg.v[e][i] = 0u;
+        for (int h = 0; h < HPW; ++h)
+#pragma unroll
+          for (int i = 0; i < VW; ++i) pg[h].v[e][i] = 0u;
       }
     }
   }
@@ -414,18 +430,28 @@ __device__ __forceinline__ void process_page(WaveState<NB, HD>& st, const typena
                         st.l[nb], pl[nb]);
   }
 
-  // O^T += V^T . P^T, one 16x16x16 MFMA per (dim block, row block). Dim block
-  // mb takes half mb%2 of dword mb/2 from the four token rows this lane holds.
+  // O^T += V^T . P^T, one 16x16x16 MFMA per (dim block, row block, head). Dim
+  // block mb takes half mb%2 of dword mb/2 from the four token rows this lane
+  // holds.
+  const u2 zero = {0u, 0u};
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int j = mb >> 1;
-    const unsigned w0 = pg.v[0][j], w1 = pg.v[1][j], w2 = pg.v[2][j], w3 = pg.v[3][j];
-    const u2 av = (mb & 1) == 0 ? u2{pack_lo(w0, w1), pack_lo(w2, w3)}
-                                : u2{pack_hi(w0, w1), pack_hi(w2, w3)};
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      st.acc[mb][nb] = E::mma_pv(av, ph[nb], st.acc[mb][nb]);
-      if constexpr (E::kSplitP) st.acc[mb][nb] = E::mma_pv(av, pl[nb], st.acc[mb][nb]);
+    for (int h = 0; h < HPW; ++h) {
+      const unsigned w0 = pg[h].v[0][j], w1 = pg[h].v[1][j], w2 = pg[h].v[2][j],
+                     w3 = pg[h].v[3][j];
+      const u2 av = (mb & 1) == 0 ? u2{pack_lo(w0, w1), pack_lo(w2, w3)}
+                                  : u2{pack_hi(w0, w1), pack_hi(w2, w3)};
+      // With two heads, head h's product takes only the probabilities of its
+      // own rows (the other rows' lanes pass zeros).
+      const bool mine = HPW == 1 || (h == 1) == upper;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        st.acc[mb][nb] = E::mma_pv(av, mine ? ph[nb] : zero, st.acc[mb][nb]);
+        if constexpr (E::kSplitP)
+          st.acc[mb][nb] = E::mma_pv(av, mine ? pl[nb] : zero, st.acc[mb][nb]);
+      }
     }
   }
 }
@@ -566,15 +592,17 @@ __device__ ItemRange balanced_item(const PartialArgs& a, int item) {
   return r;
 }
 
-// One workgroup = one (sequence b, split) x WW waves; wave w serves kv head
-// head_group * WW + w with all of its rows (NB blocks of 16); WPE = waves per
-// SIMD the register budget allows. All waves walk the same pages in the same
-// order, so the heads' 256-byte slices of each page are requested together and
-// HBM sees whole 1 KiB (4 heads) runs; the two head groups of a page range are
-// dispatch neighbours. Each wave keeps its own softmax state and writes its
-// own partial (or, with a single split, the output). Every K/V byte is read by
-// one wave only, so the loads are non-temporal.
-template <int NB, int D, int WW, int WPE, int HD, typename E, typename KV>
+// One workgroup = one (sequence b, split) x WW waves; wave w serves the HPW kv
+// heads from (head_group * WW + w) * HPW with all of their rows (NB blocks of
+// 16; with HPW = 2 one block, rows 0-7 of the first head and 8-15 of the
+// second); WPE = waves per SIMD the register budget allows. All waves walk the
+// same pages in the same order, so the heads' 256-byte slices of each page are
+// requested together and HBM sees 1 KiB (4 heads) or 2 KiB (8 heads) runs; the
+// head groups of a page range are dispatch neighbours. Each wave keeps its own
+// softmax state and writes its own partials (or, with a single split, the
+// output). Every K/V byte is read by one wave only, so the loads are
+// non-temporal.
+template <int NB, int D, int WW, int WPE, int HD, typename E, typename KV, int HPW>
 __global__ __launch_bounds__(WW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void sqa_partial_kernel(PartialArgs a) {
   constexpr int KK = Dims<HD>::KK, MB = Dims<HD>::MB;
@@ -584,13 +612,20 @@ void sqa_partial_kernel(PartialArgs a) {
   const int l16 = lane & 15;
 
   // blockIdx.x = item * head_groups + head_group.
-  const int head_groups = (a.hkv + WW - 1) / WW;
+  const int head_groups = (a.hkv + WW * HPW - 1) / (WW * HPW);
   const int hgrp = blockIdx.x % head_groups;
   const int item = blockIdx.x / head_groups;
-  const int kvh = hgrp * WW + wave;
-  // Waves past the last kv head (hkv not a multiple of WW) idle but stay for
-  // the barrier.
+  const int kvh = (hgrp * WW + wave) * HPW;  // the wave's first kv head
+  // Waves past the last kv head (hkv not a multiple of WW * HPW) idle but stay
+  // for the barrier.
   const bool active = kvh < a.hkv;
+  // Row slot r of block nb (r = 0..15) -> kv head kvh + row_head(r) and row
+  // row_in_head(nb, r) of that head (row = qi * group + g).
+  auto row_head = [](int r) { return HPW == 1 ? 0 : r >> 3; };
+  auto row_in_head = [](int nb, int r) { return HPW == 1 ? nb * 16 + r : (r & 7); };
+  auto slot_real = [&](int nb, int r) {
+    return kvh + row_head(r) < a.hkv && row_in_head(nb, r) < a.rows;
+  };
 
   // Start-up. First: the work item (fixed plan: the sequence length, with the
   // ids of the split's first D pages loaded alongside; balanced plan: all
@@ -649,11 +684,11 @@ void sqa_partial_kernel(PartialArgs a) {
     // Loads are unconditional from an in-bounds address (padding rows and idle
     // waves read row 0 of kv head 0) and the value is selected afterwards, so
     // no lane-divergent branch splits the load stream.
-    const int r = nb * 16 + l16;
-    const bool real = active && r < a.rows;
+    const int r = row_in_head(nb, l16);
+    const bool real = slot_real(nb, l16);
     const int qi = real ? r / a.group : 0;
     const int gg = real ? r - qi * a.group : 0;
-    const int hh = real ? kvh * a.group + gg : 0;
+    const int hh = real ? (kvh + row_head(l16)) * a.group + gg : 0;
     const _Float16* qp = a.q + ((size_t)(b * a.q_len + qi) * a.hq + hh) * HD;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
@@ -694,6 +729,8 @@ void sqa_partial_kernel(PartialArgs a) {
   const unsigned tok_bytes = a.token_stride;
   const unsigned k_lane = l16 * tok_bytes + kvh_c * a.head_stride + KV::k_lane_bytes(g16);
   const unsigned v_lane = 4 * g16 * tok_bytes + kvh_c * a.head_stride + KV::v_lane_bytes(l16);
+  // Offset of the wave's second head (the first head again if it does not exist).
+  const unsigned head1 = HPW == 2 && kvh_c + 1 < a.hkv ? a.head_stride : 0u;
   // pid < 0 gives a zero-length resource: the loads return zeros without
   // touching memory, so every slot refill below is unconditional and the
   // compiler's wait counts stay exact (one page retires per step). K/V are
@@ -701,7 +738,7 @@ void sqa_partial_kernel(PartialArgs a) {
   // Kernel page p of the sequence is sub-page p & sub_mask of cache page
   // block_tables[b][p >> shift].
   const size_t sub_bytes = (size_t)kPageSize * tok_bytes;
-  auto load_page = [&](int pid, int p, typename KV::Regs& pg) {
+  auto load_page = [&](int pid, int p, typename KV::Regs (&pg)[HPW]) {
     const size_t off =
         pid >= 0 ? (size_t)pid * (size_t)a.page_stride + (size_t)(p & sub_mask) * sub_bytes : 0;
     const int nrec = pid >= 0 ? (int)a.page_extent : 0;
@@ -709,11 +746,12 @@ void sqa_partial_kernel(PartialArgs a) {
         (void*)((const char*)a.k + off), (short)0, nrec, kBufferFlags);
     const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)((const char*)a.v + off), (short)0, nrec, kBufferFlags);
-    KV::load(pg, kr, vr, k_lane, v_lane, tok_bytes);
+    KV::load(pg[0], kr, vr, k_lane, v_lane, tok_bytes);
+    if constexpr (HPW == 2) KV::load(pg[HPW - 1], kr, vr, k_lane + head1, v_lane + head1, tok_bytes);
   };
   // Ring of D pages in flight: page i is processed from slot i % D, which is
   // then refilled with page i + D.
-  typename KV::Regs ring[D];
+  typename KV::Regs ring[D][HPW];
 #pragma unroll
   for (int j = 0; j < D; ++j) {
     load_page(j < n_pages ? clamp_page(first_id[j], a.num_pages) : -1, p_begin + j, ring[j]);
@@ -762,8 +800,8 @@ void sqa_partial_kernel(PartialArgs a) {
       if (ii < n_pages) {
         const int p = p_begin + ii;
         const bool masked = (p + 1) * kPageSize > mask_from;
-        process_page<NB, HD, E, KV>(st, ring[j], my_q, lane, dbits, mask_from,
-                                    p * kPageSize + 4 * g16, len, masked, a.scale_log2);
+        process_page<NB, HD, E, KV, HPW>(st, ring[j], my_q, lane, l16 >= 8, dbits, mask_from,
+                                         p * kPageSize + 4 * g16, len, masked, a.scale_log2);
       }
       const int pid = next_pid;
       next_pid = page_id(ii + D + 1);
@@ -785,14 +823,16 @@ void sqa_partial_kernel(PartialArgs a) {
   constexpr int kStageRow = HD + 4;  // floats per staged row; the pad spreads rows over banks
   constexpr int CPR = HD / 4;        // 4-value chunks per row
   float* stage = sm_stage + wave * 16 * kStageRow;
-  const size_t item0 = ((size_t)(it.slot0 + split) * a.hkv + kvh) * a.rows;
+  // Partial item of the kv head of row slot r: [slots, Hkv] items of rows rows.
+  auto item_of = [&](int r) {
+    return ((size_t)(it.slot0 + split) * a.hkv + kvh + row_head(r)) * a.rows;
+  };
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const int rb = min(16, a.rows - 16 * nb);  // rows of this block (uniform)
-    if (rb <= 0) break;
+    if (nb * 16 >= a.rows) break;  // uniform
     const float inv = st.l[nb] > 0.f ? a.out_scale / st.l[nb] : 0.f;
     const float sc = direct ? inv : 1.f;
-    if (l16 < rb) {
+    if (slot_real(nb, l16)) {
       float* dst = stage + l16 * kStageRow + (HD / 4) * g16;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
@@ -820,11 +860,13 @@ void sqa_partial_kernel(PartialArgs a) {
 #pragma unroll
       for (int i = 0; i < CPR / 4; ++i) {
         const int e = i * 64 + lane;
-        const int r = 16 * nb + e / CPR;
-        if (e / CPR < rb) {
+        const int slot = e / CPR;
+        if (slot_real(nb, slot)) {
+          const int r = row_in_head(nb, slot);
           const int qi = r / a.group;
           const int gg = r - qi * a.group;
-          _Float16* op = a.out + ((size_t)(b * a.q_len + qi) * a.hq + kvh * a.group + gg) * HD +
+          _Float16* op = a.out + ((size_t)(b * a.q_len + qi) * a.hq +
+                                  (kvh + row_head(slot)) * a.group + gg) * HD +
                          4 * (e % CPR);
           const float o[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
           *(u2*)op = E::pack4(o);
@@ -834,11 +876,12 @@ void sqa_partial_kernel(PartialArgs a) {
 #pragma unroll
       for (int i = 0; i < CPR / 4; ++i) {
         const int e = i * 64 + lane;
-        if (e / CPR < rb)
-          *(f4*)(a.part_o + (item0 + 16 * nb + e / CPR) * HD + 4 * (e % CPR)) = v[i];
+        const int slot = e / CPR;
+        if (slot_real(nb, slot))
+          *(f4*)(a.part_o + (item_of(slot) + row_in_head(nb, slot)) * HD + 4 * (e % CPR)) = v[i];
       }
-      if (g16 == 0 && l16 < rb) {
-        const size_t pitem = item0 + 16 * nb + l16;
+      if (g16 == 0 && slot_real(nb, l16)) {
+        const size_t pitem = item_of(l16) + row_in_head(nb, l16);
         a.part_ml[pitem * 2 + 0] = st.m[nb];
         a.part_ml[pitem * 2 + 1] = st.l[nb];
       }
@@ -978,13 +1021,21 @@ template <int HD, typename E, typename KV>
 void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
                        hipStream_t stream) {
   constexpr int kScale = (2 / KV::kBytes) * 128;  // 32 KiB / (16 * HD * kBytes * 2) * 4
-  constexpr int D4 = 4 * kScale / HD, D3 = 3 * kScale / HD;
-  if (sh.row_blocks == 1) {
-    hipLaunchKernelGGL((sqa_partial_kernel<1, D4, 4, 1, HD, E, KV>), grid, block, 0, stream, a);
+  constexpr int D4 = 4 * kScale / HD, D3 = 3 * kScale / HD, D2 = 2 * kScale / HD;
+  if (sh.hpw == 2) {
+    // Two heads per wave: half the pages in flight, each twice the bytes.
+    if constexpr (HD == 64)
+      hipLaunchKernelGGL((sqa_partial_kernel<1, D2, 4, 1, HD, E, KV, 2>), grid, block, 0, stream,
+                         a);
+  } else if (sh.row_blocks == 1) {
+    hipLaunchKernelGGL((sqa_partial_kernel<1, D4, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
+                       a);
   } else if (sh.row_blocks == 2) {
-    hipLaunchKernelGGL((sqa_partial_kernel<2, D4, 4, 1, HD, E, KV>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((sqa_partial_kernel<2, D4, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
+                       a);
   } else if constexpr (HD != 256) {
-    hipLaunchKernelGGL((sqa_partial_kernel<4, D3, 4, 1, HD, E, KV>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((sqa_partial_kernel<4, D3, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
+                       a);
   }
 }
 
@@ -1027,10 +1078,10 @@ void launch_merge_as(const MergeArgs& a, int per_row, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
-  const LaunchShape sh = launch_shape(a.rows);
+  const LaunchShape sh = launch_shape(a.rows, a.hkv, a.head_dim);
   const int head_groups = (a.hkv + sh.heads - 1) / sh.heads;
   const dim3 grid((unsigned)(plan_slots(a.batch, a.num_splits, a.pages_per_split) * head_groups));
-  const dim3 block(sh.heads * 64);
+  const dim3 block(sh.waves() * 64);
   if (a.bf16) {
     if (a.kv_fp8)
       launch_partial_as<ElemBF16, KvFp8>(a, sh, grid, block, stream);

@@ -205,7 +205,7 @@ def _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
     # The plan counts 16-token kernel pages.
     kernel_pages = block_tables.shape[1] * (key_cache.shape[1] // PAGE_SIZE)
     num_splits, pps = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv,
-                                       int(max_seq_len), kernel_pages, ck)
+                                       query.shape[-1], int(max_seq_len), kernel_pages, ck)
     if _tracing():
         # Under torch.compile / export the registered custom op is the traceable unit.
         return _lib.custom_op()(query, key_cache, value_cache, block_tables, seq_lens,

@@ -112,8 +112,9 @@ def _run(query, k, v, block_tables, seq_lens, max_seq_len: int, q_len: int, scal
     elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor shaped and typed like query")
     if plan is None:
-        plan = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv, int(max_seq_len),
-                                block_tables.shape[1] * (k.shape[1] // PAGE_SIZE), 0)
+        plan = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv, d,
+                                int(max_seq_len), block_tables.shape[1] * (k.shape[1] // PAGE_SIZE),
+                                0)
     ns, pps = plan
     need = _lib.workspace_bytes(batch, q_len, hq, hkv, d, ns, pps)
     ws = None
@@ -245,7 +246,7 @@ class _PagedWrapper:
         batch = block_tables.shape[0]
         max_seq_len = int(seq_lens.max()) if batch else 0
         plan = _lib.plan_splits(block_tables.device.index or 0, batch, q_len, num_qo_heads,
-                                num_kv_heads, max(max_seq_len, 1),
+                                num_kv_heads, head_dim, max(max_seq_len, 1),
                                 block_tables.shape[1] * (page_size // PAGE_SIZE), 0)
         need = _lib.workspace_bytes(batch, q_len, num_qo_heads, num_kv_heads, head_dim, *plan)
         if need and self._workspace is not None:

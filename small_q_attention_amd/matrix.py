@@ -112,8 +112,8 @@ def measure_case(torch, variant, case, page_mode, chunk_keys, warmup, repeats, s
     q, k, v, bt, sl = sets[0]
     plan_ck = 0 if ck is None else ck
     max_seq = case["kv_len"] if variant not in ("v0", "v1") else 0
-    ns, pps = _lib.plan_splits(0, c.batch, c.q_len, c.num_query_heads, c.num_kv_heads, max_seq,
-                               bt.shape[1], plan_ck)
+    ns, pps = _lib.plan_splits(0, c.batch, c.q_len, c.num_query_heads, c.num_kv_heads,
+                               c.head_dim, max_seq, bt.shape[1], plan_ck)
     nbytes = _lib.workspace_bytes(c.batch, c.q_len, c.num_query_heads, c.num_kv_heads,
                                   c.head_dim, ns, pps)
     ws = torch.empty(max(1, nbytes), dtype=torch.uint8, device="cuda")

@@ -64,13 +64,13 @@ def test_workspace_bytes(lib):
 
 
 def _plan(lib, **kw):
-    args = dict(device=0, batch=4, q_len=4, hq=32, hkv=8, max_seq_len=8192, max_pages=512,
-                chunk_keys=512)
+    args = dict(device=0, batch=4, q_len=4, hq=32, hkv=8, hd=128, max_seq_len=8192,
+                max_pages=512, chunk_keys=512)
     args.update(kw)
     ns, pps = ctypes.c_int(-7), ctypes.c_int(-7)
     rc = lib.sqa_plan_splits(args["device"], args["batch"], args["q_len"], args["hq"], args["hkv"],
-                             args["max_seq_len"], args["max_pages"], args["chunk_keys"],
-                             ctypes.byref(ns), ctypes.byref(pps))
+                             args["hd"], args["max_seq_len"], args["max_pages"],
+                             args["chunk_keys"], ctypes.byref(ns), ctypes.byref(pps))
     return rc, ns.value, pps.value
 
 
@@ -90,7 +90,7 @@ def test_plan_rejects_bad_arguments(lib):
     assert _plan(lib, batch=0)[0] == SQA_ERR_INVALID
     assert _plan(lib, chunk_keys=-1)[0] == SQA_ERR_INVALID
     assert _plan(lib, max_pages=0)[0] == SQA_ERR_INVALID
-    rc = lib.sqa_plan_splits(0, 1, 2, 32, 8, 16, 1, 16, None, None)
+    rc = lib.sqa_plan_splits(0, 1, 2, 32, 8, 128, 16, 1, 16, None, None)
     assert rc == SQA_ERR_INVALID
 
 

@@ -99,7 +99,7 @@ def test_draft_masks(q_len):
     assert_parity(got, _oracle(q, k, v, bt, sl, draft_mask=tree), label="tree")
     # Explicit fixed plans (several splits per sequence) agree with the automatic one.
     for ck in (32, 512):
-        ns, pps = _lib.plan_splits(0, B, q_len, 32, 8, max(lens), bt.shape[1], ck)
+        ns, pps = _lib.plan_splits(0, B, q_len, 32, 8, 128, max(lens), bt.shape[1], ck)
         out = torch.empty_like(q)
         words = torch.from_numpy(tree.numpy().view(np.int32)).cuda()
         wsb = torch.empty(max(1, _lib.workspace_bytes(B, q_len, 32, 8, 128, ns, pps)),

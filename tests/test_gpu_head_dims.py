@@ -114,6 +114,38 @@ def test_fp8_cache(d, q_len, qdt):
     assert_parity(out.view_as(q), ref, label=f"fp8 d{d} q{q_len} {qdt}")
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (64, 16)])
+def test_two_heads_per_wave(hq, hkv):
+    """Head dim 64 with 8 rows per kv head runs two kv heads per wave (rows 0-7 and
+    8-15 of one block): tree masks, scales, one and two head groups, B1 and ragged
+    batches, every plan."""
+    q_len, d = 2, 64
+    lens = [2, 9, 700, 3000]
+    c = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=2600 + hkv,
+                    num_query_heads=hq, num_kv_heads=hkv, head_dim=d)
+    q, k, v, bt, sl = (t.cuda() for t in inputs.make_inputs(c))
+    g = torch.Generator().manual_seed(26)
+    vis = torch.rand(len(lens), q_len, q_len, generator=g) < 0.5
+    vis[:, torch.arange(q_len), torch.arange(q_len)] = True
+    mask = pack_draft_mask(vis)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    kv = torch.stack([k, v], 1).contiguous()
+    out = fi.xqa_batch_decode_with_kv_cache(q.reshape(-1, hq, d), kv, ws, bt, sl, max(lens),
+                                            0.09, 0.8, q_len_per_req=q_len, mask=mask.cuda())
+    ref = attention_c64(q.cpu(), k.cpu(), v.cpu(), bt.cpu(), sl.cpu(), 16, hkv,
+                        draft_mask=mask, scale=0.09, out_scale=0.8)
+    assert_parity(out.view_as(q), ref, label=f"hq{hq} hkv{hkv} tree")
+    plain = attention_c64(q.cpu(), k.cpu(), v.cpu(), bt.cpu(), sl.cpu(), 16, hkv)
+    for ck in (None, 64, 1 << 20):
+        got = sqa.paged_mtp_attention(q, k, v, bt, sl, 16, max(lens), chunk_keys=ck)
+        assert_parity(got, plain, label=f"hq{hq} hkv{hkv} ck{ck}")
+    one = inputs.Case(batch=1, q_len=q_len, seq_lens=[4500], seed=27, num_query_heads=hq,
+                      num_kv_heads=hkv, head_dim=d)
+    t1 = tuple(t.cuda() for t in inputs.make_inputs(one))
+    assert_parity(sqa.paged_mtp_attention(*t1, 16),
+                  attention_c64(*(x.cpu() for x in t1), 16, hkv), label=f"hq{hq} hkv{hkv} B1")
+
+
 def test_wrapper_plan_checks_head_dim():
     d, q_len, lens = 64, 4, [50, 300]
     q, k, v, bt, sl = _inputs(lens, q_len, d, 2500)

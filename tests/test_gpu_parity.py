@@ -121,7 +121,7 @@ def test_balanced_plan_on_a_skewed_batch(q_len):
     case = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=400 + q_len)
     tensors = _to_gpu(inputs.make_inputs(case))
     bt = tensors[3]
-    ns, pps = _lib.plan_splits(0, len(lens), q_len, 32, 8, max(lens), bt.shape[1], 0)
+    ns, pps = _lib.plan_splits(0, len(lens), q_len, 32, 8, 128, max(lens), bt.shape[1], 0)
     assert pps == 0 and ns > len(lens)
     ref = _oracle(tensors)
     out = sqa.paged_mtp_attention(*tensors, 16, max(lens))
@@ -143,7 +143,7 @@ def test_balanced_plan_at_the_batch_limit():
         wide = torch.zeros(batch, 4096, dtype=torch.int32)  # 2x the cap: slots >= 2 * batch
         wide[:, :bt.shape[1]] = bt
         tensors = _to_gpu((q, k, v, wide, sl))
-        ns, pps = _lib.plan_splits(0, batch, 4, 32, 8, 0, 4096, 0)
+        ns, pps = _lib.plan_splits(0, batch, 4, 32, 8, 128, 0, 4096, 0)
         if batch == 256:
             assert pps == 0 and ns >= batch + batch * 4096 // 2048
         else:
@@ -281,7 +281,7 @@ def test_custom_op_matches_the_eager_path():
     and its fake implementation shapes the output without running anything."""
     case = inputs.Case(batch=3, q_len=8, seq_lens=[900, 40, 2100], seed=19)
     tensors = _to_gpu(inputs.make_inputs(case))
-    ns, pps = _lib.plan_splits(0, 3, 8, 32, 8, 2100, tensors[3].shape[1], 0)
+    ns, pps = _lib.plan_splits(0, 3, 8, 32, 8, 128, 2100, tensors[3].shape[1], 0)
     eager = sqa.paged_mtp_attention(*tensors, 16, 2100)
     _lib.custom_op()  # registers the op
     via_op = torch.ops.sqa.paged_mtp_attention(*tensors, ns, pps)
@@ -300,7 +300,7 @@ def test_c_abi_direct_with_caller_workspace():
     case = inputs.Case(batch=3, q_len=4, seq_lens=[500, 64, 1500], seed=17)
     tensors = _to_gpu(inputs.make_inputs(case))
     q, k, v, bt, sl = tensors
-    ns, pps = _lib.plan_splits(0, 3, 4, 32, 8, 1500, bt.shape[1], 256)
+    ns, pps = _lib.plan_splits(0, 3, 4, 32, 8, 128, 1500, bt.shape[1], 256)
     assert ns > 1
     ws = torch.empty(_lib.workspace_bytes(3, 4, 32, 8, 128, ns, pps), dtype=torch.uint8, device="cuda")
     out = torch.empty_like(q)
