@@ -29,7 +29,9 @@
 // Rows beyond q_len*group (q_len*group not a multiple of 16) carry zero Q and
 // are never stored. The figures above are for head dim 128; the kernels are
 // also built for 64 and 256 (HD), where the per-lane counts scale with HD
-// (Dims<HD>) and a ring slot holds a page of HD-wide rows.
+// (Dims<HD>) and a ring slot holds a page of HD-wide rows, and at head dim 64
+// with up to 8 rows per kv head a wave takes two kv heads (HPW = 2, rows 0-7
+// and 8-15 of its one block; a workgroup then serves 8 kv heads).
 #include "sqa_internal.h"
 
 #include <math.h>
