@@ -1018,12 +1018,16 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
 // pages of 16-bit elements at head dim 128 (3 at 64 rows, where the registers
 // run out), proportionally more pages when a page holds fewer bytes (e4m3
 // caches, head dim 64) and fewer at head dim 256, which holds at most 32 rows
-// (its accumulators double).
+// (its accumulators double). At 64 rows an e4m3 ring stays at 3 pages: the
+// widened K and V fragments take the registers a deeper ring would need
+// (measured at 16 rows per head and 32K keys, head dim 128: 260 us at 3 pages,
+// 278 us at 6; head dim 64: 169 us at 3, 185 us at 12).
 template <int HD, typename E, typename KV>
 void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
                        hipStream_t stream) {
   constexpr int kScale = (2 / KV::kBytes) * 128;  // 32 KiB / (16 * HD * kBytes * 2) * 4
-  constexpr int D4 = 4 * kScale / HD, D3 = 3 * kScale / HD, D2 = 2 * kScale / HD;
+  constexpr int D4 = 4 * kScale / HD, D2 = 2 * kScale / HD;
+  constexpr int D3 = KV::kBytes == 1 ? 3 : 3 * kScale / HD;
   if (sh.hpw == 2) {
     // Two heads per wave: half the pages in flight, each twice the bytes.
     if constexpr (HD == 64)
