@@ -11,7 +11,9 @@ call (KV bytes / mean call time); ``roofline`` uses the partial kernel's own
 mean duration from HIP events the library records around it on the launch
 stream; ``cpu_baseline`` times the loop-faithful CPU oracle on a bounded
 sample of the same workload. ``per_q_len`` repeats the timing at q_len 2, 4
-and 16 on the same KV pool.
+and 16 on the same KV pool. ``roofline.read_probe`` is the practical read
+ceiling: the library's streaming-read probe over ~2 GiB of the same resident
+pool (``frac_of_read_probe`` = the partial kernel's rate over it).
 """
 
 from __future__ import annotations
@@ -106,6 +108,29 @@ def time_calls(torch, lib, tensors, plan, steps, warmup):
     part = [kev[3 * i].elapsed_time(kev[3 * i + 1]) for i in range(steps)]
     merge = [kev[3 * i + 1].elapsed_time(kev[3 * i + 2]) for i in range(steps)]
     return total_ms / steps, statistics.mean(part), statistics.mean(merge), out
+
+
+def read_probe(torch, lib, pool, steps):
+    """The practical HBM read ceiling: ``sqa_read_probe`` (one workgroup per CU,
+    contiguous chunks, 16-byte non-temporal loads) over the first ~2 GiB of the
+    resident K pool, `steps` passes between two events. Returns (GB/s, bytes, us)."""
+    blocks = lib.load().sqa_device_cu_count(0)
+    flat = pool.view(-1).view(torch.uint8)
+    unit = 16 * 256 * blocks
+    nbytes = min(flat.numel(), 1 << 31) // unit * unit
+    data = flat[:nbytes]
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=pool.device)
+    handle = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        lib.read_probe(data, sink, blocks, handle)
+    start, end = _events(torch, 2)
+    start.record()
+    for _ in range(steps):
+        lib.read_probe(data, sink, blocks, handle)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / steps
+    return nbytes / (us * 1e-6) / 1e9, nbytes, us
 
 
 def _ramp_clocks(torch, lib, tensors, plan, seconds=0.25):
@@ -267,6 +292,11 @@ def main():
             "merge_us": round(merge_ms * 1e3, 2),
         },
     }
+    probe_gbps, probe_bytes, probe_us = read_probe(torch, _lib, k, args.steps)
+    result["roofline"]["read_probe"] = {
+        "GBps": round(probe_gbps, 1), "bytes": probe_bytes, "us": round(probe_us, 2),
+        "frac_of_peak": round(probe_gbps / PEAK_HBM_GBPS, 4)}
+    result["roofline"]["frac_of_read_probe"] = round(achieved / probe_gbps, 4)
     if not args.no_per_q:
         extra = {}
         for ql in (2, 4, 16):

@@ -181,6 +181,17 @@ typedef struct sqa_attention_args {
  */
 int sqa_paged_attention(const sqa_attention_args* args);
 
+/*
+ * Streaming-read probe. No counterpart in the reference: a measurement aid that
+ * gives the practical HBM read rate the attention kernels are compared with.
+ * Reads the `bytes` bytes at `data` once (`blocks` workgroups of 256 threads,
+ * each over one contiguous chunk, 16-byte non-temporal loads) and writes one
+ * dword per thread to `sink` (blocks * 256 dwords). `data` 16-byte aligned,
+ * `bytes` a positive multiple of 16 * blocks, 1 <= blocks <= 65536, `sink` 4-byte
+ * aligned. Asynchronous on `stream`; SQA_ERR_INVALID or SQA_ERR_HIP otherwise.
+ */
+int sqa_read_probe(const void* data, size_t bytes, unsigned* sink, int blocks, void* stream);
+
 /* Compute units of `device` (256 on MI355X), or -1 on error. */
 int sqa_device_cu_count(int device);
 

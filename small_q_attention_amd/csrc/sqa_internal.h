@@ -121,5 +121,9 @@ inline LaunchShape launch_shape(int rows, int hkv, int head_dim) {
 
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream);
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream);
+// Streaming read of `bytes` (a multiple of 16 * blocks) in `blocks` contiguous
+// chunks, one dword per thread (blocks * 256) written to `sink`.
+hipError_t launch_read_probe(const void* data, size_t bytes, unsigned* sink, int blocks,
+                             hipStream_t stream);
 
 }  // namespace sqa

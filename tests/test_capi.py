@@ -186,3 +186,19 @@ def test_general_entry_struct_matches_the_header(lib):
     # (and is then refused for a missing workspace, before any device access).
     assert _general(lib, struct_size=ctypes.sizeof(_lib.AttentionArgs) - 8) == SQA_ERR_INVALID
     assert _general(lib, num_splits=2) == SQA_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("args,msg", [
+    ((0, 4096, 4096, 1), "null pointer"),
+    ((4096, 4096, 0, 1), "null pointer"),
+    ((4096, 4096, 4096, 0), "blocks"),
+    ((4096, 4096, 4096, 65537), "blocks"),
+    ((4104, 4096, 4096, 1), "aligned"),
+    ((4096, 4096, 4098, 1), "aligned"),
+    ((4096, 0, 4096, 1), "multiple"),
+    ((4096, 4096 + 16, 4096, 2), "multiple"),
+])
+def test_read_probe_rejects_bad_arguments_without_a_gpu(lib, args, msg):
+    data, nbytes, sink, blocks = args
+    assert lib.sqa_read_probe(data, nbytes, sink, blocks, None) == SQA_ERR_INVALID
+    assert msg in lib.sqa_last_error().decode()
