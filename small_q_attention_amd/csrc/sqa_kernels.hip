@@ -1014,20 +1014,21 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   *(u2*)(a.out + (size_t)row * HD + 4 * c) = E::pack4(out);
 }
 
-// Ring depth: the pages in flight per wave hold about 32 KiB of K and V, 4
-// pages of 16-bit elements at head dim 128 (3 at 64 rows, where the registers
-// run out), proportionally more pages when a page holds fewer bytes (e4m3
-// caches, head dim 64) and fewer at head dim 256, which holds at most 32 rows
-// (its accumulators double). At 64 rows an e4m3 ring stays at 3 pages: the
-// widened K and V fragments take the registers a deeper ring would need
-// (measured at 16 rows per head and 32K keys, head dim 128: 260 us at 3 pages,
-// 278 us at 6; head dim 64: 169 us at 3, 185 us at 12).
+// Ring depth: the pages in flight per wave hold about 32 KiB of 16-bit K and
+// V: 4 pages at head dim 128 (3 at 64 rows, where the registers run out), 8 at
+// head dim 64 and 2 at 256, which holds at most 32 rows (its accumulators
+// double). e4m3 caches keep the same page counts although their pages hold
+// half the bytes, and 3 pages at 64 rows at head dim 64 too: the widened K and
+// V fragments take the registers a deeper ring would need. Measured at 16
+// sequences of 32K keys, partial kernel, e4m3 ring at twice these depths ->
+// these: head dim 128 q2 / q8 / q16 170.7 / 181.4 / 278 -> 169.7 / 174.2 /
+// 261 us; head dim 256 q8 342.7 -> 325.1 us; head dim 64 q4 / q8 / q16
+// 104.2 / 119.8 / 185 -> 100.7 / 116.6 / 169 us.
 template <int HD, typename E, typename KV>
 void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
                        hipStream_t stream) {
-  constexpr int kScale = (2 / KV::kBytes) * 128;  // 32 KiB / (16 * HD * kBytes * 2) * 4
-  constexpr int D4 = 4 * kScale / HD, D2 = 2 * kScale / HD;
-  constexpr int D3 = KV::kBytes == 1 ? 3 : 3 * kScale / HD;
+  constexpr int D4 = 4 * 128 / HD, D2 = 2 * 128 / HD;
+  constexpr int D3 = KV::kBytes == 1 ? 3 : 3 * 128 / HD;
   if (sh.hpw == 2) {
     // Two heads per wave: half the pages in flight, each twice the bytes.
     if constexpr (HD == 64)
