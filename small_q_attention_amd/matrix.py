@@ -10,7 +10,8 @@ same way (events around the Python call, warmup then repeats,
 are appended to ``--output`` as they complete. Added columns:
 
 * ``kernel_p50_us`` / ``merge_p50_us``: partial and merge kernels alone, from
-  HIP events the library records around them on the launch stream;
+  HIP events the library records around them on the launch stream, timed
+  after ~0.1 s of back-to-back calls (clocks settled);
 * ``kv_bytes``, ``kv_GBps`` and ``pct_peak`` (KV bytes over ``kernel_p50_us``),
   ``call_GBps`` (over ``p50_us``), ``num_splits``, ``pages_per_split``;
 * ``pools``: KV sets smaller than the 256 MB MALL are rotated through this many
@@ -28,6 +29,7 @@ import itertools
 import json
 import statistics
 import sys
+import time
 from pathlib import Path
 
 PEAK_HBM_GBPS = 8000.0
@@ -120,7 +122,13 @@ def measure_case(torch, variant, case, page_mode, chunk_keys, warmup, repeats, s
     outs = [torch.empty_like(s[0]) for s in sets]
     stream = torch.cuda.current_stream().cuda_stream
     evs = _events(torch, 3 * repeats)
-    torch.cuda.synchronize()
+    # The synchronised calls above leave the GPU idle between calls; ~0.1 s of
+    # back-to-back calls first lets the clocks settle, as bench.py does.
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.1:
+        for i in range(4):
+            _lib.launch(*sets[i % pools], outs[i % pools], ws, ns, pps, stream)
+        torch.cuda.synchronize()
     for i in range(repeats):
         s = sets[i % pools]
         _lib.launch(*s, outs[i % pools], ws, ns, pps, stream,
