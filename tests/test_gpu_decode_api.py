@@ -71,6 +71,29 @@ def test_interleaved_layouts_give_the_same_bits(q_len):
     assert_parity(base, _oracle(q, k, v, bt, sl), label=f"q{q_len}")
 
 
+def test_every_q_len_up_to_16():
+    """Every draft length 1..16 (4 to 64 rows per kv head at GQA 4): one, two and four
+    16-row blocks per wave with their padding rows, the causal chain and a random tree,
+    on sequences from the draft length itself up to a few pages."""
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    for q_len in range(1, 17):
+        lens = [q_len, q_len + 16, 700, 2500 + q_len]
+        q, k, v, bt, sl = _inputs(lens, q_len, seed=650 + q_len)
+        nhd = _nhd(k, v)
+        g = torch.Generator().manual_seed(650 + q_len)
+        vis = torch.rand(len(lens), q_len, q_len, generator=g) < 0.4
+        vis[:, torch.arange(q_len), torch.arange(q_len)] = True
+        tree = pack_draft_mask(vis)
+        for mask in (None, tree):
+            out = fi.xqa_batch_decode_with_kv_cache(_flat(q), nhd, ws, bt, sl, max(lens),
+                                                    128 ** -0.5, 1.0, q_len_per_req=q_len,
+                                                    mask=None if mask is None else mask.cuda())
+            torch.cuda.synchronize()
+            ref = _oracle(q, k, v, bt, sl, draft_mask=mask)
+            assert_parity(out.view_as(q), ref,
+                          label=f"q{q_len} {'tree' if mask is not None else 'causal'}")
+
+
 @pytest.mark.parametrize("q_len", [2, 4, 8, 16])
 def test_draft_masks(q_len):
     """Causal packed mask = the default chain (same bits); full and random tree masks vs
