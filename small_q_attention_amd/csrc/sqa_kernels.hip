@@ -190,13 +190,7 @@ struct Dims {
 // 4*(l/16) + 0..3, dims (HD/16)*(l%16) + 0..HD/16-1. The head dims of K
 // fragment kk are q_dims(kk, l/16) + 0..7 (Q is loaded with the same map, so
 // the QK contraction is unchanged); V and the output mapping are the same for
-// every storage type. expand() hands the MFMAs 16-bit elements.
-// One page of K and V in the query's 16-bit type (what the MFMAs take).
-template <int HD>
-struct PageVals {
-  u4 k[Dims<HD>::KK];
-  unsigned v[4][Dims<HD>::VW];
-};
+// every storage type. expand_k() / expand_v() hand the MFMAs 16-bit elements.
 
 template <int HD>
 struct KvNative {  // the query's 16-bit type
@@ -234,13 +228,16 @@ struct KvNative {  // the query's 16-bit type
     }
   }
   template <typename E>
-  static __device__ __forceinline__ void expand(const Regs& r, PageVals<HD>& pg) {
+  static __device__ __forceinline__ void expand_k(const Regs& r, u4 (&k)[KK]) {
 #pragma unroll
-    for (int i = 0; i < KK; ++i) pg.k[i] = r.k[i];
+    for (int i = 0; i < KK; ++i) k[i] = r.k[i];
+  }
+  template <typename E>
+  static __device__ __forceinline__ void expand_v(const Regs& r, unsigned (&v)[4][VW]) {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int i = 0; i < VW; ++i) pg.v[e][i] = r.v[e][i];
+      for (int i = 0; i < VW; ++i) v[e][i] = r.v[e][i];
   }
 };
 
@@ -283,19 +280,22 @@ struct KvFp8 {  // OCP e4m3 bytes, widened exactly to the query's type
     }
   }
   template <typename E>
-  static __device__ __forceinline__ void expand(const Regs& r, PageVals<HD>& pg) {
+  static __device__ __forceinline__ void expand_k(const Regs& r, u4 (&k)[KK]) {
 #pragma unroll
     for (int i = 0; i < KK / 2; ++i) {
-      pg.k[2 * i] = E::widen_fp8(u2{r.k[i][0], r.k[i][1]});
-      pg.k[2 * i + 1] = E::widen_fp8(u2{r.k[i][2], r.k[i][3]});
+      k[2 * i] = E::widen_fp8(u2{r.k[i][0], r.k[i][1]});
+      k[2 * i + 1] = E::widen_fp8(u2{r.k[i][2], r.k[i][3]});
     }
+  }
+  template <typename E>
+  static __device__ __forceinline__ void expand_v(const Regs& r, unsigned (&v)[4][VW]) {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
       for (int i = 0; i < VW / 2; ++i) {
         const u2 w = E::widen_fp8x4(r.v[e][i]);
-        pg.v[e][2 * i] = w[0];
-        pg.v[e][2 * i + 1] = w[1];
+        v[e][2 * i] = w[0];
+        v[e][2 * i + 1] = w[1];
       }
   }
 };
@@ -332,31 +332,48 @@ __device__ __forceinline__ unsigned pack_hi(unsigned a, unsigned b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
-// One 16-token page for one wave. sm_q: Q fragments in LDS, [nb][kk][lane]
-// (the B-operand layout). c = softmax scale * log2(e); scores stay raw until
-// the exponent, where the scale and the running max meet in one FMA.
-// Visibility on masked pages: token t < len is seen by a row when it lies
-// before the draft block (t < draft_base = len - q_len) or when bit
-// t - draft_base of the row's draft bits is set.
+// One 16-token page for one wave, in two steps: page_scores() runs the QK
+// products, page_finish() masks, updates the softmax state and runs the PV
+// products. The pipelined loop issues the next page's scores before this
+// page's finish, so those MFMAs run under the softmax.
+// sm_q: Q fragments in LDS, [nb][kk][lane] (the B-operand layout).
 // HPW = 2 (one 16-row block, rows 0-7 of kv head 0 of the wave and rows 8-15
 // of head 1): the QK and PV products run once per head over all 16 rows; each
 // lane keeps the scores of its own row's head (`upper`: row >= 8), and each
 // head's PV product gets the probabilities of its own rows only, so both land
 // in the one set of accumulators.
-template <int NB, int HD, typename E, typename KV, int HPW>
-__device__ __forceinline__ void process_page(WaveState<NB, HD>& st,
-                                             const typename KV::Regs (&raw)[HPW],
-                                             const u4* sm_q, int lane, bool upper,
-                                             const unsigned long long (&dbits)[NB],
-                                             int draft_base, int tok0, int len, bool masked,
-                                             float c) {
-  constexpr int KK = Dims<HD>::KK, MB = Dims<HD>::MB, VW = Dims<HD>::VW;
-  static_assert(HPW == 1 || NB == 1, "two heads per wave share one 16-row block");
-  PageVals<HD> pg[HPW];
+// A page's K and V widened to the MFMAs' 16-bit type (a register copy for
+// 16-bit caches).
+template <int HD, int HPW>
+struct PageK {
+  u4 k[HPW][Dims<HD>::KK];
+};
+template <int HD, int HPW>
+struct PageV {
+  unsigned v[HPW][4][Dims<HD>::VW];
+};
+
+template <typename E, typename KV, int HD, int HPW>
+__device__ __forceinline__ PageK<HD, HPW> widen_k(const typename KV::Regs (&raw)[HPW]) {
+  PageK<HD, HPW> kf;
 #pragma unroll
-  for (int h = 0; h < HPW; ++h) KV::template expand<E>(raw[h], pg[h]);
+  for (int h = 0; h < HPW; ++h) KV::template expand_k<E>(raw[h], kf.k[h]);
+  return kf;
+}
+template <typename E, typename KV, int HD, int HPW>
+__device__ __forceinline__ PageV<HD, HPW> widen_v(const typename KV::Regs (&raw)[HPW]) {
+  PageV<HD, HPW> pv;
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) KV::template expand_v<E>(raw[h], pv.v[h]);
+  return pv;
+}
+
+template <int NB, int HD, typename E, typename KV, int HPW>
+__device__ __forceinline__ void page_scores(f4 (&s)[NB], const PageK<HD, HPW>& kf,
+                                            const u4* sm_q, int lane, bool upper) {
+  constexpr int KK = Dims<HD>::KK;
+  static_assert(HPW == 1 || NB == 1, "two heads per wave share one 16-row block");
   // Raw scores S^T[token][row] = K . Q^T for this page.
-  f4 s[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     s[nb] = f4{0.f, 0.f, 0.f, 0.f};
@@ -364,14 +381,28 @@ __device__ __forceinline__ void process_page(WaveState<NB, HD>& st,
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const u4 qf = sm_q[(nb * KK + kk) * 64 + lane];
-      s[nb] = E::mma_qk(pg[0].k[kk], qf, s[nb]);
-      if constexpr (HPW == 2) s1 = E::mma_qk(pg[HPW - 1].k[kk], qf, s1);
+      s[nb] = E::mma_qk(kf.k[0][kk], qf, s[nb]);
+      if constexpr (HPW == 2) s1 = E::mma_qk(kf.k[HPW - 1][kk], qf, s1);
     }
     if constexpr (HPW == 2) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) s[nb][e] = upper ? s1[e] : s[nb][e];
     }
   }
+}
+
+// c = softmax scale * log2(e); scores stay raw until the exponent, where the
+// scale and the running max meet in one FMA. Visibility on masked pages: token
+// t < len is seen by a row when it lies before the draft block
+// (t < draft_base = len - q_len) or when bit t - draft_base of the row's draft
+// bits is set.
+template <int NB, int HD, typename E, typename KV, int HPW>
+__device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
+                                            PageV<HD, HPW>& pv, bool upper,
+                                            const unsigned long long (&dbits)[NB],
+                                            int draft_base, int tok0, int len, bool masked,
+                                            float c) {
+  constexpr int MB = Dims<HD>::MB, VW = Dims<HD>::VW;
   if (masked) {
     // tok0 = absolute index of this lane's first token (4 consecutive tokens).
 #pragma unroll
@@ -395,7 +426,7 @@ __device__ __forceinline__ void process_page(WaveState<NB, HD>& st,
 #pragma unroll
         for (int h = 0; h < HPW; ++h)
 #pragma unroll
-          for (int i = 0; i < VW; ++i) pg[h].v[e][i] = 0u;
+          for (int i = 0; i < VW; ++i) pv.v[h][e][i] = 0u;
       }
     }
   }
@@ -441,8 +472,8 @@ __device__ __forceinline__ void process_page(WaveState<NB, HD>& st,
     const int j = mb >> 1;
 #pragma unroll
     for (int h = 0; h < HPW; ++h) {
-      const unsigned w0 = pg[h].v[0][j], w1 = pg[h].v[1][j], w2 = pg[h].v[2][j],
-                     w3 = pg[h].v[3][j];
+      const unsigned w0 = pv.v[h][0][j], w1 = pv.v[h][1][j], w2 = pv.v[h][2][j],
+                     w3 = pv.v[h][3][j];
       const u2 av = (mb & 1) == 0 ? u2{pack_lo(w0, w1), pack_lo(w2, w3)}
                                   : u2{pack_hi(w0, w1), pack_hi(w2, w3)};
       // With two heads, head h's product takes only the probabilities of its
@@ -794,7 +825,23 @@ void sqa_partial_kernel(PartialArgs a) {
 
   __syncthreads();  // sm_q and sm_ids written
 
+  // With two or four row blocks whose accumulators take at most 64 VGPRs
+  // (NB * HD <= 256) the page loop is software-pipelined: the scores of page
+  // i + 1 are issued before page i's mask, softmax and PV products, so their
+  // MFMAs run under the softmax (16 x 32K keys, head dim 64: q16 177.7 -> 173.8
+  // us, e4m3 q8 / q16 117.2 / 168.5 -> 111.6 / 154.2 us; head dim 128 q8 317.5
+  // -> 316.1 us; bit-identical results). Page i + 1 must then be resident one
+  // step earlier and its scores held alongside: with 128 accumulator VGPRs
+  // (head dim 128 at 64 rows) the extra registers spill (e4m3 q16 261 -> 269
+  // us), with a ring of 2 the wait is longer (head dim 256: 662 -> 916 us),
+  // and at one block there is little softmax to hide (e4m3 head dim 64 q4:
+  // -1.5%).
+  constexpr bool kPipelined = NB >= 2 && D >= 3 && NB * HD <= 256;
+  const bool upper = l16 >= 8;
   int next_pid = page_id(D);
+  f4 s_cur[NB];
+  if constexpr (kPipelined)
+    page_scores<NB, HD, E, KV, HPW>(s_cur, widen_k<E, KV, HD, HPW>(ring[0]), my_q, lane, upper);
   for (int i = 0; i < n_pages; i += D) {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
@@ -802,8 +849,25 @@ void sqa_partial_kernel(PartialArgs a) {
       if (ii < n_pages) {
         const int p = p_begin + ii;
         const bool masked = (p + 1) * kPageSize > mask_from;
-        process_page<NB, HD, E, KV, HPW>(st, ring[j], my_q, lane, l16 >= 8, dbits, mask_from,
-                                         p * kPageSize + 4 * g16, len, masked, a.scale_log2);
+        if constexpr (kPipelined) {
+          // Slot (j + 1) % D holds page ii + 1 (a zero page past the split).
+          f4 s_next[NB];
+          page_scores<NB, HD, E, KV, HPW>(s_next, widen_k<E, KV, HD, HPW>(ring[(j + 1) % D]),
+                                          my_q, lane, upper);
+          PageV<HD, HPW> pv = widen_v<E, KV, HD, HPW>(ring[j]);
+          page_finish<NB, HD, E, KV, HPW>(st, s_cur, pv, upper, dbits, mask_from,
+                                          p * kPageSize + 4 * g16, len, masked, a.scale_log2);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) s_cur[nb] = s_next[nb];
+        } else {
+          // K and V widened together, then the scores (the order that schedules
+          // best where no pipelining is done).
+          const PageK<HD, HPW> kf = widen_k<E, KV, HD, HPW>(ring[j]);
+          PageV<HD, HPW> pv = widen_v<E, KV, HD, HPW>(ring[j]);
+          page_scores<NB, HD, E, KV, HPW>(s_cur, kf, my_q, lane, upper);
+          page_finish<NB, HD, E, KV, HPW>(st, s_cur, pv, upper, dbits, mask_from,
+                                          p * kPageSize + 4 * g16, len, masked, a.scale_log2);
+        }
       }
       const int pid = next_pid;
       next_pid = page_id(ii + D + 1);
