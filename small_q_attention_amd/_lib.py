@@ -66,8 +66,13 @@ def library_path() -> Path:
 
 
 def load(verbose: bool = False, build_if_missing: bool = True):
-    """Load ``libsqa.so`` (building it first if it does not exist yet)."""
+    """Load ``libsqa.so`` (building it first if it does not exist yet). ``verbose``
+    echoes the library path and the hipcc command that builds it, as the
+    reference's loaders echo their JIT build (``cuda.py:31-36``)."""
     global _LIB
+    if verbose:
+        print(f"[sqa] {_build.LIB_PATH}; build command: {' '.join(_build.build_command())}",
+              flush=True)
     with _LOCK:
         if _LIB is None:
             path = _build.LIB_PATH

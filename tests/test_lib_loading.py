@@ -26,3 +26,11 @@ def test_unloadable_library_raises(fresh_loader):
     # Every entry point goes through the same loader.
     with pytest.raises(RuntimeError):
         _lib.plan_splits(0, 1, 2, 32, 8, 128, 64, 4, 0)
+
+
+def test_verbose_load_echoes_the_build(capsys):
+    from small_q_attention_amd import cuda as sqa
+
+    sqa.load_v3(verbose=True)
+    out = capsys.readouterr().out
+    assert "libsqa.so" in out and "hipcc" in out and "--offload-arch=gfx950" in out
