@@ -31,14 +31,19 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, AMD published peak
 # rocprofv3 FETCH_SIZE + WRITE_SIZE summary of the partial kernel on this workload
-# (calibrated against a plain 1 GiB copy); regenerated with the kernel.
-PROFILE = ROOT / "profiles" / "sqa_partial_kernel_cfg3_b16_q8_kv32768.txt"
+# (calibrated against a plain 1 GiB copy); regenerated with the kernel. The bench
+# line's is profiles/sqa_partial_kernel_cfg3_b16_q8_kv32768.txt.
+def profile_path(config: str, q_len: int, kv_dtype: str) -> Path:
+    shape = {"cfg2": f"cfg2_b4_q{q_len}_kv8192", "cfg3": f"cfg3_b16_q{q_len}_kv32768",
+             "cfg5": f"cfg5_b16_q{q_len}_ragged"}[config]
+    suffix = "" if kv_dtype == "fp16" else f"_{kv_dtype}"
+    return ROOT / "profiles" / f"sqa_partial_kernel_{shape}{suffix}.txt"
 
 
-def _profiled_traffic():
-    """HBM bytes per partial-kernel launch from the committed counter summary, or None."""
+def _profiled_traffic(path: Path):
+    """HBM bytes per partial-kernel launch from a committed counter summary, or None."""
     try:
-        for line in PROFILE.read_text().splitlines():
+        for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch:"):
                 return int(float(line.split(":", 1)[1]))
     except OSError:
@@ -60,6 +65,10 @@ def _parse():
                     help="override the workload's q_len (profiling other rows per kv head)")
     ap.add_argument("--config", default="cfg3", choices=("cfg2", "cfg3", "cfg5"),
                     help="workload (cfg3 is the bench line; others for profiling)")
+    ap.add_argument("--kv-dtype", default="fp16", choices=("fp16", "bf16", "e4m3"),
+                    help="element types of the timed workload (profiling the other kernels): "
+                         "bf16 = bf16 Q/K/V/output, e4m3 = fp16 Q/output over an OCP e4m3 "
+                         "cache; fp16 (the bench line) also reports both as extras")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -71,6 +80,23 @@ def _events(torch, n):
         e.record()  # creates the underlying hipEvent_t
     torch.cuda.synchronize()
     return evs
+
+
+def _caller(torch, lib, tensors):
+    """The C entry for these tensors: ``sqa_paged_mtp_attention`` for fp16 Q/K/V, the
+    general entry (``sqa_paged_attention``) for bf16 or e4m3 caches. Returns
+    ``call(out, ws, num_splits, pages_per_split, stream, timing_events=None)``."""
+    q, k, v, bt, sl = tensors
+    if q.dtype == torch.float16 and k.dtype == torch.float16:
+        def call(out, ws, ns, pps, handle, timing_events=None):
+            lib.launch(q, k, v, bt, sl, out, ws, ns, pps, handle, timing_events=timing_events)
+    else:
+        scale = q.shape[-1] ** -0.5
+
+        def call(out, ws, ns, pps, handle, timing_events=None):
+            lib.launch_general(q, out, k, v, bt, sl, None, scale, 1.0, ns, pps, ws, handle,
+                               timing_events=timing_events)
+    return call
 
 
 def time_calls(torch, lib, tensors, plan, steps, warmup):
@@ -90,20 +116,21 @@ def time_calls(torch, lib, tensors, plan, steps, warmup):
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     stream = torch.cuda.current_stream()
     handle = stream.cuda_stream
+    call = _caller(torch, lib, tensors)
     for _ in range(warmup):
-        lib.launch(q, k, v, bt, sl, out, ws, num_splits, pps, handle)
+        call(out, ws, num_splits, pps, handle)
     kev = _events(torch, 3 * steps)
     start, end = _events(torch, 2)
     torch.cuda.synchronize()
     start.record(stream)
     for _ in range(steps):
-        lib.launch(q, k, v, bt, sl, out, ws, num_splits, pps, handle)
+        call(out, ws, num_splits, pps, handle)
     end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
     for i in range(steps):
-        lib.launch(q, k, v, bt, sl, out, ws, num_splits, pps, handle,
-                   timing_events=[e.cuda_event for e in kev[3 * i:3 * i + 3]])
+        call(out, ws, num_splits, pps, handle,
+             timing_events=[e.cuda_event for e in kev[3 * i:3 * i + 3]])
     torch.cuda.synchronize()
     part = [kev[3 * i].elapsed_time(kev[3 * i + 1]) for i in range(steps)]
     merge = [kev[3 * i + 1].elapsed_time(kev[3 * i + 2]) for i in range(steps)]
@@ -142,10 +169,11 @@ def _ramp_clocks(torch, lib, tensors, plan, seconds=0.25):
                                  plan[0], plan[1])
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     handle = torch.cuda.current_stream().cuda_stream
+    call = _caller(torch, lib, tensors)
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds:
         for _ in range(20):
-            lib.launch(q, k, v, bt, sl, out, ws, plan[0], plan[1], handle)
+            call(out, ws, plan[0], plan[1], handle)
         torch.cuda.synchronize()
 
 
@@ -248,13 +276,20 @@ def main():
         case.q_len = args.q_len
     tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
     q, k, v, bt, sl = tensors
+    if args.kv_dtype == "bf16":
+        q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    elif args.kv_dtype == "e4m3":
+        k, v = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
+    tensors = (q, k, v, bt, sl)
+    default_types = args.kv_dtype == "fp16"
     plan = _lib.plan_splits(0, case.batch, case.q_len, case.num_query_heads, case.num_kv_heads,
                             case.head_dim, case.max_seq_len, bt.shape[1], 0)
     _ramp_clocks(torch, _lib, tensors, plan)
     ms, part_ms, merge_ms, out = time_calls(torch, _lib, tensors, plan, args.steps, args.warmup)
     if not torch.isfinite(out).all():
         raise SystemExit("non-finite output")
-    kvb = inputs.kv_bytes(case.seq_lens, case.num_kv_heads, case.head_dim)
+    prof = profile_path(args.config, case.q_len, args.kv_dtype)
+    kvb = inputs.kv_bytes(case.seq_lens, case.num_kv_heads, case.head_dim) * k.element_size() // 2
     value = kvb / (ms * 1e-3) / 1e9
     achieved = kvb / (part_ms * 1e-3) / 1e9
     result = {
@@ -270,10 +305,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 in/out, fp32 accumulate",
-        "data": "synthetic: N(0,1) fp16 Q/K/V drawn on the device, seeded",
+        "dtype": {"fp16": "fp16 in/out, fp32 accumulate",
+                  "bf16": "bf16 in/out, fp32 accumulate",
+                  "e4m3": "fp16 Q/out over an OCP e4m3 KV cache, fp32 accumulate"}[args.kv_dtype],
+        "data": "synthetic: N(0,1) fp16 Q/K/V drawn on the device, seeded"
+                + ("" if default_types else f", converted to {args.kv_dtype}"),
         "config": {
-            "workload": _describe(args.config, case),
+            "workload": _describe(args.config, case) + ("" if default_types else
+                                                         f", {args.kv_dtype} K/V"),
             "batch": case.batch, "q_len": case.q_len,
             "kv_len": case.seq_lens[0] if len(set(case.seq_lens)) == 1 else "ragged",
             "num_splits": plan[0], "pages_per_split": plan[1],
@@ -285,8 +324,8 @@ def main():
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": _profiled_traffic(),
-            "traffic_source": str(PROFILE.relative_to(ROOT)),
+            "traffic": _profiled_traffic(prof),
+            "traffic_source": str(prof.relative_to(ROOT)),
             "kernel": "sqa_partial_kernel",
             "kernel_us": round(part_ms * 1e3, 2),
             "merge_us": round(merge_ms * 1e3, 2),
@@ -297,7 +336,7 @@ def main():
         "GBps": round(probe_gbps, 1), "bytes": probe_bytes, "us": round(probe_us, 2),
         "frac_of_peak": round(probe_gbps / PEAK_HBM_GBPS, 4)}
     result["roofline"]["frac_of_read_probe"] = round(achieved / probe_gbps, 4)
-    if not args.no_per_q:
+    if not args.no_per_q and default_types:
         extra = {}
         for ql in (2, 4, 16):
             g = torch.Generator(device="cuda").manual_seed(100 + ql)
@@ -364,7 +403,7 @@ def main():
                             "kernel_frac": round(kvb / 2 / (p8 * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
                             "speedup_vs_fp16_kv": round(part_ms / p8, 3)}
         del k8, v8, out8, ws8
-    if not args.no_per_q:
+    if not args.no_per_q and default_types:
         # The other single-GPU BASELINE configs, same timing (extra fields only).
         others = {}
         del tensors, q, k, v, bt, sl, out
@@ -386,7 +425,7 @@ def main():
             torch.cuda.empty_cache()
         result["other_configs"] = others
         tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and default_types:
         result["cpu_baseline"] = cpu_baseline(torch, tensors, case, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
