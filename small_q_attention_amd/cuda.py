@@ -82,7 +82,7 @@ _MODULE = None
 
 def _module(verbose):
     global _MODULE
-    if _MODULE is None:
+    if _MODULE is None or verbose:
         _MODULE = _Module(_load(verbose))
     return _MODULE
 
