@@ -31,7 +31,10 @@
 // also built for 64 and 256 (HD), where the per-lane counts scale with HD
 // (Dims<HD>) and a ring slot holds a page of HD-wide rows, and at head dim 64
 // with up to 8 rows per kv head a wave takes two kv heads (HPW = 2, rows 0-7
-// and 8-15 of its one block; a workgroup then serves 8 kv heads).
+// and 8-15 of its one block; a workgroup then serves 8 kv heads). The element
+// traits swap in the bf16 MFMAs (PV then as one 16x16x32 over P's high and low
+// parts) and e4m3 K/V widened in registers; where the registers allow, the
+// page loop runs the next page's QK products under this page's softmax.
 #include "sqa_internal.h"
 
 #include <math.h>
