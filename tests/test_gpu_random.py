@@ -5,7 +5,8 @@ and GQA group (1-8), head dim (64/128/256), query type (fp16/bf16), cache type
 (the query's or e4m3), cache page (16-256 tokens), cache layout (NHD/HND),
 causal or random tree mask, softmax and output scales, ragged lengths (from the
 draft length itself to a few thousand tokens) and K outliers, and runs
-``xqa_batch_decode_with_kv_cache`` (automatic plan). Bar:
+``xqa_batch_decode_with_kv_cache`` (automatic plan); cases the native entry takes
+also run through ``paged_mtp_attention`` with a random fixed plan. Bar:
 ``|a - r| <= 2e-3 + 1e-2 |r|`` against the oracle rounded to the output type.
 """
 
@@ -16,7 +17,7 @@ import pytest
 import torch
 
 from oracle import attention_c64
-from small_q_attention_amd import decode_api as fi, inputs
+from small_q_attention_amd import cuda as sqa, decode_api as fi, inputs
 from small_q_attention_amd.masks import pack_draft_mask
 from tests._helpers import assert_parity
 
@@ -46,6 +47,7 @@ def draw(i):
             for _ in range(batch)]
     qdt = rng.choice([torch.float16, torch.bfloat16])
     return dict(d=d, hkv=hkv, hq=hkv * group, q_len=q_len, lens=lens, qdt=qdt,
+                chunk=rng.choice([None, 16, 64, 512, 1 << 20]),
                 fp8=rng.random() < 0.3, page=rng.choice([16, 16, 32, 64, 128, 256]),
                 layout=rng.choice(["NHD", "HND"]), tree=rng.random() < 0.4,
                 s1=d ** -0.5 * rng.uniform(0.5, 2.0), s2=rng.uniform(0.5, 2.0),
@@ -88,3 +90,10 @@ def test_random_case(i):
     ref = attention_c64(q, k, v, bt, sl, p["page"], p["hkv"], draft_mask=mask, scale=p["s1"],
                         out_scale=p["s2"])
     assert_parity(out.view_as(q), ref, label=label)
+    # Plain causal cases the native entry takes (q_len 2/4/8/16, 16-bit caches),
+    # with a random fixed plan as well.
+    if not p["fp8"] and not p["tree"] and p["q_len"] in sqa.SUPPORTED_Q_LENS:
+        got = sqa.paged_mtp_attention(q.cuda(), k.cuda(), v.cuda(), bt.cuda(), sl.cuda(),
+                                      p["page"], max(p["lens"]), chunk_keys=p["chunk"])
+        plain = attention_c64(q, k, v, bt, sl, p["page"], p["hkv"])
+        assert_parity(got, plain, label=f"{label} native ck{p['chunk']}")
