@@ -114,7 +114,8 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
     // Each split writes rows x (head_dim + 2) floats per kv head for the merge;
     // past 16 rows that rivals a 4-page split's K/V bytes, so splits start at
     // 8 pages there (single-sequence batches of a few thousand tokens).
-    const long long min_pps = sh.row_blocks > 1 ? 2 * sqa::kMinSplitPages : sqa::kMinSplitPages;
+    const bool past16 = (long long)q_len * (num_query_heads / num_kv_heads) > 16;
+    const long long min_pps = past16 ? 2 * sqa::kMinSplitPages : sqa::kMinSplitPages;
     if (pps < min_pps) pps = min_pps;
   }
   if (pps > pages) pps = pages;

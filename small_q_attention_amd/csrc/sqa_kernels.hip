@@ -30,8 +30,9 @@
 // are never stored. The figures above are for head dim 128; the kernels are
 // also built for 64 and 256 (HD), where the per-lane counts scale with HD
 // (Dims<HD>) and a ring slot holds a page of HD-wide rows, and at head dim 64
-// with up to 8 rows per kv head a wave takes two kv heads (HPW = 2, rows 0-7
-// and 8-15 of its one block; a workgroup then serves 8 kv heads). The element
+// a wave takes two kv heads (HPW = 2; a workgroup then serves 8 kv heads):
+// with up to 8 rows per kv head in one block (rows 0-7 and 8-15), with up to
+// 16 in one block each (NB = 2, block nb = head nb). The element
 // traits swap in the bf16 MFMAs (PV then as one 16x16x32 over P's high and low
 // parts) and e4m3 K/V widened in registers; where the registers allow, the
 // page loop runs the next page's QK products under this page's softmax.
@@ -344,11 +345,12 @@ __device__ __forceinline__ unsigned pack_hi(unsigned a, unsigned b) {
 // products. The pipelined loop issues the next page's scores before this
 // page's finish, so those MFMAs run under the softmax.
 // sm_q: Q fragments in LDS, [nb][kk][lane] (the B-operand layout).
-// HPW = 2 (one 16-row block, rows 0-7 of kv head 0 of the wave and rows 8-15
-// of head 1): the QK and PV products run once per head over all 16 rows; each
-// lane keeps the scores of its own row's head (`upper`: row >= 8), and each
-// head's PV product gets the probabilities of its own rows only, so both land
-// in the one set of accumulators.
+// HPW = 2 with NB = 1 (one 16-row block, rows 0-7 of kv head 0 of the wave
+// and rows 8-15 of head 1): the QK and PV products run once per head over all
+// 16 rows; each lane keeps the scores of its own row's head (`upper`: row >=
+// 8), and each head's PV product gets the probabilities of its own rows only,
+// so both land in the one set of accumulators. HPW = 2 with NB = 2: block nb
+// holds head nb's rows and takes only that head's K and V.
 // A page's K and V widened to the MFMAs' 16-bit type (a register copy for
 // 16-bit caches).
 template <int HD, int HPW>
@@ -379,7 +381,7 @@ template <int NB, int HD, typename E, typename KV, int HPW>
 __device__ __forceinline__ void page_scores(f4 (&s)[NB], const PageK<HD, HPW>& kf,
                                             const u4* sm_q, int lane, bool upper) {
   constexpr int KK = Dims<HD>::KK;
-  static_assert(HPW == 1 || NB == 1, "two heads per wave share one 16-row block");
+  static_assert(HPW == 1 || NB <= 2, "two heads per wave: one shared block or one block each");
   // Raw scores S^T[token][row] = K . Q^T for this page.
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -388,10 +390,14 @@ __device__ __forceinline__ void page_scores(f4 (&s)[NB], const PageK<HD, HPW>& k
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const u4 qf = sm_q[(nb * KK + kk) * 64 + lane];
-      s[nb] = E::mma_qk(kf.k[0][kk], qf, s[nb]);
-      if constexpr (HPW == 2) s1 = E::mma_qk(kf.k[HPW - 1][kk], qf, s1);
+      if constexpr (HPW == 2 && NB == 2) {
+        s[nb] = E::mma_qk(kf.k[nb][kk], qf, s[nb]);  // block nb holds head nb's rows
+      } else {
+        s[nb] = E::mma_qk(kf.k[0][kk], qf, s[nb]);
+        if constexpr (HPW == 2) s1 = E::mma_qk(kf.k[HPW - 1][kk], qf, s1);
+      }
     }
-    if constexpr (HPW == 2) {
+    if constexpr (HPW == 2 && NB == 1) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) s[nb][e] = upper ? s1[e] : s[nb][e];
     }
@@ -486,9 +492,10 @@ __device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
                                   : u2{pack_hi(w0, w1), pack_hi(w2, w3)};
       // With two heads, head h's product takes only the probabilities of its
       // own rows (the other rows' lanes pass zeros).
-      const bool mine = HPW == 1 || (h == 1) == upper;
+      const bool mine = HPW == 1 || NB == 2 || (h == 1) == upper;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
+        if (HPW == 2 && NB == 2 && h != nb) continue;  // block nb: head nb's V only
         st.acc[mb][nb] =
             E::mma_pv(av, mine ? ph[nb] : zero, mine ? pl[nb] : zero, st.acc[mb][nb]);
       }
@@ -634,8 +641,9 @@ __device__ ItemRange balanced_item(const PartialArgs& a, int item) {
 
 // One workgroup = one (sequence b, split) x WW waves; wave w serves the HPW kv
 // heads from (head_group * WW + w) * HPW with all of their rows (NB blocks of
-// 16; with HPW = 2 one block, rows 0-7 of the first head and 8-15 of the
-// second); WPE = waves per SIMD the register budget allows. All waves walk the
+// 16; with HPW = 2 either one block, rows 0-7 of the first head and 8-15 of
+// the second, or one block per head); WPE = waves per SIMD the register
+// budget allows. All waves walk the
 // same pages in the same order, so the heads' 256-byte slices of each page are
 // requested together and HBM sees 1 KiB (4 heads) or 2 KiB (8 heads) runs; the
 // head groups of a page range are dispatch neighbours. Each wave keeps its own
@@ -659,12 +667,14 @@ void sqa_partial_kernel(PartialArgs a) {
   // Waves past the last kv head (hkv not a multiple of WW * HPW) idle but stay
   // for the barrier.
   const bool active = kvh < a.hkv;
-  // Row slot r of block nb (r = 0..15) -> kv head kvh + row_head(r) and row
-  // row_in_head(nb, r) of that head (row = qi * group + g).
-  auto row_head = [](int r) { return HPW == 1 ? 0 : r >> 3; };
-  auto row_in_head = [](int nb, int r) { return HPW == 1 ? nb * 16 + r : (r & 7); };
+  // Row slot r of block nb (r = 0..15) -> kv head kvh + row_head(nb, r) and
+  // row row_in_head(nb, r) of that head (row = qi * group + g).
+  auto row_head = [](int nb, int r) { return HPW == 1 ? 0 : (NB == 1 ? r >> 3 : nb); };
+  auto row_in_head = [](int nb, int r) {
+    return HPW == 1 ? nb * 16 + r : (NB == 1 ? (r & 7) : r);
+  };
   auto slot_real = [&](int nb, int r) {
-    return kvh + row_head(r) < a.hkv && row_in_head(nb, r) < a.rows;
+    return kvh + row_head(nb, r) < a.hkv && row_in_head(nb, r) < a.rows;
   };
 
   // Start-up. First: the work item (fixed plan: the sequence length, with the
@@ -728,7 +738,7 @@ void sqa_partial_kernel(PartialArgs a) {
     const bool real = slot_real(nb, l16);
     const int qi = real ? r / a.group : 0;
     const int gg = real ? r - qi * a.group : 0;
-    const int hh = real ? (kvh + row_head(l16)) * a.group + gg : 0;
+    const int hh = real ? (kvh + row_head(nb, l16)) * a.group + gg : 0;
     const _Float16* qp = a.q + ((size_t)(b * a.q_len + qi) * a.hq + hh) * HD;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
@@ -897,12 +907,12 @@ void sqa_partial_kernel(PartialArgs a) {
   constexpr int CPR = HD / 4;        // 4-value chunks per row
   float* stage = sm_stage + wave * 16 * kStageRow;
   // Partial item of the kv head of row slot r: [slots, Hkv] items of rows rows.
-  auto item_of = [&](int r) {
-    return ((size_t)(it.slot0 + split) * a.hkv + kvh + row_head(r)) * a.rows;
+  auto item_of = [&](int nb, int r) {
+    return ((size_t)(it.slot0 + split) * a.hkv + kvh + row_head(nb, r)) * a.rows;
   };
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    if (nb * 16 >= a.rows) break;  // uniform
+    if (row_in_head(nb, 0) >= a.rows) break;  // uniform
     const float inv = st.l[nb] > 0.f ? a.out_scale / st.l[nb] : 0.f;
     const float sc = direct ? inv : 1.f;
     if (slot_real(nb, l16)) {
@@ -939,7 +949,7 @@ void sqa_partial_kernel(PartialArgs a) {
           const int qi = r / a.group;
           const int gg = r - qi * a.group;
           _Float16* op = a.out + ((size_t)(b * a.q_len + qi) * a.hq +
-                                  (kvh + row_head(slot)) * a.group + gg) * HD +
+                                  (kvh + row_head(nb, slot)) * a.group + gg) * HD +
                          4 * (e % CPR);
           const float o[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
           *(u2*)op = E::pack4(o);
@@ -951,10 +961,10 @@ void sqa_partial_kernel(PartialArgs a) {
         const int e = i * 64 + lane;
         const int slot = e / CPR;
         if (slot_real(nb, slot))
-          *(f4*)(a.part_o + (item_of(slot) + row_in_head(nb, slot)) * HD + 4 * (e % CPR)) = v[i];
+          *(f4*)(a.part_o + (item_of(nb, slot) + row_in_head(nb, slot)) * HD + 4 * (e % CPR)) = v[i];
       }
       if (g16 == 0 && slot_real(nb, l16)) {
-        const size_t pitem = item_of(l16) + row_in_head(nb, l16);
+        const size_t pitem = item_of(nb, l16) + row_in_head(nb, l16);
         a.part_ml[pitem * 2 + 0] = st.m[nb];
         a.part_ml[pitem * 2 + 1] = st.l[nb];
       }
@@ -1102,9 +1112,14 @@ void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, d
   constexpr int D3 = KV::kBytes == 1 ? 3 : 3 * 128 / HD;
   if (sh.hpw == 2) {
     // Two heads per wave: half the pages in flight, each twice the bytes.
-    if constexpr (HD == 64)
-      hipLaunchKernelGGL((sqa_partial_kernel<1, D2, 4, 1, HD, E, KV, 2>), grid, block, 0, stream,
-                         a);
+    if constexpr (HD == 64) {
+      if (sh.row_blocks == 1)
+        hipLaunchKernelGGL((sqa_partial_kernel<1, D2, 4, 1, HD, E, KV, 2>), grid, block, 0,
+                           stream, a);
+      else
+        hipLaunchKernelGGL((sqa_partial_kernel<2, D2, 4, 1, HD, E, KV, 2>), grid, block, 0,
+                           stream, a);
+    }
   } else if (sh.row_blocks == 1) {
     hipLaunchKernelGGL((sqa_partial_kernel<1, D4, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
                        a);
