@@ -32,7 +32,7 @@
 // (Dims<HD>) and a ring slot holds a page of HD-wide rows, and at head dim 64
 // a wave takes two kv heads (HPW = 2; a workgroup then serves 8 kv heads):
 // with up to 8 rows per kv head in one block (rows 0-7 and 8-15), with up to
-// 16 in one block each (NB = 2, block nb = head nb). The element
+// 16 or 32 in one or two blocks each (NB = 2 or 4). The element
 // traits swap in the bf16 MFMAs (PV then as one 16x16x32 over P's high and low
 // parts) and e4m3 K/V widened in registers; where the registers allow, the
 // page loop runs the next page's QK products under this page's softmax.
@@ -349,8 +349,8 @@ __device__ __forceinline__ unsigned pack_hi(unsigned a, unsigned b) {
 // and rows 8-15 of head 1): the QK and PV products run once per head over all
 // 16 rows; each lane keeps the scores of its own row's head (`upper`: row >=
 // 8), and each head's PV product gets the probabilities of its own rows only,
-// so both land in the one set of accumulators. HPW = 2 with NB = 2: block nb
-// holds head nb's rows and takes only that head's K and V.
+// so both land in the one set of accumulators. HPW = 2 with NB = 2 or 4:
+// blocks nb of head nb / (NB / 2) take only that head's K and V.
 // A page's K and V widened to the MFMAs' 16-bit type (a register copy for
 // 16-bit caches).
 template <int HD, int HPW>
@@ -381,7 +381,7 @@ template <int NB, int HD, typename E, typename KV, int HPW>
 __device__ __forceinline__ void page_scores(f4 (&s)[NB], const PageK<HD, HPW>& kf,
                                             const u4* sm_q, int lane, bool upper) {
   constexpr int KK = Dims<HD>::KK;
-  static_assert(HPW == 1 || NB <= 2, "two heads per wave: one shared block or one block each");
+  static_assert(HPW == 1 || NB <= 4, "two heads per wave: one shared block or NB / 2 each");
   // Raw scores S^T[token][row] = K . Q^T for this page.
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -390,8 +390,8 @@ __device__ __forceinline__ void page_scores(f4 (&s)[NB], const PageK<HD, HPW>& k
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const u4 qf = sm_q[(nb * KK + kk) * 64 + lane];
-      if constexpr (HPW == 2 && NB == 2) {
-        s[nb] = E::mma_qk(kf.k[nb][kk], qf, s[nb]);  // block nb holds head nb's rows
+      if constexpr (HPW == 2 && NB >= 2) {
+        s[nb] = E::mma_qk(kf.k[nb / (NB / 2)][kk], qf, s[nb]);  // head nb / (NB / 2)
       } else {
         s[nb] = E::mma_qk(kf.k[0][kk], qf, s[nb]);
         if constexpr (HPW == 2) s1 = E::mma_qk(kf.k[HPW - 1][kk], qf, s1);
@@ -492,10 +492,10 @@ __device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
                                   : u2{pack_hi(w0, w1), pack_hi(w2, w3)};
       // With two heads, head h's product takes only the probabilities of its
       // own rows (the other rows' lanes pass zeros).
-      const bool mine = HPW == 1 || NB == 2 || (h == 1) == upper;
+      const bool mine = HPW == 1 || NB >= 2 || (h == 1) == upper;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        if (HPW == 2 && NB == 2 && h != nb) continue;  // block nb: head nb's V only
+        if (HPW == 2 && NB >= 2 && h != nb / (NB / 2)) continue;  // its own head's V only
         st.acc[mb][nb] =
             E::mma_pv(av, mine ? ph[nb] : zero, mine ? pl[nb] : zero, st.acc[mb][nb]);
       }
@@ -669,9 +669,10 @@ void sqa_partial_kernel(PartialArgs a) {
   const bool active = kvh < a.hkv;
   // Row slot r of block nb (r = 0..15) -> kv head kvh + row_head(nb, r) and
   // row row_in_head(nb, r) of that head (row = qi * group + g).
-  auto row_head = [](int nb, int r) { return HPW == 1 ? 0 : (NB == 1 ? r >> 3 : nb); };
+  constexpr int BPH = NB >= 2 ? NB / HPW : 1;  // blocks per head (HPW = 2, NB >= 2)
+  auto row_head = [](int nb, int r) { return HPW == 1 ? 0 : (NB == 1 ? r >> 3 : nb / BPH); };
   auto row_in_head = [](int nb, int r) {
-    return HPW == 1 ? nb * 16 + r : (NB == 1 ? (r & 7) : r);
+    return HPW == 1 ? nb * 16 + r : (NB == 1 ? (r & 7) : (nb % BPH) * 16 + r);
   };
   auto slot_real = [&](int nb, int r) {
     return kvh + row_head(nb, r) < a.hkv && row_in_head(nb, r) < a.rows;
@@ -1116,8 +1117,11 @@ void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, d
       if (sh.row_blocks == 1)
         hipLaunchKernelGGL((sqa_partial_kernel<1, D2, 4, 1, HD, E, KV, 2>), grid, block, 0,
                            stream, a);
-      else
+      else if (sh.row_blocks == 2)
         hipLaunchKernelGGL((sqa_partial_kernel<2, D2, 4, 1, HD, E, KV, 2>), grid, block, 0,
+                           stream, a);
+      else
+        hipLaunchKernelGGL((sqa_partial_kernel<4, D2, 4, 1, HD, E, KV, 2>), grid, block, 0,
                            stream, a);
     }
   } else if (sh.row_blocks == 1) {

@@ -114,12 +114,12 @@ def test_fp8_cache(d, q_len, qdt):
     assert_parity(out.view_as(q), ref, label=f"fp8 d{d} q{q_len} {qdt}")
 
 
-@pytest.mark.parametrize("q_len", [2, 4])
+@pytest.mark.parametrize("q_len", [2, 4, 8])
 @pytest.mark.parametrize("hq,hkv", [(32, 8), (64, 16)])
 def test_two_heads_per_wave(hq, hkv, q_len):
-    """Head dim 64 with up to 16 rows per kv head runs two kv heads per wave (8 rows:
-    rows 0-7 and 8-15 of one block; 16 rows: one block per head): tree masks,
-    scales, one and two head groups, B1 and ragged batches, every plan."""
+    """Head dim 64 with up to 32 rows per kv head runs two kv heads per wave (8 rows:
+    rows 0-7 and 8-15 of one block; 16 or 32 rows: one or two blocks per head): tree
+    masks, scales, one and two head groups, B1 and ragged batches, every plan."""
     d = 64
     lens = [q_len, 9, 700, 3000]
     c = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=2600 + hkv + q_len,
