@@ -1,9 +1,9 @@
 """Benchmark of the paged small-q attention op on one MI355X.
 
 One step = one call of the op over one batch (inputs resident in HBM). The
-workload is BASELINE cfg3 (B16, q_len 8, KV 32768, Hq/Hkv 32/8, d 128,
+workload is cfg3 (B16, q_len 8, KV 32768, Hq/Hkv 32/8, d 128,
 page 16, 1% of K scaled x4, random page table over a 2x pool): the shape the
-BASELINE target is quoted at (KV = 32K, batch 16) and the largest single-GPU
+70%-of-peak target is stated for (KV = 32K, batch 16) and the largest single-GPU
 config; its 2.15 GB of KV cannot sit in the 256 MB MALL, so the figure is HBM.
 
 Prints ONE JSON line (the driver's contract). ``value`` is KV GB/s of the whole
@@ -404,7 +404,7 @@ def main():
                             "speedup_vs_fp16_kv": round(part_ms / p8, 3)}
         del k8, v8, out8, ws8
     if not args.no_per_q and default_types:
-        # The other single-GPU BASELINE configs, same timing (extra fields only).
+        # The other single-GPU benchmark configs, same timing (extra fields only).
         others = {}
         del tensors, q, k, v, bt, sl, out
         torch.cuda.empty_cache()

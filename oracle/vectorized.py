@@ -5,7 +5,7 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 Same mathematics as ``/root/reference/src/small_q_attention/reference.py:46-72``
 (scale ``D**-0.5``, GQA map ``qh // group``, row ``qi`` sees the first
 ``seq_len - q_len + qi + 1`` tokens, softmax then V), batched per sequence so
-it finishes full BASELINE sizes in seconds. Computes in float64 by default;
+it finishes full benchmark sizes in seconds. Computes in float64 by default;
 ``dtype=np.float32`` mirrors the reference's fp32 callers.
 """
 

@@ -158,7 +158,7 @@ def make_inputs(case: Case, device="cpu", gen_device: Optional[str] = None):
 
 
 def baseline_configs():
-    """The BASELINE configurations as :class:`Case` objects (``cfg1``..``cfg5``).
+    """The benchmark configurations as :class:`Case` objects (``cfg1``..``cfg5``).
 
     ``cfg4`` (the 36-case matrix) is expanded by :func:`matrix_cases`.
     """

@@ -1,6 +1,6 @@
 """Shared test helpers: the parity bar and two checkers.
 
-Parity bar: fp16 output within ``|a - r| <= 2e-3 + 1e-2 * |r|``
+Parity bar (the project's correctness target): fp16 output within ``|a - r| <= 2e-3 + 1e-2 * |r|``
 of the oracle rounded to fp16, with max abs error reported as well, and also
 measured against the unrounded float64 oracle.
 """

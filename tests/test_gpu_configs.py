@@ -1,4 +1,4 @@
-"""GPU parity at the BASELINE configurations' full sizes and over the 36-case matrix.
+"""GPU parity at the benchmark configurations' full sizes and over the 36-case matrix.
 
 cfg1 (B1 q2 L1024) and cfg2 (B4 q4 L8192) are checked whole against the float64
 C oracle. cfg3 (B16 q8 L32768, K x4 on 1% of slots), cfg5 (ragged B16 q8,
