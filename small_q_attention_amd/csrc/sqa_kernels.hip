@@ -1100,17 +1100,18 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
 // V: 4 pages at head dim 128 (3 at 64 rows, where the registers run out), 8 at
 // head dim 64 and 2 at 256, which holds at most 32 rows (its accumulators
 // double). e4m3 caches keep the same page counts although their pages hold
-// half the bytes, and 3 pages at 64 rows at head dim 64 too: the widened K and
-// V fragments take the registers a deeper ring would need. Measured at 16
-// sequences of 32K keys, partial kernel, e4m3 ring at twice these depths ->
-// these: head dim 128 q2 / q8 / q16 170.7 / 181.4 / 278 -> 169.7 / 174.2 /
-// 261 us; head dim 256 q8 342.7 -> 325.1 us; head dim 64 q4 / q8 / q16
-// 104.2 / 119.8 / 185 -> 100.7 / 116.6 / 169 us.
+// half the bytes, and fewer at 64 rows (2 pages at head dim 128, 3 at 64): the
+// widened K and V fragments take the registers a deeper ring would need.
+// Measured at 16 sequences of 32K keys, partial kernel, e4m3 ring at twice
+// these depths -> these: head dim 128 q2 / q8 170.7 / 181.4 -> 169.7 / 174.2
+// us, q16 278 (6 pages) -> 261 (3) -> 251 us (2); head dim 256 q8 342.7 ->
+// 325.1 us; head dim 64 q4 / q8 / q16 104.2 / 119.8 / 185 -> 100.7 / 116.6 /
+// 169 us (2 pages at 64 rows there lose the pipelined loop: 154 -> 165 us).
 template <int HD, typename E, typename KV>
 void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
                        hipStream_t stream) {
   constexpr int D4 = 4 * 128 / HD, D2 = 2 * 128 / HD;
-  constexpr int D3 = KV::kBytes == 1 ? 3 : 3 * 128 / HD;
+  constexpr int D3 = KV::kBytes == 1 ? (HD == 128 ? 2 : 3) : 3 * 128 / HD;
   if (sh.hpw == 2) {
     // Two heads per wave: half the pages in flight, each twice the bytes.
     if constexpr (HD == 64) {
