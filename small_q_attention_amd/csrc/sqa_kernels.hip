@@ -129,7 +129,9 @@ struct ElemBF16 {
     const b4 hi = {(__bf16)p0, (__bf16)p1, (__bf16)p2, (__bf16)p3};
     const float h0 = (float)hi[0], h1 = (float)hi[1], h2v = (float)hi[2], h3 = (float)hi[3];
     const b4 lw = {(__bf16)(p0 - h0), (__bf16)(p1 - h1), (__bf16)(p2 - h2v), (__bf16)(p3 - h3)};
-    l += ((h0 + (float)lw[0]) + (h1 + (float)lw[1])) + ((h2v + (float)lw[2]) + (h3 + (float)lw[3]));
+    // The row sum takes p itself: hi + lo is within 2^-17 of p, and summing p
+    // saves the conversions back (bf16 q16: 363 -> 350 us).
+    l += (p0 + p1) + (p2 + p3);
     lo = __builtin_bit_cast(u2, lw);
     return __builtin_bit_cast(u2, hi);
   }
@@ -465,8 +467,9 @@ __device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
     }
   }
 
-  // P = 2^(c*s - m), rounded once to the element type; the row sum is taken
-  // over the rounded values so O is an exact convex combination.
+  // P = 2^(c*s - m), rounded once to the element type; with fp16 the row sum
+  // is taken over the rounded values so O is an exact convex combination (with
+  // bf16, P is hi + lo and the sum is within 2^-17 of it).
   u2 ph[NB], pl[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
