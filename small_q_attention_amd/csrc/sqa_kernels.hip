@@ -1101,8 +1101,8 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
 
 // Ring depth: the pages in flight per wave hold about 32 KiB of 16-bit K and
 // V: 4 pages at head dim 128 (3 at 64 rows, where the registers run out), 8 at
-// head dim 64 and 2 at 256, which holds at most 32 rows (its accumulators
-// double). e4m3 caches keep the same page counts although their pages hold
+// head dim 64 (4 at 64 rows: bf16 q16 201.5 -> 194.5 us, fp16 174.5 -> 173.9)
+// and 2 at 256, which holds at most 32 rows (its accumulators double). e4m3 caches keep the same page counts although their pages hold
 // half the bytes, and fewer at 64 rows (2 pages at head dim 128, 3 at 64): the
 // widened K and V fragments take the registers a deeper ring would need.
 // Measured at 16 sequences of 32K keys, partial kernel, e4m3 ring at twice
@@ -1114,7 +1114,7 @@ template <int HD, typename E, typename KV>
 void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
                        hipStream_t stream) {
   constexpr int D4 = 4 * 128 / HD, D2 = 2 * 128 / HD;
-  constexpr int D3 = KV::kBytes == 1 ? (HD == 128 ? 2 : 3) : 3 * 128 / HD;
+  constexpr int D3 = KV::kBytes == 1 ? (HD == 128 ? 2 : 3) : (HD == 64 ? 4 : 3 * 128 / HD);
   if (sh.hpw == 2) {
     // Two heads per wave: half the pages in flight, each twice the bytes.
     if constexpr (HD == 64) {
