@@ -23,9 +23,11 @@ the zero fixture corrected), closed forms (uniform softmax gives the mean of
 the visible V rows, ``seq_len == q_len`` gives ``V[0]`` for row 0, one visible
 key gives that key's V), invariants (page-table permutation, GQA head
 symmetry) and agreement of the three restatements with each other on
-seeded inputs. The fp16-CPU-input path of the reference (``reference.py:69``
-casting probabilities back to fp16) is restated op for op but is parity
-unpinned: no caller of the reference uses it and no fixture covers it.
+seeded inputs. The fp16-CPU-input path of the reference (``reference.py:68-70``:
+fp16 logits, probabilities cast back to fp16, fp16 PV) is pinned by closed
+forms in ``tests/test_checker_pinned.py``: a uniform softmax over 4 and 8 keys,
+3:1 weights and a dominant key, where every weight and product is exact in
+fp16, give the fp32 path's result rounded to fp16 bit for bit.
 """
 
 from .reference import paged_mtp_attention_reference

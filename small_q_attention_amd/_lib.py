@@ -66,9 +66,12 @@ def library_path() -> Path:
 
 
 def load(verbose: bool = False, build_if_missing: bool = True):
-    """Load ``libsqa.so`` (building it first if it does not exist yet). ``verbose``
-    echoes the library path and the hipcc command that builds it, as the
-    reference's loaders echo their JIT build (``cuda.py:31-36``)."""
+    """Load ``libsqa.so``, building it first if it is missing or was built from other
+    sources (the source hash stamped into the library differs from the hash of the
+    sources beside it). With ``build_if_missing=False`` either case raises
+    ``RuntimeError`` instead. ``verbose`` echoes the library path and the hipcc
+    command that builds it, as the reference's loaders echo their JIT build
+    (``cuda.py:31-36``)."""
     global _LIB
     if verbose:
         print(f"[sqa] {_build.LIB_PATH}; build command: {' '.join(_build.build_command())}",
@@ -76,10 +79,17 @@ def load(verbose: bool = False, build_if_missing: bool = True):
     with _LOCK:
         if _LIB is None:
             path = _build.LIB_PATH
-            if not path.exists():
-                if not build_if_missing:
+            want = _build.source_hash()
+            have = _build.built_hash(path) if path.exists() else None
+            if have != want:
+                if build_if_missing:
+                    _build.build(verbose=verbose)
+                elif not path.exists():
                     raise RuntimeError(f"{path} is not built; run small_q_attention_amd.build")
-                _build.build(verbose=verbose)
+                elif have is not None:
+                    raise RuntimeError(f"{path} is stale (built from sources {have}, sources "
+                                       f"now {want}); run small_q_attention_amd.build")
+                # An unstamped file: loading it below fails, or its version check does.
             try:
                 lib = ctypes.CDLL(str(path))
             except OSError as exc:
@@ -88,6 +98,10 @@ def load(verbose: bool = False, build_if_missing: bool = True):
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
+            version = lib.sqa_version().decode(errors="replace")
+            if f"sqa-src-hash:{want}" not in version:
+                raise RuntimeError(f"{path} reports '{version}', not the sources' hash {want}; "
+                                   "rebuild with small_q_attention_amd.build")
             _LIB = lib
         return _LIB
 

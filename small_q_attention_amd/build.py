@@ -5,10 +5,18 @@ The reference JIT-compiles its CUDA source through
 (``/root/reference/src/small_q_attention/cuda.py:16-37``). Here the library is
 one plain shared object with a C ABI, compiled once for gfx950 by hipcc; every
 ``load_vN`` returns a handle to the same library.
+
+The library carries the SHA-256 (first 16 hex digits) of its sources, headers
+and compiler flags, both as the string ``sqa-src-hash:<hash>`` inside
+``sqa_version()`` and as bytes of the file, so a loader can tell, before
+``dlopen``, whether the library on disk was built from the sources beside it
+(the reference's loaders rebuild through torch's extension cache keyed the same
+way, ``cuda.py:16-37``).
 """
 
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -32,21 +40,40 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found; ROCm is required to build libsqa.so")
 
 
-def build_command(output: Path = LIB_PATH):
+FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # Packed fp32 VALU ops are kept out of the generated code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA operands and results in VGPRs: the softmax reads every score and
+    # rescales every accumulator with VALU ops, and with the default AGPR
+    # form each of those costs a copy (q16: ~1500 copies per 3 pages,
+    # 375 -> 334 us at KV 32K x B16).
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
+]
+HASH_MARKER = b"sqa-src-hash:"
+HASH_LEN = 16
+
+
+def source_hash() -> str:
+    """SHA-256 (first 16 hex digits) over the compiler flags and the name and bytes of
+    every source and header the library is built from."""
+    h = hashlib.sha256()
+    h.update("\0".join(FLAGS).encode())
+    for path in SOURCES + HEADERS:
+        h.update(b"\0" + path.name.encode() + b"\0")
+        h.update(path.read_bytes())
+    return h.hexdigest()[:HASH_LEN]
+
+
+def build_command(output: Path = LIB_PATH, src_hash: str = ""):
     return [
         hipcc_path(),
-        f"--offload-arch={ARCH}",
-        "-O3",
-        "-std=c++17",
-        "-fPIC",
-        "-shared",
-        # Packed fp32 VALU ops are kept out of the generated code.
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        # MFMA operands and results in VGPRs: the softmax reads every score and
-        # rescales every accumulator with VALU ops, and with the default AGPR
-        # form each of those costs a copy (q16: ~1500 copies per 3 pages,
-        # 375 -> 334 us at KV 32K x B16).
-        "-mllvm", "-amdgpu-mfma-vgpr-form",
+        *FLAGS,
+        f'-DSQA_SOURCE_HASH="{src_hash or source_hash()}"',
         f"-I{INCLUDE}",
         f"-I{CSRC}",
         *[str(s) for s in SOURCES],
@@ -54,16 +81,30 @@ def build_command(output: Path = LIB_PATH):
     ]
 
 
+def built_hash(path: Path = LIB_PATH):
+    """The source hash stamped into a built library, or None (missing or unstamped)."""
+    try:
+        data = path.read_bytes()
+    except OSError:
+        return None
+    i = data.find(HASH_MARKER)
+    if i < 0:
+        return None
+    stamp = data[i + len(HASH_MARKER):i + len(HASH_MARKER) + HASH_LEN]
+    try:
+        return stamp.decode("ascii")
+    except UnicodeDecodeError:
+        return None
+
+
 def is_stale() -> bool:
-    if not LIB_PATH.exists():
-        return True
-    built = LIB_PATH.stat().st_mtime
-    return any(p.stat().st_mtime > built for p in SOURCES + HEADERS)
+    """True when the library is missing or was built from other sources or flags."""
+    return built_hash(LIB_PATH) != source_hash()
 
 
 def build(verbose: bool = False) -> Path:
     """Compile ``libsqa.so`` (always; callers decide whether a rebuild is due)."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = LIB_PATH.with_name(f"{LIB_PATH.name}.tmp{os.getpid()}")
     cmd = build_command(tmp)
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -71,6 +112,7 @@ def build(verbose: bool = False) -> Path:
     errors = [ln for ln in (res.stdout + res.stderr).splitlines()
               if "packed-fp32-ops" not in ln and "unknown target feature" not in ln.lower()]
     if res.returncode != 0:
+        tmp.unlink(missing_ok=True)
         raise RuntimeError("hipcc failed building libsqa.so:\n" + "\n".join(errors))
     if verbose and errors:
         print("\n".join(errors), flush=True)

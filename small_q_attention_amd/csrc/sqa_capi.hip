@@ -43,7 +43,12 @@ extern "C" {
 
 const char* sqa_last_error(void) { return g_last_error.c_str(); }
 
-const char* sqa_version(void) { return "sqa 0.1.0 gfx950"; }
+// The build passes the source hash (small_q_attention_amd/build.py); the loader
+// compares it with the sources beside the library.
+#ifndef SQA_SOURCE_HASH
+#define SQA_SOURCE_HASH "unstamped"
+#endif
+const char* sqa_version(void) { return "sqa 0.2.0 gfx950 sqa-src-hash:" SQA_SOURCE_HASH; }
 
 int sqa_read_probe(const void* data, size_t bytes, unsigned* sink, int blocks, void* stream) {
   if (!data || !sink) return fail(SQA_ERR_INVALID, "null pointer");

@@ -76,36 +76,11 @@ def compact_sequences(query, key_cache, value_cache, block_tables, seq_lens, bat
 
 def torch_fp32_reference(query, key_cache, value_cache, block_tables, seq_lens, page_size,
                          num_kv_heads, batches=None):
-    """Same op in torch fp32 on the tensors' device (a second, fast checker).
+    """The float32 torch checker (``small_q_attention_amd.checker.attention_fp32``) on the
+    tensors' device; pinned against the float64 C oracle by
+    ``tests/test_checker_pinned.py``. Float64 numpy ``[B, Q, Hq, D]`` (NaN for
+    skipped batches)."""
+    from small_q_attention_amd.checker import attention_fp32
 
-    Float32 throughout, contiguous operands only. Rows with no visible key are 0.
-    Returns a float64 numpy array ``[B, Q, Hq, D]`` (NaN for skipped batches).
-    """
-    import torch
-
-    n_batch, q_len, hq, dim = query.shape
-    group = hq // num_kv_heads
-    out = np.full((n_batch, q_len, hq, dim), np.nan)
-    for b in (range(n_batch) if batches is None else batches):
-        n = int(seq_lens[b])
-        if n <= 0:
-            out[b] = 0
-            continue
-        pages = -(-n // page_size)
-        ids = block_tables[b, :pages].long()
-        k = key_cache.index_select(0, ids).reshape(-1, num_kv_heads, dim)[:n].float()
-        v = value_cache.index_select(0, ids).reshape(-1, num_kv_heads, dim)[:n].float()
-        qg = query[b].float().reshape(q_len, num_kv_heads, group, dim).permute(1, 0, 2, 3)
-        qg = qg.reshape(num_kv_heads, q_len * group, dim).contiguous()
-        kt = k.permute(1, 2, 0).contiguous()  # [Hkv, D, L]
-        logits = torch.matmul(qg, kt) * (dim ** -0.5)  # [Hkv, Q*G, L]
-        vis = n - q_len + torch.arange(q_len, device=query.device) + 1
-        vis = vis.repeat_interleave(group)
-        mask = torch.arange(n, device=query.device)[None, :] < vis[:, None]
-        logits = logits.masked_fill(~mask[None], float("-inf"))
-        w = torch.softmax(logits, dim=-1)
-        w = torch.nan_to_num(w, nan=0.0)
-        o = torch.matmul(w, v.permute(1, 0, 2).contiguous())  # [Hkv, Q*G, D]
-        o = o.reshape(num_kv_heads, q_len, group, dim).permute(1, 0, 2, 3).reshape(q_len, hq, dim)
-        out[b] = o.double().cpu().numpy()
-    return out
+    return attention_fp32(query, key_cache, value_cache, block_tables, seq_lens, page_size,
+                          num_kv_heads, batches)
