@@ -98,6 +98,30 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
                             int64_t num_pages, int page_size, int max_pages, int num_splits,
                             int pages_per_split, void* stream, void** timing_events);
 
+/* Device scratch the no-allocation entry point holds per GPU (64 MiB). */
+#define SQA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/*
+ * sqa_paged_mtp_attention without a workspace argument. No counterpart in the
+ * reference: it serves callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The plan's split partials go to a device array of SQA_NOALLOC_SCRATCH_BYTES
+ * that the library holds on every GPU it runs on until the process ends; its
+ * device address is looked up once per device (hipGetSymbolAddress). Same
+ * arguments, plans, kernels, results and status codes as
+ * sqa_paged_mtp_attention, on the current device's array; a plan whose
+ * sqa_workspace_bytes exceeds SQA_NOALLOC_SCRATCH_BYTES is rejected with
+ * SQA_ERR_WORKSPACE. Allocates nothing, never synchronises. All calls on one
+ * GPU share its array: calls that overlap on one GPU (other streams or host
+ * threads) race; serialise them.
+ */
+int sqa_paged_mtp_attention_noalloc(const void* query, const void* key_cache,
+                                    const void* value_cache, const int32_t* block_tables,
+                                    const int32_t* seq_lens, void* output, int batch, int q_len,
+                                    int num_query_heads, int num_kv_heads, int head_dim,
+                                    int64_t num_pages, int page_size, int max_pages,
+                                    int num_splits, int pages_per_split, void* stream);
+
 /*
  * Where the K and V of a paged cache live, for sqa_paged_attention. Strides
  * are in fp16 elements; the head dimension is contiguous. Element d of kv head

@@ -27,6 +27,8 @@ _SIGNATURES = [
     ("sqa_paged_mtp_attention", _C.c_int,
      [_C.c_void_p] * 7 + [_C.c_size_t] + [_C.c_int] * 5 + [_C.c_int64] + [_C.c_int] * 4
      + [_C.c_void_p, _C.c_void_p]),
+    ("sqa_paged_mtp_attention_noalloc", _C.c_int,
+     [_C.c_void_p] * 6 + [_C.c_int] * 5 + [_C.c_int64] + [_C.c_int] * 4 + [_C.c_void_p]),
     ("sqa_paged_attention", _C.c_int, [_C.c_void_p]),
     ("sqa_read_probe", _C.c_int, [_C.c_void_p, _C.c_size_t, _C.c_void_p, _C.c_int, _C.c_void_p]),
     ("sqa_device_cu_count", _C.c_int, [_C.c_int]),

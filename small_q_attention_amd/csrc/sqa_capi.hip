@@ -319,26 +319,13 @@ int run_attention(const sqa_attention_args& a) {
   return SQA_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int sqa_paged_attention(const sqa_attention_args* args) {
-  if (!args) return fail(SQA_ERR_INVALID, "null argument struct");
-  if (args->struct_size != sizeof(sqa_attention_args))
-    return fail(SQA_ERR_INVALID, "struct_size %zu does not match this library's %zu",
-                args->struct_size, sizeof(sqa_attention_args));
-  return run_attention(*args);
-}
-
-int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void* value_cache,
+// The reference's separate [num_pages, page, Hkv, head_dim] caches, causal draft
+// chain, scale head_dim^-1/2; workspace and timing events left empty.
+sqa_attention_args mtp_args(const void* query, const void* key_cache, const void* value_cache,
                             const int32_t* block_tables, const int32_t* seq_lens, void* output,
-                            void* workspace, size_t workspace_bytes, int batch, int q_len,
-                            int num_query_heads, int num_kv_heads, int head_dim,
-                            int64_t num_pages, int page_size, int max_pages, int num_splits,
-                            int pages_per_split, void* stream, void** timing_events) {
-  // The reference's separate [num_pages, 16, Hkv, head_dim] caches, causal
-  // draft chain, scale head_dim^-1/2.
+                            int batch, int q_len, int num_query_heads, int num_kv_heads,
+                            int head_dim, int64_t num_pages, int page_size, int max_pages,
+                            int num_splits, int pages_per_split, void* stream) {
   sqa_attention_args a;
   memset(&a, 0, sizeof(a));
   a.struct_size = sizeof(a);
@@ -363,10 +350,88 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
   a.page_size = page_size;
   a.num_splits = num_splits;
   a.pages_per_split = pages_per_split;
+  a.stream = stream;
+  return a;
+}
+
+// Scratch of the no-allocation entry point: a file-scope device array every GPU
+// the library runs on holds (zero-initialised at load) until the process ends.
+// Host code never uses the array's name as an address: the device address comes
+// from hipGetSymbolAddress, once per device with that device current, and only
+// that address reaches kernels. Every call on a device shares its array, so calls
+// that overlap on one GPU (other streams, other threads) race on it.
+constexpr size_t kScratchBytes = SQA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mutex;
+std::vector<void*> g_scratch_ptr;  // per device, nullptr until looked up
+
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SQA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sqa_paged_attention(const sqa_attention_args* args) {
+  if (!args) return fail(SQA_ERR_INVALID, "null argument struct");
+  if (args->struct_size != sizeof(sqa_attention_args))
+    return fail(SQA_ERR_INVALID, "struct_size %zu does not match this library's %zu",
+                args->struct_size, sizeof(sqa_attention_args));
+  return run_attention(*args);
+}
+
+int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void* value_cache,
+                            const int32_t* block_tables, const int32_t* seq_lens, void* output,
+                            void* workspace, size_t workspace_bytes, int batch, int q_len,
+                            int num_query_heads, int num_kv_heads, int head_dim,
+                            int64_t num_pages, int page_size, int max_pages, int num_splits,
+                            int pages_per_split, void* stream, void** timing_events) {
+  sqa_attention_args a = mtp_args(query, key_cache, value_cache, block_tables, seq_lens, output,
+                                  batch, q_len, num_query_heads, num_kv_heads, head_dim, num_pages,
+                                  page_size, max_pages, num_splits, pages_per_split, stream);
   a.workspace = workspace;
   a.workspace_bytes = workspace_bytes;
-  a.stream = stream;
   a.timing_events = timing_events;
+  return run_attention(a);
+}
+
+int sqa_paged_mtp_attention_noalloc(const void* query, const void* key_cache,
+                                    const void* value_cache, const int32_t* block_tables,
+                                    const int32_t* seq_lens, void* output, int batch, int q_len,
+                                    int num_query_heads, int num_kv_heads, int head_dim,
+                                    int64_t num_pages, int page_size, int max_pages,
+                                    int num_splits, int pages_per_split, void* stream) {
+  const size_t need = sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, head_dim,
+                                          num_splits, pages_per_split);
+  if (need > kScratchBytes)
+    return fail(SQA_ERR_WORKSPACE,
+                "the plan needs %zu bytes of scratch; the no-allocation entry point holds at most "
+                "%zu (use sqa_paged_mtp_attention with a caller workspace)",
+                need, kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_address(&ws);
+    if (rc != SQA_OK) return rc;
+  }
+  sqa_attention_args a = mtp_args(query, key_cache, value_cache, block_tables, seq_lens, output,
+                                  batch, q_len, num_query_heads, num_kv_heads, head_dim, num_pages,
+                                  page_size, max_pages, num_splits, pages_per_split, stream);
+  a.workspace = ws;
+  a.workspace_bytes = ws ? kScratchBytes : 0;
   return run_attention(a);
 }
 

@@ -202,3 +202,16 @@ def test_read_probe_rejects_bad_arguments_without_a_gpu(lib, args, msg):
     data, nbytes, sink, blocks = args
     assert lib.sqa_read_probe(data, nbytes, sink, blocks, None) == SQA_ERR_INVALID
     assert msg in lib.sqa_last_error().decode()
+
+
+def test_noalloc_rejects_plans_beyond_its_scratch_before_any_device_call(lib):
+    """SQA_NOALLOC_SCRATCH_BYTES (64 MiB) bounds the plan; larger plans fail with
+    SQA_ERR_WORKSPACE before the library touches a device (so this runs without a GPU)."""
+    need = lib.sqa_workspace_bytes(1, 16, 32, 8, 128, 2048, 1)
+    assert need > (64 << 20)
+    rc = lib.sqa_paged_mtp_attention_noalloc(None, None, None, None, None, None, 1, 16, 32, 8,
+                                             128, 4096, 16, 2048, 2048, 1, None)
+    assert rc == SQA_ERR_WORKSPACE
+    assert b"no-allocation" in lib.sqa_last_error()
+    header = HEADER.read_text()
+    assert "#define SQA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)" in header
