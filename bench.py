@@ -30,25 +30,52 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, AMD published peak
+# KV sets smaller than this are timed over several distinct pools in turn, so
+# repeats cannot be served from the 256 MB MALL (Infinity Cache).
+ROTATE_BELOW_BYTES = 512 << 20
+
+
 # rocprofv3 FETCH_SIZE + WRITE_SIZE summary of the partial kernel on this workload
 # (calibrated against a plain 1 GiB copy); regenerated with the kernel. The bench
 # line's is profiles/sqa_partial_kernel_cfg3_b16_q8_kv32768.txt.
 def profile_path(config: str, q_len: int, kv_dtype: str) -> Path:
-    shape = {"cfg2": f"cfg2_b4_q{q_len}_kv8192", "cfg3": f"cfg3_b16_q{q_len}_kv32768",
-             "cfg5": f"cfg5_b16_q{q_len}_ragged"}[config]
+    shape = {"cfg1": f"cfg1_b1_q{q_len}_kv1024", "cfg2": f"cfg2_b4_q{q_len}_kv8192",
+             "cfg3": f"cfg3_b16_q{q_len}_kv32768", "cfg5": f"cfg5_b16_q{q_len}_ragged"}[config]
     suffix = "" if kv_dtype == "fp16" else f"_{kv_dtype}"
     return ROOT / "profiles" / f"sqa_partial_kernel_{shape}{suffix}.txt"
 
 
-def _profiled_traffic(path: Path):
-    """HBM bytes per partial-kernel launch from a committed counter summary, or None."""
+def _profile_fields(path: Path):
+    """``key: value`` lines of a committed rocprof summary (first token of the value)."""
+    out = {}
     try:
         for line in path.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(float(line.split(":", 1)[1]))
+            if ":" in line and not line.startswith("#") and "|" not in line:
+                key, val = line.split(":", 1)
+                if val.split():
+                    out[key.strip()] = val.split()[0]
     except OSError:
         pass
-    return None
+    return out
+
+
+def _profiled_traffic(path: Path):
+    """HBM bytes per partial-kernel launch from a committed counter summary, or None."""
+    val = _profile_fields(path).get("traffic_bytes_per_launch")
+    return int(float(val)) if val is not None else None
+
+
+def _profiled_times(path: Path):
+    """Partial and merge kernel durations (us, the bench's timed steps) from a committed
+    rocprof summary, or None."""
+    f = _profile_fields(path)
+    if "partial_kernel_timed_steps_avg_us" not in f:
+        return None
+    out = {"partial_us": float(f["partial_kernel_timed_steps_avg_us"]),
+           "source": str(path.relative_to(ROOT))}
+    if "merge_kernel_timed_steps_avg_us" in f:
+        out["merge_us"] = float(f["merge_kernel_timed_steps_avg_us"])
+    return out
 METRIC = "µs/call + achieved HBM GB/s (% peak), q_len 2/4/8, KV 8K/32K, batch 1/4/16"
 
 
@@ -63,7 +90,7 @@ def _parse():
     ap.add_argument("--no-per-q", action="store_true", help="skip the q_len 2/4/16 extras")
     ap.add_argument("--q-len", type=int, default=0,
                     help="override the workload's q_len (profiling other rows per kv head)")
-    ap.add_argument("--config", default="cfg3", choices=("cfg2", "cfg3", "cfg5"),
+    ap.add_argument("--config", default="cfg3", choices=("cfg1", "cfg2", "cfg3", "cfg5"),
                     help="workload (cfg3 is the bench line; others for profiling)")
     ap.add_argument("--kv-dtype", default="fp16", choices=("fp16", "bf16", "e4m3"),
                     help="element types of the timed workload (profiling the other kernels): "
@@ -99,42 +126,61 @@ def _caller(torch, lib, tensors):
     return call
 
 
-def time_calls(torch, lib, tensors, plan, steps, warmup):
-    """Time `steps` calls through the C ABI with a preallocated workspace.
+def input_sets(inputs, case, kv_bytes):
+    """The workload's inputs on the device: one set, or, when its KV bytes are under
+    ``ROTATE_BELOW_BYTES``, enough distinct sets (other seeds, at least 3) that together
+    they exceed it; the timed calls cycle through them so no call finds its pages in
+    the MALL from the call before."""
+    import copy
+
+    n = 1 if kv_bytes >= ROTATE_BELOW_BYTES else max(3, -(-ROTATE_BELOW_BYTES // kv_bytes) + 1)
+    sets = []
+    for i in range(n):
+        c = copy.copy(case)
+        c.seed = case.seed + 7919 * i
+        sets.append(inputs.make_inputs(c, device="cuda", gen_device="cuda"))
+    return sets
+
+
+def time_calls(torch, lib, sets, plan, steps, warmup):
+    """Time `steps` calls through the C ABI with a preallocated workspace, cycling
+    through the input sets (see :func:`input_sets`).
 
     Two passes of `steps` calls: the first, bracketed by synchronisations with
     nothing inside it but the calls, gives the ms per call; the second records
     the library's timing events around each kernel (events between the
-    kernels add a little time per call, so they stay out of the first pass).
-    Returns (ms per call, mean partial-kernel ms, mean merge-kernel ms, output).
+    kernels add a little time per call, so they stay out of the first pass and
+    make the per-kernel figures upper bounds). Returns (ms per call, mean
+    partial-kernel ms, mean merge-kernel ms, output of set 0).
     """
-    q, k, v, bt, sl = tensors
+    q, k = sets[0][0], sets[0][1]
     num_splits, pps = plan
-    out = torch.empty_like(q)
+    outs = [torch.empty_like(t[0]) for t in sets]
     nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], q.shape[3],
                                  num_splits, pps)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     stream = torch.cuda.current_stream()
     handle = stream.cuda_stream
-    call = _caller(torch, lib, tensors)
-    for _ in range(warmup):
-        call(out, ws, num_splits, pps, handle)
+    calls = [_caller(torch, lib, t) for t in sets]
+    n = len(sets)
+    for i in range(max(warmup, n)):
+        calls[i % n](outs[i % n], ws, num_splits, pps, handle)
     kev = _events(torch, 3 * steps)
     start, end = _events(torch, 2)
     torch.cuda.synchronize()
     start.record(stream)
-    for _ in range(steps):
-        call(out, ws, num_splits, pps, handle)
+    for i in range(steps):
+        calls[i % n](outs[i % n], ws, num_splits, pps, handle)
     end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
     for i in range(steps):
-        call(out, ws, num_splits, pps, handle,
-             timing_events=[e.cuda_event for e in kev[3 * i:3 * i + 3]])
+        calls[i % n](outs[i % n], ws, num_splits, pps, handle,
+                     timing_events=[e.cuda_event for e in kev[3 * i:3 * i + 3]])
     torch.cuda.synchronize()
     part = [kev[3 * i].elapsed_time(kev[3 * i + 1]) for i in range(steps)]
     merge = [kev[3 * i + 1].elapsed_time(kev[3 * i + 2]) for i in range(steps)]
-    return total_ms / steps, statistics.mean(part), statistics.mean(merge), out
+    return total_ms / steps, statistics.mean(part), statistics.mean(merge), outs[0]
 
 
 def read_probe(torch, lib, pool, steps):
@@ -163,7 +209,7 @@ def read_probe(torch, lib, pool, steps):
 def _ramp_clocks(torch, lib, tensors, plan, seconds=0.25):
     """Setup, not a step: run the op for ~0.25 s so GPU clocks settle before the
     warmup steps (the first calls of a process otherwise run up to ~10% slow)."""
-    q, k, v, bt, sl = tensors
+    q, k = tensors[0], tensors[1]
     out = torch.empty_like(q)
     nbytes = lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], q.shape[3],
                                  plan[0], plan[1])
@@ -274,22 +320,25 @@ def main():
     case = inputs.baseline_configs()[args.config]
     if args.q_len:
         case.q_len = args.q_len
-    tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
+    kvb16 = inputs.kv_bytes(case.seq_lens, case.num_kv_heads, case.head_dim)
+    sets = []
+    for q, k, v, bt, sl in input_sets(inputs, case, kvb16):
+        if args.kv_dtype == "bf16":
+            q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+        elif args.kv_dtype == "e4m3":
+            k, v = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
+        sets.append((q, k, v, bt, sl))
+    tensors = sets[0]
     q, k, v, bt, sl = tensors
-    if args.kv_dtype == "bf16":
-        q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
-    elif args.kv_dtype == "e4m3":
-        k, v = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
-    tensors = (q, k, v, bt, sl)
     default_types = args.kv_dtype == "fp16"
     plan = _lib.plan_splits(0, case.batch, case.q_len, case.num_query_heads, case.num_kv_heads,
                             case.head_dim, case.max_seq_len, bt.shape[1], 0)
     _ramp_clocks(torch, _lib, tensors, plan)
-    ms, part_ms, merge_ms, out = time_calls(torch, _lib, tensors, plan, args.steps, args.warmup)
+    ms, part_ms, merge_ms, out = time_calls(torch, _lib, sets, plan, args.steps, args.warmup)
     if not torch.isfinite(out).all():
         raise SystemExit("non-finite output")
     prof = profile_path(args.config, case.q_len, args.kv_dtype)
-    kvb = inputs.kv_bytes(case.seq_lens, case.num_kv_heads, case.head_dim) * k.element_size() // 2
+    kvb = kvb16 * k.element_size() // 2
     value = kvb / (ms * 1e-3) / 1e9
     achieved = kvb / (part_ms * 1e-3) / 1e9
     result = {
@@ -344,7 +393,7 @@ def main():
                              generator=g, device="cuda", dtype=torch.float16)
             planx = _lib.plan_splits(0, case.batch, ql, case.num_query_heads, case.num_kv_heads,
                                      case.head_dim, case.max_seq_len, bt.shape[1], 0)
-            msx, px, mx, _ = time_calls(torch, _lib, (qx, k, v, bt, sl), planx, args.steps,
+            msx, px, mx, _ = time_calls(torch, _lib, [(qx, k, v, bt, sl)], planx, args.steps,
                                         args.warmup)
             extra[f"q{ql}"] = {"us_per_call": round(msx * 1e3, 2),
                                "kv_GBps": round(kvb / (msx * 1e-3) / 1e9, 1),
@@ -406,22 +455,34 @@ def main():
     if not args.no_per_q and default_types:
         # The other single-GPU benchmark configs, same timing (extra fields only).
         others = {}
-        del tensors, q, k, v, bt, sl, out
+        del tensors, sets, q, k, v, bt, sl, out
         torch.cuda.empty_cache()
         for name in ("cfg1", "cfg2", "cfg5"):
             c = inputs.baseline_configs()[name]
-            t = inputs.make_inputs(c, device="cuda", gen_device="cuda")
-            pl = _lib.plan_splits(0, c.batch, c.q_len, c.num_query_heads, c.num_kv_heads,
-                                  c.head_dim, c.max_seq_len, t[3].shape[1], 0)
-            _ramp_clocks(torch, _lib, t, pl, seconds=0.1)
-            msx, px, mx, _ = time_calls(torch, _lib, t, pl, args.steps, args.warmup)
             kb = inputs.kv_bytes(c.seq_lens, c.num_kv_heads, c.head_dim)
-            others[name] = {"batch": c.batch, "q_len": c.q_len, "kv_lens": "ragged" if name == "cfg5"
-                            else c.seq_lens[0], "kv_bytes": kb, "us_per_call": round(msx * 1e3, 2),
-                            "kernel_us": round(px * 1e3, 2), "merge_us": round(mx * 1e3, 2),
-                            "kernel_frac": round(kb / (px * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
-                            "num_splits": pl[0], "pages_per_split": pl[1]}
-            del t
+            ts = input_sets(inputs, c, kb)
+            pl = _lib.plan_splits(0, c.batch, c.q_len, c.num_query_heads, c.num_kv_heads,
+                                  c.head_dim, c.max_seq_len, ts[0][3].shape[1], 0)
+            _ramp_clocks(torch, _lib, ts[0], pl, seconds=0.1)
+            msx, px, mx, _ = time_calls(torch, _lib, ts, pl, args.steps, args.warmup)
+            row = {"batch": c.batch, "q_len": c.q_len,
+                   "kv_lens": "ragged" if name == "cfg5" else c.seq_lens[0], "kv_bytes": kb,
+                   "pools": len(ts), "us_per_call": round(msx * 1e3, 2),
+                   "call_kv_GBps": round(kb / (msx * 1e-3) / 1e9, 1),
+                   # Upper bounds: the library's events between the kernels add time.
+                   "partial_us_events": round(px * 1e3, 2), "merge_us_events": round(mx * 1e3, 2),
+                   "num_splits": pl[0], "pages_per_split": pl[1]}
+            prof_times = _profiled_times(profile_path(name, c.q_len, "fp16"))
+            if prof_times is not None:
+                row["rocprof"] = prof_times
+                row["kernel_us"] = prof_times["partial_us"]
+                row["kernel_us_source"] = "rocprof (committed profile of bench.py --config " + name + ")"
+            else:
+                row["kernel_us"] = round(px * 1e3, 2)
+                row["kernel_us_source"] = "events"
+            row["kernel_frac"] = round(kb / (row["kernel_us"] * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)
+            others[name] = row
+            del ts
             torch.cuda.empty_cache()
         result["other_configs"] = others
         tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")

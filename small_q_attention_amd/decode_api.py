@@ -64,11 +64,20 @@ def _kv_views(kv_cache, kv_layout: str):
     raise ValueError(f"kv_layout must be 'NHD' or 'HND', got {kv_layout!r}")
 
 
+def _on_device(t, device, what):
+    """ValueError unless ``t`` is a GPU tensor on ``device`` (raw pointers of host or
+    other-device memory must never reach a kernel)."""
+    if not getattr(t, "is_cuda", False) or t.device != device:
+        raise ValueError(f"{what} must be a GPU tensor on {device}")
+
+
 def _check_tensors(query, k, v, num_qo_heads: Optional[int] = None):
     import torch
 
-    if not query.is_cuda or not k.is_cuda:
+    if not query.is_cuda or not k.is_cuda or not v.is_cuda:
         raise ValueError("query and kv_cache must be GPU tensors")
+    if k.device != query.device or v.device != query.device:
+        raise ValueError("query and kv_cache must be on the same GPU")
     fp8 = getattr(torch, "float8_e4m3fn", None)
     if query.dtype not in (torch.float16, torch.bfloat16) or (
             k.dtype != query.dtype and (fp8 is None or k.dtype != fp8)):
@@ -105,12 +114,26 @@ def _run(query, k, v, block_tables, seq_lens, max_seq_len: int, q_len: int, scal
                          f"head_dim {d}")
     if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32:
         raise ValueError("block_tables and seq_lens must be int32")
+    # Every buffer the kernel reads or writes through a raw pointer: on the query's
+    # GPU, with the layout the kernel assumes (row-major block table, one length
+    # per request).
+    device = query.device
+    _on_device(block_tables, device, "block_tables")
+    _on_device(seq_lens, device, "seq_lens")
+    if block_tables.dim() != 2 or not block_tables.is_contiguous():
+        raise ValueError("block_tables must be a contiguous [batch, max_pages] tensor")
+    if seq_lens.dim() != 1 or seq_lens.numel() != batch or not seq_lens.is_contiguous():
+        raise ValueError(f"seq_lens must be a contiguous [{batch}] tensor")
     words = None if mask is None else as_words(mask, batch, q_len)
+    if words is not None:
+        _on_device(words, device, "mask")
     q4 = query.view(batch, q_len, hq, d)
     if out is None:
         out = torch.empty_like(query)
-    elif out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
-        raise ValueError("out must be a contiguous tensor shaped and typed like query")
+    else:
+        _on_device(out, device, "out")
+        if out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
+            raise ValueError("out must be a contiguous tensor shaped and typed like query")
     if plan is None:
         plan = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv, d,
                                 int(max_seq_len), block_tables.shape[1] * (k.shape[1] // PAGE_SIZE),
@@ -122,6 +145,7 @@ def _run(query, k, v, block_tables, seq_lens, max_seq_len: int, q_len: int, scal
         if workspace_buffer is None:
             ws = torch.empty(need, dtype=torch.uint8, device=query.device)
         else:
+            _on_device(workspace_buffer, device, "workspace_buffer")
             have = workspace_buffer.numel() * workspace_buffer.element_size()
             if have < need or not workspace_buffer.is_contiguous():
                 raise ValueError(f"workspace_buffer must be contiguous and hold at least {need} "
@@ -207,19 +231,49 @@ def csr_to_block_table(indptr, indices, last_page_len, page_size: int = PAGE_SIZ
     return block_tables.contiguous(), seq_lens.contiguous()
 
 
+def _capacity(kw, *names):
+    """Length of the first FlashInfer CUDA-graph buffer given under one of ``names``."""
+    for name in names:
+        buf = kw.get(name)
+        if buf is not None:
+            return int(buf.numel())
+    return None
+
+
 class _PagedWrapper:
-    """Plan once (CSR -> block table, split plan, workspace check), run per layer."""
+    """Plan once (CSR -> block table, split plan, workspace check), run per layer.
+
+    With ``use_cuda_graph=True`` the plan's block table and lengths live in
+    buffers fixed by the first ``plan()`` (width: the ``paged_kv_indices_buffer``
+    length when given, as FlashInfer sizes its graph buffers, else the first
+    plan's widest request) and every later ``plan()`` copies into them in place,
+    so kernels captured in a graph read the new plan on replay. The split plan
+    then covers the buffer's whole width (it may not depend on the lengths);
+    a re-plan that changes the batch, heads, draft length, mask or page size, or
+    needs a wider table, raises ``ValueError``.
+    """
 
     def __init__(self, float_workspace_buffer, kv_layout="NHD", use_cuda_graph=False,
-                 use_tensor_cores=False, **_unused):
+                 use_tensor_cores=False, **kw):
         if kv_layout not in ("NHD", "HND"):
             raise ValueError(f"kv_layout must be 'NHD' or 'HND', got {kv_layout!r}")
         self._workspace = float_workspace_buffer
         self._kv_layout = kv_layout
         self._planned = None
+        self._use_cuda_graph = bool(use_cuda_graph)
+        self._graph_width = _capacity(kw, "paged_kv_indices_buffer", "paged_kv_indices_buf")
+        self._graph = None  # persistent plan state in CUDA-graph mode
 
     def reset_workspace_buffer(self, float_workspace_buffer, *_unused):
         self._workspace = float_workspace_buffer
+
+    def _plan_device(self, indptr):
+        """Plan data lives where the kernels run: the workspace buffer's GPU when it
+        has one (CSR lists may come from the host, as FlashInfer allows)."""
+        ws = self._workspace
+        if ws is not None and getattr(ws, "is_cuda", False):
+            return ws.device
+        return indptr.device
 
     def _plan(self, indptr, indices, last_page_len, num_qo_heads, num_kv_heads, head_dim,
               page_size, q_len, mask_words, sm_scale, pos_encoding_mode, window_left,
@@ -242,12 +296,24 @@ class _PagedWrapper:
                              "64, 128 or 256")
         if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
             raise ValueError("num_qo_heads must be a multiple of num_kv_heads")
-        block_tables, seq_lens = csr_to_block_table(indptr, indices, last_page_len, page_size)
+        device = self._plan_device(indptr)
+        block_tables, seq_lens = csr_to_block_table(indptr.to(device), indices.to(device),
+                                                    last_page_len.to(device), page_size)
+        if mask_words is not None:
+            mask_words = mask_words.to(device)
         batch = block_tables.shape[0]
         max_seq_len = int(seq_lens.max()) if batch else 0
-        plan = _lib.plan_splits(block_tables.device.index or 0, batch, q_len, num_qo_heads,
-                                num_kv_heads, head_dim, max(max_seq_len, 1),
-                                block_tables.shape[1] * (page_size // PAGE_SIZE), 0)
+        shape = dict(batch=batch, q_len=q_len, hq=num_qo_heads, hkv=num_kv_heads,
+                     head_dim=head_dim, page_size=page_size,
+                     mask=None if mask_words is None else tuple(mask_words.shape))
+        if self._use_cuda_graph:
+            block_tables, seq_lens, mask_words, plan = self._graph_plan(
+                shape, block_tables, seq_lens, mask_words, device)
+            max_seq_len = 0
+        else:
+            plan = _lib.plan_splits(device.index or 0, batch, q_len, num_qo_heads, num_kv_heads,
+                                    head_dim, max(max_seq_len, 1),
+                                    block_tables.shape[1] * (page_size // PAGE_SIZE), 0)
         need = _lib.workspace_bytes(batch, q_len, num_qo_heads, num_kv_heads, head_dim, *plan)
         if need and self._workspace is not None:
             have = self._workspace.numel() * self._workspace.element_size()
@@ -260,10 +326,61 @@ class _PagedWrapper:
                              page_size=page_size, head_dim=head_dim,
                              scale=head_dim ** -0.5 if sm_scale is None else float(sm_scale))
 
-    def run(self, q, paged_kv_cache, *_unused, out=None, **_kw):
+    def _graph_plan(self, shape, block_tables, seq_lens, mask_words, device):
+        """Copy a plan into the persistent CUDA-graph buffers (allocated by the first plan)."""
+        import torch
+
+        g = self._graph
+        if g is None:
+            width = max(self._graph_width or 0, block_tables.shape[1], 1)
+            kernel_pages = width * (shape["page_size"] // PAGE_SIZE)
+            plan = _lib.plan_splits(device.index or 0, shape["batch"], shape["q_len"],
+                                    shape["hq"], shape["hkv"], shape["head_dim"], 0, kernel_pages,
+                                    0)
+            g = dict(shape=shape, plan=plan,
+                     block_tables=torch.zeros(shape["batch"], width, dtype=torch.int32,
+                                              device=device),
+                     seq_lens=torch.zeros(shape["batch"], dtype=torch.int32, device=device),
+                     mask=None if mask_words is None else torch.empty_like(mask_words))
+            self._graph = g
+        elif g["shape"] != shape:
+            raise ValueError(f"use_cuda_graph=True: a re-plan must keep {g['shape']}, got {shape}")
+        width = g["block_tables"].shape[1]
+        if block_tables.shape[1] > width:
+            raise ValueError(f"use_cuda_graph=True: this plan needs {block_tables.shape[1]} pages "
+                             f"per request, the graph buffers hold {width}")
+        g["block_tables"].zero_()
+        g["block_tables"][:, :block_tables.shape[1]].copy_(block_tables)
+        g["seq_lens"].copy_(seq_lens)
+        if mask_words is not None:
+            g["mask"].copy_(mask_words)
+        return g["block_tables"], g["seq_lens"], g["mask"], g["plan"]
+
+    def run(self, q, paged_kv_cache, *args, q_scale=None, k_scale=None, v_scale=None, out=None,
+            lse=None, return_lse=False, enable_pdl=None, window_left=None, sinks=None, **kwargs):
+        """FlashInfer's ``run`` keywords: ``q_scale`` and ``k_scale`` multiply the softmax
+        scale, ``v_scale`` the output (per-tensor FP8 scales); ``enable_pdl`` is a
+        launch hint and has no effect here. ``lse``/``return_lse``, sliding windows,
+        sinks, extra positional arguments and unknown keywords raise ``ValueError``."""
+        if args:
+            raise ValueError("run() takes (q, paged_kv_cache) positionally; pass the rest "
+                             "by keyword")
+        if kwargs:
+            raise ValueError(f"unsupported run() arguments: {sorted(kwargs)}")
+        if return_lse or lse is not None:
+            raise ValueError("returning the log-sum-exp (lse / return_lse) is not supported")
+        if window_left not in (None, -1):
+            raise ValueError("sliding windows are not supported (window_left must be -1)")
+        if sinks is not None:
+            raise ValueError("attention sinks are not supported")
         if self._planned is None:
             raise RuntimeError("plan() must be called before run()")
         p = self._planned
+        scale = p["scale"]
+        for name, x in (("q_scale", q_scale), ("k_scale", k_scale)):
+            if x is not None:
+                scale *= _scalar(x, name)
+        out_scale = 1.0 if v_scale is None else _scalar(v_scale, "v_scale")
         k, v = _kv_views(paged_kv_cache, self._kv_layout)
         _check_tensors(q, k, v, p["hq"])
         if k.shape[2] != p["hkv"]:
@@ -275,7 +392,7 @@ class _PagedWrapper:
             raise ValueError(f"kv_cache pages hold {k.shape[1]} tokens, plan() was given "
                              f"{p['page_size']}")
         return _run(q, k, v, p["block_tables"], p["seq_lens"], p["max_seq_len"], p["q_len"],
-                    p["scale"], 1.0, p["mask_words"], self._workspace, out, plan=p["plan"])
+                    scale, out_scale, p["mask_words"], self._workspace, out, plan=p["plan"])
 
     forward = run
 

@@ -15,11 +15,20 @@ are appended to ``--output`` as they complete. Added columns:
 * ``kv_bytes``, ``kv_GBps`` and ``pct_peak`` (KV bytes over ``kernel_p50_us``),
   ``call_GBps`` (over ``p50_us``), ``num_splits``, ``pages_per_split``;
 * ``pools``: KV sets smaller than the 256 MB MALL are rotated through this many
-  distinct pools so repeats do not read from the cache (``mall_resident`` says
-  whether one pool alone would fit).
+  distinct pools (together at least twice the MALL) so repeats do not read from
+  the cache (``mall_resident`` says whether one pool alone would fit);
+* ``b2b_us``: mean time per call over ``repeats`` calls issued back to back
+  through the C ABI (events only around the batch of calls), rotating the
+  pools: what a decode loop sees, without the per-call synchronisation of
+  ``p50_us`` and without the inter-kernel events of ``kernel_p50_us``, which
+  are upper bounds.
 
-Correctness is not checked here: the parity tests in ``tests/`` compare every
-case with the CPU oracle.
+``--check-correctness`` (with ``--correctness-limit``, default 3 cases, as in
+``run_gpu_matrix.py:126-127,159-169``) adds ``max_abs_error`` and
+``max_rel_error`` of the call's output against the float32 checker
+(:mod:`small_q_attention_amd.checker`) rounded to fp16, as the reference runner
+compares with its CPU oracle rounded to fp16, plus ``within_tolerance``
+(``|a - r| <= 2e-3 + 1e-2 |r|``). The full parity suite is ``tests/``.
 """
 
 from __future__ import annotations
@@ -83,7 +92,22 @@ def _events(torch, n):
     return evs
 
 
-def measure_case(torch, variant, case, page_mode, chunk_keys, warmup, repeats, seed, max_pools=4):
+def check_case(torch, forward, tensors, page_size, num_kv_heads):
+    """``max_abs_error`` / ``max_rel_error`` of one call against the float32 checker
+    rounded to fp16 (``run_gpu_matrix.py:159-169``), and the parity bar."""
+    from .checker import attention_fp32
+
+    actual = forward(*tensors, page_size)
+    ref = torch.from_numpy(attention_fp32(*tensors, page_size, num_kv_heads))
+    ref = ref.to(device=actual.device, dtype=torch.float16).float()
+    err = (actual.float() - ref).abs()
+    return {"max_abs_error": err.max().item(),
+            "max_rel_error": (err / ref.abs().clamp_min(1e-5)).max().item(),
+            "within_tolerance": bool((err <= 2e-3 + 1e-2 * ref.abs()).all().item())}
+
+
+def measure_case(torch, variant, case, page_mode, chunk_keys, warmup, repeats, seed,
+                 max_pools=160, check=False):
     from . import _lib, inputs
 
     c = inputs.uniform_case(case["batch_size"], case["q_len"], case["kv_len"], page_mode=page_mode,
@@ -129,6 +153,14 @@ def measure_case(torch, variant, case, page_mode, chunk_keys, warmup, repeats, s
         for i in range(4):
             _lib.launch(*sets[i % pools], outs[i % pools], ws, ns, pps, stream)
         torch.cuda.synchronize()
+    b0, b1 = _events(torch, 2)
+    torch.cuda.synchronize()
+    b0.record()
+    for i in range(repeats):
+        _lib.launch(*sets[i % pools], outs[i % pools], ws, ns, pps, stream)
+    b1.record()
+    torch.cuda.synchronize()
+    b2b = b0.elapsed_time(b1) * 1000.0 / repeats
     for i in range(repeats):
         s = sets[i % pools]
         _lib.launch(*s, outs[i % pools], ws, ns, pps, stream,
@@ -139,17 +171,21 @@ def measure_case(torch, variant, case, page_mode, chunk_keys, warmup, repeats, s
     kvb = inputs.kv_bytes(c.seq_lens, c.num_kv_heads, c.head_dim)
     kern = statistics.median(part) + statistics.median(merge)
     p50 = statistics.median(samples)
-    del sets
-    return {
+    row = {
         "p50_us": p50, "p99_us": _percentile(samples, 0.99), "min_us": min(samples),
         "max_us": max(samples),
         "kernel_p50_us": statistics.median(part), "merge_p50_us": statistics.median(merge),
+        "b2b_us": b2b, "b2b_kv_GBps": kvb / (b2b * 1e-6) / 1e9,
         "kv_bytes": kvb, "kv_GBps": kvb / (kern * 1e-6) / 1e9,
         "pct_peak": 100.0 * kvb / (kern * 1e-6) / 1e9 / PEAK_HBM_GBPS,
         "call_GBps": kvb / (p50 * 1e-6) / 1e9,
         "num_splits": ns, "pages_per_split": pps, "pools": pools,
         "mall_resident": pool_bytes / 2 <= MALL_BYTES,
     }
+    if check:
+        row.update(check_case(torch, forward, sets[0], page, c.num_kv_heads))
+    del sets
+    return row
 
 
 def main(argv=None):
@@ -169,6 +205,10 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--repeats", type=int, default=15)
     ap.add_argument("--limit", type=int, default=0, help="cases per variant; 0 = all")
+    ap.add_argument("--check-correctness", action="store_true",
+                    help="add max_abs_error / max_rel_error against the float32 checker")
+    ap.add_argument("--correctness-limit", type=int, default=3,
+                    help="cases checked when --check-correctness is given")
     ap.add_argument("--output", type=Path, help="JSONL file rows are appended to")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
@@ -181,6 +221,7 @@ def main(argv=None):
     cases = [dict(q_len=q, kv_len=kv, batch_size=b, token_group=args.token_group, **fixed)
              for q, kv, b in itertools.product(args.q_lens, args.kv_lens, args.batch_sizes)]
     device_name = torch.cuda.get_device_name(0)
+    checked = 0
     for variant in args.variants:
         for index, case in enumerate(cases):
             if args.limit and index >= args.limit:
@@ -193,10 +234,12 @@ def main(argv=None):
             if estimated > int(free_bytes * 0.70):
                 row.update(status="skipped", reason="estimated_memory_limit")
             else:
+                check = args.check_correctness and checked < args.correctness_limit
                 try:
                     row.update(status="ok", **measure_case(
                         torch, variant, case, args.page_mode, args.chunk_keys, args.warmup,
-                        args.repeats, seed=1000 + index))
+                        args.repeats, seed=1000 + index, check=check))
+                    checked += int(check)
                 except (ValueError, RuntimeError) as exc:
                     row.update(status="error", reason=str(exc))
             line = json.dumps(row, sort_keys=True)

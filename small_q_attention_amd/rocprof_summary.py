@@ -123,6 +123,9 @@ def main(argv=None):
                              "dispatches = the bench's timed steps)")
                 lines.append(f"partial_kernel_timed_steps_kv_GBps: "
                              f"{args.kv_bytes / (t * 1e-6) / 1e9:.1f}")
+        if name.startswith("sqa_merge_kernel") and name in timed:
+            lines.append(f"merge_kernel_timed_steps_avg_us: {timed[name]:.2f} (last "
+                         f"{args.steps} dispatches)")
     if partial_traffic is not None:
         lines.append(f"traffic_bytes_per_launch: {partial_traffic:.0f}")
     if args.mfma:

@@ -68,3 +68,29 @@ def test_wrappers_reject_unsupported_plans():
                  custom_mask=torch.ones(8, dtype=torch.bool))
     with pytest.raises(ValueError, match="kv_layout"):
         fi.BatchPrefillWithPagedKVCacheWrapper(None, "NDH")
+
+
+@pytest.mark.parametrize("call,match", [
+    (lambda w, q, kv: w.run(q, kv, None), "positionally"),
+    (lambda w, q, kv: w.run(q, kv, return_lse=True), "lse"),
+    (lambda w, q, kv: w.run(q, kv, lse=torch.zeros(1)), "lse"),
+    (lambda w, q, kv: w.run(q, kv, window_left=128), "window"),
+    (lambda w, q, kv: w.run(q, kv, sinks=torch.zeros(32)), "sinks"),
+    (lambda w, q, kv: w.run(q, kv, logits_soft_cap=30.0), "unsupported run"),
+])
+def test_wrapper_run_rejects_what_it_would_otherwise_drop(call, match):
+    """FlashInfer run() arguments this build cannot honour raise instead of being ignored
+    (checked before the plan and before any tensor reaches the library)."""
+    q = torch.zeros(2, 32, 128, dtype=torch.float16)
+    kv = torch.zeros(3, 2, 16, 8, 128, dtype=torch.float16)
+    for cls in (fi.BatchDecodeWithPagedKVCacheWrapper, fi.BatchPrefillWithPagedKVCacheWrapper):
+        with pytest.raises(ValueError, match=match):
+            call(cls(None, "NHD"), q, kv)
+
+
+def test_run_checks_every_pointer_argument_for_the_device():
+    """The shared launch refuses host tensors for each raw-pointer argument (the GPU
+    tests repeat this on a real device with the rest of the call valid)."""
+    q, kv, _, bt, sl, msl, s1, s2 = _args()
+    with pytest.raises(ValueError, match="GPU"):
+        fi.xqa_batch_decode_with_kv_cache(q, kv, None, bt, sl, msl, s1, s2, q_len_per_req=4)

@@ -324,3 +324,118 @@ def test_larger_cache_pages_full_size():
     assert torch.equal(out64, out16)
     cq, ck, cv, cbt, csl = compact_sequences(q, k16, v16, bt16, sl, [0, 11])
     assert_parity(out64[[0, 11]], attention_c64(cq, ck, cv, cbt, csl, 16, 8), label="cfg3 p64")
+
+
+def test_buffers_off_the_device_or_misshaped_raise_before_any_launch():
+    """Every raw-pointer argument is checked before the launch: host memory, the wrong
+    length or a strided view raises ValueError and leaves ``out`` untouched."""
+    q_len, lens = 4, [100, 200]
+    q, k, v, bt, sl = _inputs(lens, q_len, seed=2)
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    out = torch.full_like(_flat(q), float("nan"))
+    mask = spec_dec_mask(2, q_len)
+    wide = torch.zeros(2, 2 * bt.shape[1], dtype=torch.int32, device="cuda")
+    wide[:, ::2] = bt
+    cases = {
+        "block_tables on the host": dict(block_tables=bt.cpu()),
+        "seq_lens on the host": dict(seq_lens=sl.cpu()),
+        "seq_lens shorter than the batch": dict(seq_lens=sl[:1]),
+        "strided block_tables": dict(block_tables=wide[:, ::2]),
+        "strided seq_lens": dict(seq_lens=torch.stack([sl, sl], 1)[:, 0]),
+        "value cache on the host": dict(kv_cache=(k, v.cpu())),
+        "mask on the host": dict(mask=mask),
+        "workspace on the host": dict(workspace_buffer=ws.cpu()),
+        "out on the host": dict(out=out.cpu()),
+    }
+    for label, change in cases.items():
+        args = dict(query=_flat(q), kv_cache=_nhd(k, v), workspace_buffer=ws, block_tables=bt,
+                    seq_lens=sl, max_seq_len=200, bmm1_scale=0.1, bmm2_scale=1.0, out=out,
+                    q_len_per_req=q_len, mask=mask.cuda())
+        args.update(change)
+        with pytest.raises(ValueError):
+            fi.xqa_batch_decode_with_kv_cache(**args)
+        torch.cuda.synchronize()
+        assert torch.isnan(out).all(), label
+
+
+def test_wrapper_plans_host_csr_onto_the_workspace_device():
+    """CSR lists on the host (FlashInfer allows it) are moved to the workspace's GPU at
+    plan time, so run() reads device memory."""
+    q_len, lens = 2, [700, 33, 4000]
+    indptr, ids, last, pool = _csr(lens, seed=21)
+    g = torch.Generator().manual_seed(21)
+    kv = torch.randn(pool, 2, 16, 8, 128, generator=g).half().cuda()
+    q = torch.randn(len(lens) * q_len, 32, 128, generator=g).half().cuda()
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    dec = fi.BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
+    dec.plan(indptr, ids, last, 32, 8, 128, 16, q_len_per_req=q_len)
+    bt, sl = fi.csr_to_block_table(indptr, ids, last)
+    q4 = q.view(len(lens), q_len, 32, 128)
+    assert_parity(dec.run(q, kv).view_as(q4), _oracle(q4, kv[:, 0], kv[:, 1], bt, sl))
+
+
+def test_wrapper_run_scales():
+    """run(k_scale=, q_scale=, v_scale=): the first two multiply the softmax scale, the
+    last the output (per-tensor FP8 scales in FlashInfer)."""
+    q_len, lens = 4, [300, 2000]
+    indptr, ids, last, pool = _csr(lens, seed=22)
+    g = torch.Generator().manual_seed(22)
+    kv = torch.randn(pool, 2, 16, 8, 128, generator=g).half().cuda()
+    q = torch.randn(len(lens) * q_len, 32, 128, generator=g).half().cuda()
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    dec = fi.BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
+    dec.plan(indptr.cuda(), ids.cuda(), last.cuda(), 32, 8, 128, 16, q_len_per_req=q_len,
+             sm_scale=0.2)
+    bt, sl = fi.csr_to_block_table(indptr, ids, last)
+    q4 = q.view(len(lens), q_len, 32, 128)
+    got = dec.run(q, kv, k_scale=0.5, q_scale=torch.tensor(0.75), v_scale=2.0)
+    ref = _oracle(q4, kv[:, 0], kv[:, 1], bt, sl, scale=0.2 * 0.5 * 0.75, out_scale=2.0)
+    assert_parity(got.view_as(q4), ref, label="scales")
+
+
+def test_cuda_graph_wrapper_replans_in_place():
+    """use_cuda_graph=True: plan() copies each new plan into buffers fixed by the first, so
+    one captured run() serves every later plan (new lengths, new pages), each replay
+    checked against the oracle; a plan that changes the batch or outgrows the buffers
+    raises."""
+    q_len, hq, hkv = 4, 32, 8
+    lens_seq = [[900, 40, 2500], [1500, 700, 16], [4000, 4, 333]]
+    g = torch.Generator().manual_seed(23)
+    pool = 2 * sum(-(-n // 16) for lens in lens_seq for n in lens) + 7
+    kv = torch.randn(pool, 2, 16, hkv, 128, generator=g).half().cuda()
+    q = torch.randn(3 * q_len, hq, 128, generator=g).half().cuda()
+    ws = torch.zeros(WORKSPACE, dtype=torch.uint8, device="cuda")
+    indices_buf = torch.zeros(600, dtype=torch.int32, device="cuda")
+    dec = fi.BatchDecodeWithPagedKVCacheWrapper(ws, "NHD", use_cuda_graph=True,
+                                                paged_kv_indices_buffer=indices_buf)
+    csrs = [_csr(lens, seed=30 + i, pool_pages=pool) for i, lens in enumerate(lens_seq)]
+    indptr, ids, last, _ = csrs[0]
+    dec.plan(indptr, ids, last, hq, hkv, 128, 16, q_len_per_req=q_len)
+    out = torch.empty_like(q)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        dec.run(q, kv, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        dec.run(q, kv, out=out)
+    q4 = q.view(3, q_len, hq, 128)
+    for rnd in range(2):
+        for i, (indptr, ids, last, _) in enumerate(csrs):
+            dec.plan(indptr, ids, last, hq, hkv, 128, 16, q_len_per_req=q_len)
+            out.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            bt, sl = fi.csr_to_block_table(indptr, ids, last)
+            assert_parity(out.view_as(q4), _oracle(q4, kv[:, 0], kv[:, 1], bt, sl),
+                          label=f"round {rnd} plan {i}")
+            junk = torch.randn(1 << 20, device="cuda").sum()  # eager work between replays
+            torch.cuda.synchronize()
+            del junk
+    with pytest.raises(ValueError, match="re-plan"):
+        two = _csr([100, 200], seed=40, pool_pages=pool)
+        dec.plan(two[0], two[1], two[2], hq, hkv, 128, 16, q_len_per_req=q_len)
+    with pytest.raises(ValueError, match="graph buffers"):
+        big = _csr([16 * 700, 16, 16], seed=41, pool_pages=pool + 800)
+        dec.plan(big[0], big[1], big[2], hq, hkv, 128, 16, q_len_per_req=q_len)
