@@ -49,11 +49,14 @@ extern "C" {
  *     sequence b's splits are b * num_splits + s, split s covering pages
  *     [s * pages_per_split, (s + 1) * pages_per_split).
  *   chunk_keys == 0: automatic, sized from the device's compute-unit count.
- *     For 2 <= batch <= 256 this is the balanced plan, *pages_per_split = 0:
+ *     For 2 <= batch <= 256 this is the balanced plan, *pages_per_split <= 0:
  *     *num_splits work-item slots are shared by the whole batch and the kernel
  *     sizes the splits on the device from the sum of seq_lens, so ragged
- *     batches spread evenly over the chip without a host sync. Otherwise a
- *     fixed plan as above.
+ *     batches spread evenly over the chip without a host sync. With
+ *     max_seq_len > 0 it is -P, P = ceil(max_seq_len / 16) (at most max_pages):
+ *     the kernels first assume every sequence spans P pages, which saves a
+ *     memory round trip when it holds, and verify it (the result is the same
+ *     either way). Otherwise a fixed plan as above.
  * max_pages: 16-token pages a block-table row addresses (block_tables columns
  * x page_size / 16); num_splits and pages_per_split count 16-token pages too.
  * max_seq_len <= 0 means "unknown": a fixed plan covers max_pages * 16 tokens.
@@ -79,8 +82,9 @@ size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv
  * Replaces the launchers small_q_attention_v0..v5 and their pybind entries
  * forward, forward_v1..forward_v5 (csrc/small_q_attention_ext.cu:969-1378,
  * :1380-1390). num_splits/pages_per_split come from sqa_plan_splits
- * (pages_per_split 0: balanced plan, batch <= 256 and num_splits >= batch +
- * max(1, ceil(batch * max_pages * page_size / 16 / 2048))); max_pages is the
+ * (pages_per_split 0 or -P: balanced plan, batch <= 256, P <= max_pages * page_size / 16
+ * and num_splits >= batch + max(1, ceil(batch * max_pages * page_size / 16 / 2048)));
+ * max_pages is the
  * block_tables row length. head_dim is 128 (the reference's), 64 or 256;
  * 256 needs q_len * num_query_heads / num_kv_heads <= 32. `workspace` must hold
  * sqa_workspace_bytes(...) bytes, 16-byte aligned (may be NULL when that is 0). query

@@ -111,7 +111,9 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
       if ((target + batch) * num_kv_heads > 0x7fffffffLL)
         return fail(SQA_ERR_INVALID, "grid too large");
       *num_splits = (int)(target + batch);
-      *pages_per_split = 0;
+      // With a known max_seq_len the kernels first assume every sequence spans
+      // that many pages (and check it): -pages.
+      *pages_per_split = max_seq_len > 0 ? -(int)pages : 0;
       return SQA_OK;
     }
     const long long splits = ceil_div(slots_target, batch);
@@ -138,7 +140,7 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
 size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv_heads,
                            int head_dim, int num_splits, int pages_per_split) {
   if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_query_heads <= 0 || head_dim <= 0 ||
-      num_splits <= 0 || pages_per_split < 0)
+      num_splits <= 0)
     return 0;
   const bool balanced = sqa::is_balanced(pages_per_split);
   if (!balanced && num_splits == 1) return 0;
@@ -216,19 +218,26 @@ int run_attention(const sqa_attention_args& a) {
                 a.mask_words);
   if (!(a.scale > 0.f) || !isfinite(a.scale) || !isfinite(a.out_scale))
     return fail(SQA_ERR_INVALID, "scale must be positive and finite, out_scale finite");
-  if (num_splits <= 0 || pages_per_split < 0)
-    return fail(SQA_ERR_INVALID, "num_splits must be positive and pages_per_split non-negative");
+  if (num_splits <= 0) return fail(SQA_ERR_INVALID, "num_splits must be positive");
   if (pages_per_split > sqa::kMaxSplitPages)
     return fail(SQA_ERR_INVALID, "pages_per_split %d exceeds %d", pages_per_split,
                 sqa::kMaxSplitPages);
   const bool balanced = sqa::is_balanced(pages_per_split);
+  const int spec_pages = sqa::spec_pages_of(pages_per_split);
   if (balanced) {
-    // pages_per_split == 0 selects the balanced plan (sqa_plan_splits).
+    // pages_per_split <= 0 selects the balanced plan (sqa_plan_splits); -P expects
+    // P pages in every sequence.
+    if (spec_pages > kernel_pages)
+      return fail(SQA_ERR_INVALID,
+                  "balanced plan expects %d pages per sequence; block_tables rows hold %lld",
+                  spec_pages, kernel_pages);
     if (batch > sqa::kMaxBalancedBatch)
       return fail(SQA_ERR_INVALID, "balanced plan (pages_per_split 0) needs batch <= %d, got %d",
                   sqa::kMaxBalancedBatch, batch);
     if (kernel_pages >= (1LL << 24))
       return fail(SQA_ERR_INVALID, "balanced plan needs block-table rows under 2^28 tokens");
+    if ((long long)batch * kernel_pages >= (1LL << 31))
+      return fail(SQA_ERR_INVALID, "balanced plan needs batch * pages per row under 2^31");
     const long long cap = ceil_div((long long)batch * kernel_pages, sqa::kMaxSplitPages);
     if ((long long)num_splits - batch < (cap > 1 ? cap : 1))
       return fail(SQA_ERR_INVALID,
@@ -283,8 +292,13 @@ int run_attention(const sqa_attention_args& a) {
   pa.bt_stride = max_pages;
   pa.page_shift = page_shift;
   pa.max_pages = (int)kernel_pages;
-  pa.pages_per_split = pages_per_split;
+  pa.pages_per_split = balanced ? 0 : pages_per_split;
   pa.num_splits = num_splits;
+  pa.spec_pages = spec_pages;
+  pa.spec_pps = pa.spec_splits = 0;
+  if (spec_pages > 0)
+    sqa::uniform_balanced_plan(batch, num_splits - batch, spec_pages, &pa.spec_pps,
+                               &pa.spec_splits);
   pa.scale_log2 = (float)(1.4426950408889634 * (double)a.scale);
   pa.out_scale = a.out_scale;
   pa.bf16 = a.dtype == SQA_DTYPE_BF16;
@@ -309,8 +323,10 @@ int run_attention(const sqa_attention_args& a) {
     ma.rows = (int)rows;
     ma.head_dim = head_dim;
     ma.max_pages = (int)kernel_pages;
-    ma.pages_per_split = pages_per_split;
+    ma.pages_per_split = pa.pages_per_split;
     ma.num_splits = num_splits;
+    ma.spec_pages = spec_pages;
+    ma.spec_splits = pa.spec_splits;
     ma.out_scale = a.out_scale;
     ma.bf16 = pa.bf16;
     if ((e = sqa::launch_merge(ma, s)) != hipSuccess) return hip_fail(e, "merge kernel launch");

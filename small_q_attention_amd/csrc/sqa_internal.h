@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 namespace sqa {
 
 constexpr int kHeadDim = 128;   // the reference's head_dim; 64 and 256 are also built
@@ -34,6 +36,19 @@ struct SeqSplits {
 // same number of pages whatever the length distribution. Partial slot of
 // (sequence, split) = first slot of the sequence + split; sequences whose
 // pages fit one split are written straight to the output.
+//
+// spec_pages > 0 (balanced plan only): the page count the caller expects every
+// sequence to have (from max_seq_len), with the plan for that case computed by
+// the host (uniform_balanced_plan: spec_pps pages per split, spec_splits splits
+// per sequence, sequence b's splits in slots b * spec_splits + s). Workgroups
+// take their item from it and issue their first page-id loads together with the
+// lengths; a length that does not match sends the workgroup back to the plan
+// from the loaded lengths. Either way the plan is the one the lengths give
+// (for equal page counts both rules pick the same split size): the expectation
+// only saves a memory round trip and the plan's wave reductions when it holds.
+//
+// The C ABI carries spec_pages in pages_per_split: 0 is the balanced plan,
+// -P the balanced plan expecting P pages per sequence.
 struct PartialArgs {
   const _Float16* q;          // [B, Q, Hq, head_dim]
   const _Float16* k;          // K of page 0, slot 0, kv head 0
@@ -57,13 +72,20 @@ struct PartialArgs {
   int page_shift;             // cache page = 16 << page_shift tokens = 1 << page_shift kernel pages
   int max_pages;              // kernel pages a block-table row addresses (bt_stride << page_shift)
   int pages_per_split, num_splits;
+  int spec_pages;             // balanced plan: expected pages of every sequence (0: none)
+  int spec_pps, spec_splits;  // the balanced plan when every sequence spans spec_pages pages
   float scale_log2;           // softmax scale * log2(e)
   float out_scale;            // multiplier applied to the normalised output
   int bf16;                   // element type of Q and out (and of K, V unless kv_fp8): 0 fp16, 1 bf16
   int kv_fp8;                 // K and V hold OCP e4m3 bytes
 };
 
-__host__ __device__ inline bool is_balanced(int pages_per_split) { return pages_per_split == 0; }
+// pages_per_split as the C ABI carries it: > 0 fixed plan, 0 balanced, -P balanced
+// expecting P pages per sequence.
+__host__ __device__ inline bool is_balanced(int pages_per_split) { return pages_per_split <= 0; }
+__host__ __device__ inline int spec_pages_of(int pages_per_split) {
+  return pages_per_split < 0 ? -pages_per_split : 0;
+}
 
 // Partial slots a plan uses.
 inline long long plan_slots(int batch, int num_splits, int pages_per_split) {
@@ -80,9 +102,41 @@ struct MergeArgs {
   int head_dim;
   int max_pages;  // kernel pages a block-table row addresses
   int pages_per_split, num_splits;
+  int spec_pages;   // balanced plan: expected pages of every sequence (0: none)
+  int spec_splits;  // splits per sequence of the balanced plan when that holds
   float out_scale;
   int bf16;
 };
+
+// The balanced plan's split size and split count when all `batch` sequences span
+// `pages` pages and `target` (= num_splits - batch) work items are to be filled:
+// the smallest size from ceil(total / target) up (clamped to [kMinSplitPages,
+// kMaxSplitPages], at most ceil(total / (target - batch)) when target > batch)
+// whose split counts fit the target. The kernels' balanced plan applies the same
+// rule to the loaded page counts (requires batch * pages < 2^31).
+inline void uniform_balanced_plan(int batch, int target, int pages, int* pps_out,
+                                  int* splits_out) {
+  const int total = batch * pages;
+  const int lo = std::min(std::max((total + target - 1) / target, kMinSplitPages), kMaxSplitPages);
+  int hi = lo;
+  if (target > batch)
+    hi = std::min(std::max((total + target - batch - 1) / (target - batch), lo), kMaxSplitPages);
+  auto count = [&](int size) { return (long long)batch * ((pages + size - 1) / size); };
+  int pps = lo;
+  if (hi > lo && count(lo) > target) {
+    int l = lo + 1, h = hi;
+    while (l < h) {
+      const int mid = (l + h) >> 1;
+      if (count(mid) <= target)
+        h = mid;
+      else
+        l = mid + 1;
+    }
+    pps = h;
+  }
+  *pps_out = pps;
+  *splits_out = (pages + pps - 1) / pps;
+}
 
 // Launch shape of the partial kernel for a given number of query rows per kv
 // head. A workgroup serves `heads` kv heads of one (sequence, split), `hpw`

@@ -550,29 +550,26 @@ __device__ __forceinline__ int wave_inclusive_scan_int(int v) {
 // Balanced plan (batch <= kMaxBalancedBatch = 4 x 64). num_splits = T + batch
 // slots, T = the work items one wave of resident workgroups holds. Every wave
 // derives the same plan on its own, with wave reductions only (no LDS, no
-// barrier): lane l takes sequences l, l + 64, l + 128, l + 192, and the wave
-// picks one split size for the batch: the smallest in [ceil(total / T),
-// ceil(total / (T - batch))] (clamped to [kMinSplitPages, kMaxSplitPages])
-// whose per-sequence split counts sum to at most T (bisection), so no
-// workgroup waits for a second wave; the lower end alone always fits the
-// T + batch slots. A scan of the split counts gives each sequence its first
-// slot, and the lane whose sequence holds `item` hands its range to the wave.
-// Wave 0 of workgroup 0 also stores every sequence's (first slot, split
-// count) for the merge kernel. Every workgroup computes the same plan from the
-// same seq_lens.
-__device__ ItemRange balanced_item(const PartialArgs& a, int item) {
-  constexpr int K = kMaxBalancedBatch / 64;
+// barrier), from per-lane page counts: lane l holds sequences l, l + 64,
+// l + 128, l + 192, and the wave picks one split size for the batch: the
+// smallest in [ceil(total / T), ceil(total / (T - batch))] (clamped to
+// [kMinSplitPages, kMaxSplitPages]) whose per-sequence split counts sum to at
+// most T (bisection), so no workgroup waits for a second wave; the lower end
+// alone always fits the T + batch slots. A scan of the split counts gives each
+// sequence its first slot, and the lane whose sequence holds `item` hands its
+// range to the wave. With write_table, wave 0 stores every sequence's (first
+// slot, split count) for the merge kernel. The range's `len` is left for the
+// caller. Every workgroup computes the same plan from the same page counts.
+constexpr int kSeqPerLane = kMaxBalancedBatch / 64;
+
+__device__ ItemRange balanced_plan(const PartialArgs& a, int item, const int (&pages)[kSeqPerLane],
+                                   bool write_table) {
+  constexpr int K = kSeqPerLane;
   const int lane = threadIdx.x & 63;
   const int groups = (a.batch + 63) / 64;  // uniform; groups of 64 sequences in use
-  int len[K], pages[K];
   int total = 0;
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int sq = 64 * k + lane;
-    len[k] = k < groups && sq < a.batch ? max(a.seq_lens[min(sq, a.batch - 1)], 0) : 0;
-    pages[k] = min((len[k] + kPageSize - 1) / kPageSize, a.max_pages);
-    total += pages[k];
-  }
+  for (int k = 0; k < K; ++k) total += pages[k];
   total = wave_sum_int(total);
   // ceil(n / size) for a uniform size: float reciprocal, then one correction
   // each way (n < 2^24, so the estimate is off by at most one).
@@ -623,15 +620,13 @@ __device__ ItemRange balanced_item(const PartialArgs& a, int item) {
     const int incl = wave_inclusive_scan_int(splits);
     const int first = base + incl - splits;
     const int sq = 64 * k + lane;
-    if (blockIdx.x == 0 && threadIdx.x < 64 && sq < a.batch)
-      a.seq_splits[sq] = SeqSplits{first, splits};
+    if (write_table && threadIdx.x < 64 && sq < a.batch) a.seq_splits[sq] = SeqSplits{first, splits};
     const bool mine = sq < a.batch && item >= first && item < first + splits;
     const unsigned long long hit = __ballot(mine);
     if (hit) {
       const int src = __builtin_ctzll(hit);
       r.b = 64 * k + src;
       r.split = item - __shfl(first, src);
-      r.len = __shfl(len[k], src);
       r.slot0 = __shfl(first, src);
       r.n_valid = __shfl(splits, src);
       r.p_begin = r.split * pps;
@@ -640,6 +635,32 @@ __device__ ItemRange balanced_item(const PartialArgs& a, int item) {
     base += __shfl(incl, 63);
   }
   return r;
+}
+
+// Lengths of sequences l, l + 64, l + 128, l + 192 in lane l (0 past the batch)
+// and their page counts (clamped to the block-table row). The loads are
+// unconditional, from clamped in-bounds addresses, and selected afterwards: a
+// load under a branch is waited for where the branch joins, which would put a
+// full memory round trip in front of whatever follows.
+__device__ __forceinline__ void load_lengths(const PartialArgs& a, int (&len)[kSeqPerLane],
+                                             int (&pages)[kSeqPerLane]) {
+  const int lane = threadIdx.x & 63;
+  int raw[kSeqPerLane];
+#pragma unroll
+  for (int k = 0; k < kSeqPerLane; ++k) raw[k] = a.seq_lens[min(64 * k + lane, a.batch - 1)];
+#pragma unroll
+  for (int k = 0; k < kSeqPerLane; ++k) {
+    len[k] = 64 * k + lane < a.batch ? max(raw[k], 0) : 0;
+    pages[k] = min((len[k] + kPageSize - 1) / kPageSize, a.max_pages);
+  }
+}
+
+// The length of sequence b (uniform) from the per-lane lengths.
+__device__ __forceinline__ int length_of(const int (&len)[kSeqPerLane], int b) {
+  int v = len[0];
+#pragma unroll
+  for (int k = 1; k < kSeqPerLane; ++k) v = (b >> 6) == k ? len[k] : v;
+  return __shfl(v, b & 63);
 }
 
 // One workgroup = one (sequence b, split) x WW waves; wave w serves the HPW kv
@@ -696,11 +717,49 @@ void sqa_partial_kernel(PartialArgs a) {
     for (int j = 0; j < D; ++j)
       first_id[j] = row[min(max(p0 + j, 0), a.max_pages - 1) >> a.page_shift];
   };
+  ItemRange it;
+  bool ids_loaded = !balanced;  // uniform
   if (!balanced) {
     const int seq = item / a.num_splits;
     load_first_ids(seq, (item - seq * a.num_splits) * a.pages_per_split);
+    it = fixed_item(a, item);
+  } else {
+    int len[kSeqPerLane], pages[kSeqPerLane];
+    if (a.spec_pages > 0) {
+      // The item from the host's plan for the expected page count (sequence b's
+      // splits in slots b * spec_splits + s), then its first page ids and all
+      // lengths in one round trip.
+      const int ks = a.spec_splits, P = a.spec_pages;
+      it.b = item < a.batch * ks ? item / ks : -1;
+      it.split = it.b >= 0 ? item - it.b * ks : 0;
+      it.p_begin = it.split * a.spec_pps;
+      it.p_end = it.b >= 0 ? min(it.p_begin + a.spec_pps, P) : 0;
+      it.slot0 = it.b >= 0 ? it.b * ks : 0;
+      it.n_valid = it.b >= 0 ? ks : 0;
+      if (blockIdx.x == 0 && threadIdx.x < 64) {
+#pragma unroll
+        for (int k = 0; k < kSeqPerLane; ++k) {
+          const int sq = 64 * k + lane;
+          if (sq < a.batch) a.seq_splits[sq] = SeqSplits{sq * ks, ks};
+        }
+      }
+      load_first_ids(max(it.b, 0), it.p_begin);
+      load_lengths(a, len, pages);
+      bool differs = false;
+#pragma unroll
+      for (int k = 0; k < kSeqPerLane; ++k)
+        differs |= 64 * k + lane < a.batch && pages[k] != P;
+      if (__any(differs)) {
+        it = balanced_plan(a, item, pages, blockIdx.x == 0);  // rewrites the table
+      } else {
+        ids_loaded = true;
+      }
+    } else {
+      load_lengths(a, len, pages);
+      it = balanced_plan(a, item, pages, blockIdx.x == 0);
+    }
+    it.len = it.b >= 0 ? length_of(len, it.b) : 0;
   }
-  ItemRange it = balanced ? balanced_item(a, item) : fixed_item(a, item);
   // The work item is the same for the whole workgroup; saying so keeps it (and
   // the buffer-resource addresses built from it) in scalar registers.
   it.b = __builtin_amdgcn_readfirstlane(it.b);
@@ -719,14 +778,35 @@ void sqa_partial_kernel(PartialArgs a) {
   const int32_t* bt_row = a.block_tables + (size_t)b * a.bt_stride;
   const int shift = a.page_shift;
   const int sub_mask = (1 << shift) - 1;
-  if (balanced) load_first_ids(b, p_begin);
+  if (!ids_loaded) load_first_ids(b, p_begin);
   if (it.b < 0) return;                           // uniform: no work item
-  if (p_begin >= p_end && !single) return;        // uniform; never merged
-  const int n_split = p_end > p_begin ? p_end - p_begin : 0;
-  const int n_pages = active ? n_split : 0;
   // A sequence with at most one split is finished here; otherwise this
   // workgroup leaves a partial for the merge kernel.
   const bool direct = it.n_valid <= 1;
+  // Partial item of the kv head of row slot r: [slots, Hkv] items of rows rows.
+  auto item_of = [&](int nb, int r) {
+    return ((size_t)(it.slot0 + split) * a.hkv + kvh + row_head(nb, r)) * a.rows;
+  };
+  if (p_begin >= p_end && !single) {
+    // A fixed-plan split past the sequence's pages (the balanced plan has none):
+    // the merge reads every split of a sequence without its length, so the
+    // split's rows say "no keys" (l = 0), or, when the sequence fitted one
+    // split and is already in the output, "done" (l = -1).
+    if (active && g16 == 0) {
+      const float mark = it.n_valid == 1 ? -1.f : 0.f;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        if (slot_real(nb, l16)) {
+          const size_t pitem = item_of(nb, l16) + row_in_head(nb, l16);
+          a.part_ml[pitem * 2 + 0] = -INFINITY;
+          a.part_ml[pitem * 2 + 1] = mark;
+        }
+      }
+    }
+    return;  // uniform
+  }
+  const int n_split = p_end - p_begin;
+  const int n_pages = active ? n_split : 0;
 
   // Second: Q fragments, the rest of the split's page ids and the first D
   // pages, all in flight at once (Q and ids first, so waiting for them leaves
@@ -910,10 +990,6 @@ void sqa_partial_kernel(PartialArgs a) {
   constexpr int kStageRow = HD + 4;  // floats per staged row; the pad spreads rows over banks
   constexpr int CPR = HD / 4;        // 4-value chunks per row
   float* stage = sm_stage + wave * 16 * kStageRow;
-  // Partial item of the kv head of row slot r: [slots, Hkv] items of rows rows.
-  auto item_of = [&](int nb, int r) {
-    return ((size_t)(it.slot0 + split) * a.hkv + kvh + row_head(nb, r)) * a.rows;
-  };
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     if (row_in_head(nb, 0) >= a.rows) break;  // uniform
@@ -944,6 +1020,13 @@ void sqa_partial_kernel(PartialArgs a) {
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     if (direct) {
+      // A fixed plan with several splits merges every split of the sequence:
+      // l = -1 tells the merge kernel this row is already in the output.
+      if (!single && !balanced && g16 == 0 && slot_real(nb, l16)) {
+        const size_t pitem = item_of(nb, l16) + row_in_head(nb, l16);
+        a.part_ml[pitem * 2 + 0] = -INFINITY;
+        a.part_ml[pitem * 2 + 1] = -1.f;
+      }
 #pragma unroll
       for (int i = 0; i < CPR / 4; ++i) {
         const int e = i * 64 + lane;
@@ -1008,40 +1091,53 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   const int kvh = h / a.group;
   const int r = qi * a.group + (h - kvh * a.group);
 
+  // Where the row's splits are. Fixed plan: all num_splits slots of the
+  // sequence, no length needed (splits past its pages hold l = 0, and l = -1
+  // in split 0 says the partial kernel already wrote the row). Balanced plan:
+  // the (first slot, count) table the partial kernel wrote; when every
+  // sequence was expected to span spec_pages pages, the uniform layout is
+  // assumed while the table is read, and the row is merged again from the
+  // table if the two differ.
+  const bool balanced = is_balanced(a.pages_per_split);
+  const bool expect = balanced && a.spec_pages > 0;
+  const size_t stride = (size_t)a.hkv * a.rows;  // items between consecutive splits of this row
+  const size_t row_item = (size_t)kvh * a.rows + r;
   int n_valid, slot0;
-  if (is_balanced(a.pages_per_split)) {
-    const SeqSplits ss = a.seq_splits[b];
-    n_valid = ss.count;
-    slot0 = ss.first;
+  SeqSplits table = {0, 0};
+  if (expect) {
+    n_valid = a.spec_splits;
+    slot0 = b * n_valid;
+  } else if (balanced) {
+    table = a.seq_splits[b];
+    n_valid = table.count;
+    slot0 = table.first;
   } else {
-    const int len = max(a.seq_lens[b], 0);
-    const int pages = min((len + kPageSize - 1) / kPageSize, a.max_pages);
-    n_valid = min((pages + a.pages_per_split - 1) / a.pages_per_split, a.num_splits);
+    n_valid = a.num_splits;
     slot0 = b * a.num_splits;
   }
-  // A sequence with one split was written by the partial kernel.
-  const bool skip = !live || n_valid == 1;
-  if (skip) n_valid = 0;
-
-  const size_t stride = (size_t)a.hkv * a.rows;  // items between consecutive splits of this row
-  const size_t first = ((size_t)slot0 * a.hkv + kvh) * a.rows + r;
-  const float* ml = a.part_ml + first * 2;
-  const float* po = a.part_o + first * HD + 4 * c;
+  if (!live) n_valid = 0;
 
   float mt = -INFINITY, den = 0.f;
   f4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = g; s0 < n_valid; s0 += U * SG) {
-    f4 o[U];
-    float m[U], l[U];
+  f4 o[U];
+  float m[U], l[U];
+  // One round: splits sb + u * SG (u < U) of the slots [s0, s0 + nv). Loads are
+  // unconditional, from an in-bounds slot (past the last split: split 0 of the
+  // row again, weight 0), so rounds need no branch around their loads.
+  auto load_round = [&](int s0, int nv, int sb) {
+    const float* ml = a.part_ml + ((size_t)s0 * stride + row_item) * 2;
+    const float* po = a.part_o + ((size_t)s0 * stride + row_item) * HD + 4 * c;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      // Loads stay unconditional (past the last split: split s0 again, weight 0).
-      const int s = s0 + u * SG;
-      const size_t it = (size_t)(s < n_valid ? s : s0) * stride;
+      const int sp = sb + u * SG;
+      const size_t it = (size_t)(sp < nv ? sp : 0) * stride;
       o[u] = *(const f4*)(po + it * HD);
       m[u] = ml[it * 2];
-      l[u] = s < n_valid ? ml[it * 2 + 1] : 0.f;
+      l[u] = ml[it * 2 + 1];
+      if (sp >= nv) l[u] = 0.f;
     }
+  };
+  auto add_round = [&]() {
     float cm = -INFINITY;
 #pragma unroll
     for (int u = 0; u < U; ++u) cm = l[u] > 0.f ? fmaxf(cm, m[u]) : cm;
@@ -1052,13 +1148,45 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
       acc *= sc;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const float w = l[u] > 0.f ? fast_exp2(m[u] - nm) : 0.f;
+        // Splits without keys (l <= 0) never touch the sums: their partial sums
+        // were never written and may hold anything.
+        const bool use = l[u] > 0.f;
+        const float w = use ? fast_exp2(m[u] - nm) : 0.f;
         den += w * l[u];
-        acc += w * o[u];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = use ? fmaf(w, o[u][i], acc[i]) : acc[i];
       }
       mt = nm;
     }
+  };
+  // The first round is issued before anything else is waited for (the
+  // expected layout's table read rides along with it); later rounds, rare, loop.
+  auto merge_splits = [&](int s0, int nv) {
+    mt = -INFINITY;
+    den = 0.f;
+    acc = f4{0.f, 0.f, 0.f, 0.f};
+    load_round(s0, nv, g);
+    if (expect) table = a.seq_splits[b];
+    const float first_l = l[0];  // split g (split 0 for group 0)
+    add_round();
+    for (int sb = g + U * SG; sb < nv; sb += U * SG) {
+      load_round(s0, nv, sb);
+      add_round();
+    }
+    return first_l;
+  };
+  float first_l = merge_splits(slot0, n_valid);
+  if (expect && live && (table.first != slot0 || table.count != n_valid)) {
+    n_valid = table.count;
+    slot0 = table.first;
+    first_l = merge_splits(slot0, n_valid);
   }
+  // A sequence with one split was written by the partial kernel: the balanced
+  // plan says so by its count, a fixed plan by l = -1 in split 0, which group 0
+  // (the one that stores) reads first. A sequence with no splits (no keys at
+  // all) is written here as 0.
+  const bool done = balanced ? n_valid == 1 : (g == 0 && first_l < 0.f);
+  const bool skip = !live || done;
 
   // Combine the SG groups of the row.
   auto combine = [&](float mo, float dn, f4 ao) {
@@ -1082,7 +1210,7 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
     static_assert(RPW == 1, "LDS combine serves one row per workgroup");
     __shared__ f4 sm_acc[SG][CH];
     __shared__ float sm_m[SG], sm_d[SG];
-    if (skip) return;  // uniform over the workgroup (one row)
+    if (!live || (balanced && n_valid == 1)) return;  // uniform over the workgroup (one row)
     sm_acc[g][c] = acc;
     if (c == 0) {
       sm_m[g] = mt;

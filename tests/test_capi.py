@@ -56,7 +56,9 @@ def test_workspace_bytes(lib):
     # plus one (first slot, count) pair of int32 per sequence.
     assert lib.sqa_workspace_bytes(16, 8, 32, 8, 128, 272, 0) == 272 * 8 * 32 * 130 * 4 + 16 * 8
     assert lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 1, 0) == 1 * 8 * 8 * 130 * 4 + 2 * 8
-    assert lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 3, -1) == 0
+    # -P: the balanced plan expecting P pages per sequence; the same workspace.
+    assert lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 3, -7) == \
+        lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 3, 0) == 3 * 8 * 8 * 130 * 4 + 2 * 8
     # Other head dims: head_dim + 2 floats per item.
     assert lib.sqa_workspace_bytes(1, 2, 32, 8, 64, 3, 4) == 1 * 8 * 3 * 8 * 66 * 4
     assert lib.sqa_workspace_bytes(1, 2, 32, 8, 256, 3, 4) == 1 * 8 * 3 * 8 * 258 * 4
@@ -122,7 +124,10 @@ def _call(lib, **kw):
     (dict(q_len=32), SQA_ERR_UNSUPPORTED, "exceeds"),
     (dict(splits=0), SQA_ERR_INVALID, "positive"),
     (dict(pps=2049), SQA_ERR_INVALID, "exceeds"),
-    (dict(pps=-1), SQA_ERR_INVALID, "non-negative"),
+    # -P: balanced plan expecting P pages per sequence; P beyond the block-table row
+    # (max_pages 2 x 16-token pages) is refused.
+    (dict(pps=-3, batch=2, splits=3, ws=16, ws_bytes=1 << 40), SQA_ERR_INVALID, "expects 3 pages"),
+    (dict(pps=-1, batch=1, splits=1, ws=16, ws_bytes=1 << 40), SQA_ERR_INVALID, "num_splits >="),
     # Balanced plan: at most 256 sequences, at least one spare slot per sequence
     # plus enough slots to keep every split within 2048 pages.
     (dict(pps=0, batch=257, splits=600, ws=16, ws_bytes=1 << 40), SQA_ERR_INVALID, "batch <= 256"),

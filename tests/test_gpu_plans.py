@@ -1,0 +1,107 @@
+"""Split plans on the GPU: the balanced plan's expected page count and the fixed
+plan's merge markers.
+
+* ``pages_per_split = -P`` (``sqa_plan_splits`` with a known ``max_seq_len``):
+  the kernels assume every sequence spans P pages while the lengths are read
+  and fall back to the plan the lengths give when they do not. Uniform, ragged
+  and shorter-than-promised batches must give the same bits as the plain
+  balanced plan (``pages_per_split = 0``), and parity with the oracle.
+* Fixed plans: the merge reads every split of a sequence without its length;
+  splits past a sequence's pages write "no keys" and a sequence finished by the
+  partial kernel writes "done". A workspace full of NaN (and of the previous
+  call's partials) must not leak into the output.
+"""
+
+import sys
+
+import pytest
+import torch
+
+from oracle import attention_c64
+from small_q_attention_amd import _lib, inputs
+from tests._helpers import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    sys.__stderr__.write(f"\n[gpu-test] {request.node.nodeid}\n")
+    sys.__stderr__.flush()
+
+
+def _gpu(case):
+    return tuple(t.cuda() for t in inputs.make_inputs(case))
+
+
+def _oracle(tensors, page=16, hkv=8):
+    return attention_c64(*(t.cpu() for t in tensors), page, hkv)
+
+
+def _run(tensors, ns, pps, fill=float("nan"), ws=None):
+    q, k, v, bt, sl = tensors
+    nbytes = _lib.workspace_bytes(q.shape[0], q.shape[1], q.shape[2], k.shape[2], q.shape[3],
+                                  ns, pps)
+    if ws is None:
+        ws = torch.full((max(nbytes, 4) // 4,), fill, dtype=torch.float32, device="cuda")
+    out = torch.full_like(q, float("nan"))
+    _lib.launch(q, k, v, bt, sl, out, ws if nbytes else None, ns, pps,
+                torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return out, ws
+
+
+@pytest.mark.parametrize("q_len", [2, 8, 16])
+def test_expected_pages_give_the_plain_balanced_bits(q_len):
+    promise = 3000
+    batches = {
+        "uniform": [promise] * 5,
+        "ragged": [promise, promise - 1, 17, 0, promise, q_len],
+        "all_shorter": [2000] * 5,
+        "one_longer_page": [promise] * 4 + [promise + 16],
+    }
+    for label, lens in batches.items():
+        case = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=1200 + q_len)
+        q, k, v, bt, sl = _gpu(case)
+        # A block table wider than any sequence (as in serving), so the promise is
+        # not capped by the table: "all_shorter" expects more pages than any has,
+        # "one_longer_page" has one sequence a page past the promise.
+        wide = torch.zeros(len(lens), (promise + 15) // 16 + 2, dtype=torch.int32, device="cuda")
+        wide[:, :bt.shape[1]] = bt
+        tensors = (q, k, v, wide, sl)
+        ns, pps = _lib.plan_splits(0, len(lens), q_len, 32, 8, 128, promise, wide.shape[1], 0)
+        assert pps == -((promise + 15) // 16), label
+        spec, _ = _run(tensors, ns, pps)
+        plain, _ = _run(tensors, ns, 0)
+        assert torch.equal(spec, plain), label
+        assert_parity(spec, _oracle(tensors), label=f"{label} q{q_len}")
+
+
+def test_expected_pages_at_full_size():
+    """cfg2 (B4 q_len 4 KV 8192, uniform): the expected-page plan against the plain one."""
+    case = inputs.baseline_configs()["cfg2"]
+    tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
+    ns, pps = _lib.plan_splits(0, 4, 4, 32, 8, 128, 8192, tensors[3].shape[1], 0)
+    assert pps == -512
+    spec, _ = _run(tensors, ns, pps)
+    plain, _ = _run(tensors, ns, 0)
+    assert torch.equal(spec, plain)
+    assert torch.isfinite(spec.float()).all()
+
+
+@pytest.mark.parametrize("q_len", [4, 16])
+def test_fixed_plan_merge_markers(q_len):
+    """Empty sequences, one-split sequences (finished by the partial kernel) and
+    multi-split ones in one fixed plan, over a NaN workspace, then again over the
+    first call's leftovers with other lengths."""
+    runs = [[0, 5, 16, 17, 700, 4096 + 3], [4096 + 3, 0, 700, 17, 16, q_len]]
+    ws = None
+    for i, lens in enumerate(runs):
+        case = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=1300 + 10 * q_len + i)
+        tensors = _gpu(case)
+        bt = tensors[3]
+        ns, pps = _lib.plan_splits(0, len(lens), q_len, 32, 8, 128, max(lens), bt.shape[1], 256)
+        assert pps == 16 and ns > 1
+        out, ws = _run(tensors, ns, pps, ws=ws)
+        assert torch.isfinite(out.float()).all(), lens
+        assert_parity(out, _oracle(tensors), label=f"fixed q{q_len} run {i}")
