@@ -663,60 +663,46 @@ __device__ __forceinline__ int length_of(const int (&len)[kSeqPerLane], int b) {
   return __shfl(v, b & 63);
 }
 
-// One workgroup = one (sequence b, split) x WW waves; wave w serves the HPW kv
-// heads from (head_group * WW + w) * HPW with all of their rows (NB blocks of
-// 16; with HPW = 2 either one block, rows 0-7 of the first head and 8-15 of
-// the second, or one block per head); WPE = waves per SIMD the register
-// budget allows. All waves walk the
-// same pages in the same order, so the heads' 256-byte slices of each page are
-// requested together and HBM sees 1 KiB (4 heads) or 2 KiB (8 heads) runs; the
-// head groups of a page range are dispatch neighbours. Each wave keeps its own
-// softmax state and writes its own partials (or, with a single split, the
-// output). Every K/V byte is read by one wave only, so the loads are
-// non-temporal.
-template <int NB, int D, int WW, int WPE, int HD, typename E, typename KV, int HPW>
-__global__ __launch_bounds__(WW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
-void sqa_partial_kernel(PartialArgs a) {
-  constexpr int KK = Dims<HD>::KK, MB = Dims<HD>::MB;
+// The rows of a wave: row slot r (0..15) of 16-row block nb is row row(nb, r)
+// (= qi * group + g) of kv head head(nb, r), real() unless it is padding (past
+// the rows of a head, or a head past the last). One kv head per wave (HPW = 1):
+// blocks nb hold rows 16 nb + r. Two (HPW = 2, head dim 64): one shared block,
+// rows 0-7 of the first head in slots 0-7 and of the second in 8-15, or NB / 2
+// blocks per head.
+template <int NB, int HPW>
+struct WaveRows {
+  int kvh, rows, hkv;  // the wave's first kv head; rows per kv head; kv heads
+  static constexpr int kBlocksPerHead = NB >= 2 ? NB / HPW : 1;
+  __device__ __forceinline__ int head(int nb, int r) const {
+    return kvh + (HPW == 1 ? 0 : (NB == 1 ? r >> 3 : nb / kBlocksPerHead));
+  }
+  __device__ __forceinline__ int row(int nb, int r) const {
+    return HPW == 1 ? nb * 16 + r : (NB == 1 ? (r & 7) : (nb % kBlocksPerHead) * 16 + r);
+  }
+  __device__ __forceinline__ bool real(int nb, int r) const {
+    return head(nb, r) < hkv && row(nb, r) < rows;
+  }
+};
+
+// The work item of workgroup item `item` under either plan, with the ids of its
+// first D pages loaded (index clamped into the block-table row; ids past the
+// split are never used). Fixed plan: the page range follows from `item` alone,
+// so those ids are issued before the sequence length is read and both arrive
+// in one round trip. Balanced plan: all lengths, the plan's wave reductions,
+// then the ids; with an expected page count, the host's plan for it gives the
+// item at once and the ids go out with the lengths. The fields are the same in
+// every lane (readfirstlane): the item, and the buffer-resource addresses built
+// from it, stay in scalar registers.
+template <int D>
+__device__ __forceinline__ ItemRange work_item(const PartialArgs& a, int item, int (&first_id)[D]) {
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g16 = lane >> 4;
-  const int l16 = lane & 15;
-
-  // blockIdx.x = item * head_groups + head_group.
-  const int head_groups = (a.hkv + WW * HPW - 1) / (WW * HPW);
-  const int hgrp = blockIdx.x % head_groups;
-  const int item = blockIdx.x / head_groups;
-  const int kvh = (hgrp * WW + wave) * HPW;  // the wave's first kv head
-  // Waves past the last kv head (hkv not a multiple of WW * HPW) idle but stay
-  // for the barrier.
-  const bool active = kvh < a.hkv;
-  // Row slot r of block nb (r = 0..15) -> kv head kvh + row_head(nb, r) and
-  // row row_in_head(nb, r) of that head (row = qi * group + g).
-  constexpr int BPH = NB >= 2 ? NB / HPW : 1;  // blocks per head (HPW = 2, NB >= 2)
-  auto row_head = [](int nb, int r) { return HPW == 1 ? 0 : (NB == 1 ? r >> 3 : nb / BPH); };
-  auto row_in_head = [](int nb, int r) {
-    return HPW == 1 ? nb * 16 + r : (NB == 1 ? (r & 7) : (nb % BPH) * 16 + r);
-  };
-  auto slot_real = [&](int nb, int r) {
-    return kvh + row_head(nb, r) < a.hkv && row_in_head(nb, r) < a.rows;
-  };
-
-  // Start-up. First: the work item (fixed plan: the sequence length, with the
-  // ids of the split's first D pages loaded alongside; balanced plan: all
-  // seq_lens and the plan's wave reductions, then those ids).
-  const bool balanced = is_balanced(a.pages_per_split);
-  // Ids of the split's first D pages (index clamped into the block-table row;
-  // ids past the split are never used). A fixed plan's page range follows from
-  // blockIdx alone, so they are issued before the sequence length is read and
-  // both arrive in one round trip.
-  int first_id[D];
   auto load_first_ids = [&](int seq, int p0) {
     const int32_t* row = a.block_tables + (size_t)seq * a.bt_stride;
 #pragma unroll
     for (int j = 0; j < D; ++j)
       first_id[j] = row[min(max(p0 + j, 0), a.max_pages - 1) >> a.page_shift];
   };
+  const bool balanced = is_balanced(a.pages_per_split);
   ItemRange it;
   bool ids_loaded = !balanced;  // uniform
   if (!balanced) {
@@ -760,8 +746,6 @@ void sqa_partial_kernel(PartialArgs a) {
     }
     it.len = it.b >= 0 ? length_of(len, it.b) : 0;
   }
-  // The work item is the same for the whole workgroup; saying so keeps it (and
-  // the buffer-resource addresses built from it) in scalar registers.
   it.b = __builtin_amdgcn_readfirstlane(it.b);
   it.split = __builtin_amdgcn_readfirstlane(it.split);
   it.p_begin = __builtin_amdgcn_readfirstlane(it.p_begin);
@@ -769,6 +753,174 @@ void sqa_partial_kernel(PartialArgs a) {
   it.len = __builtin_amdgcn_readfirstlane(it.len);
   it.n_valid = __builtin_amdgcn_readfirstlane(it.n_valid);
   it.slot0 = __builtin_amdgcn_readfirstlane(it.slot0);
+  if (!ids_loaded) load_first_ids(max(it.b, 0), it.p_begin);
+  return it;
+}
+
+// Draft bits of a row of sequence b, draft row qi: bit j = the row sees draft
+// token j (the caller's mask, or the causal chain j <= qi); 0 for padding rows.
+// Both mask words are loaded unconditionally (without a mask: from seq_lens,
+// never used) and selected by bit masks, not by branches on loaded values, so
+// the compiler need not wait for them before later loads are issued.
+__device__ __forceinline__ unsigned long long draft_bits(const PartialArgs& a, int b, int qi,
+                                                         bool real) {
+  const bool has_mask = a.draft_mask != nullptr;
+  const uint32_t* mp = has_mask ? a.draft_mask + (size_t)(b * a.q_len + qi) * a.mask_words
+                                : (const uint32_t*)a.seq_lens;
+  const unsigned long long lo = mp[0];
+  const unsigned long long hi = mp[a.mask_words > 1 ? 1 : 0];
+  const unsigned long long causal = qi >= 63 ? ~0ull : (2ull << qi) - 1ull;
+  const unsigned long long use_mask = 0ull - (unsigned long long)(has_mask && real);
+  const unsigned long long use_hi = 0ull - (unsigned long long)(a.mask_words > 1);
+  const unsigned long long use_causal = 0ull - (unsigned long long)(!has_mask && real);
+  return ((lo | ((hi << 32) & use_hi)) & use_mask) | (causal & use_causal);
+}
+
+// Leaves one wave's results: normalised rows of the output (`direct`: the
+// sequence's pages fit one split) or the unnormalised partial sums and (max in
+// log2 units, sum) of each row at partial slot `slot`. Row slot r of block nb is
+// map.real(nb, r), kv head map.head(nb, r), row map.row(nb, r) of that head.
+// `mark_done` (a fixed plan with several splits, finished here) also writes
+// l = -1 at the slot, which tells the merge kernel the row is in the output.
+// The results leave through LDS one 16-row block at a time: every lane writes
+// its dims (HD/4) (l/16) + (HD/16) rr + mb of row l % 16 row-major into the
+// wave's `stage` (16 rows of HD + 4 floats; the pad spreads rows over banks),
+// then reads back 4 contiguous values of a row, so a store instruction writes
+// whole rows (1 KiB runs of partial sums) instead of 64 scattered 16-byte
+// pieces, which ran at a quarter of the store rate (the epilogue of a 64-row
+// wave took 5 us).
+template <int NB, int HD, typename E, typename Map>
+__device__ __forceinline__ void write_results(const PartialArgs& a, WaveState<NB, HD>& st,
+                                              float* stage, const Map& map, bool direct,
+                                              bool mark_done, int b, size_t slot) {
+  constexpr int MB = Dims<HD>::MB;
+  constexpr int kStageRow = HD + 4;  // floats per staged row
+  constexpr int CPR = HD / 4;        // 4-value chunks per row
+  const int lane = threadIdx.x & 63;
+  const int g16 = lane >> 4, l16 = lane & 15;
+  auto item_of = [&](int nb, int r) { return (slot * a.hkv + map.head(nb, r)) * a.rows; };
+  // Row sums over the four lane groups.
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) st.l[nb] = xor_sum(st.l[nb]);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    if (map.row(nb, 0) >= a.rows) break;  // uniform
+    const float inv = st.l[nb] > 0.f ? a.out_scale / st.l[nb] : 0.f;
+    const float sc = direct ? inv : 1.f;
+    if (map.real(nb, l16)) {
+      float* dst = stage + l16 * kStageRow + (HD / 4) * g16;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+#pragma unroll
+        for (int h = 0; h < MB / 4; ++h) {
+          f4 o;
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) o[mb] = st.acc[4 * h + mb][nb][rr] * sc;
+          *(f4*)(dst + MB * rr + 4 * h) = o;
+        }
+      }
+    }
+    // The staging rows are this wave's own: LDS keeps a wave's accesses in
+    // order, the fences keep the compiler from moving them. All reads are
+    // issued before the first store, so the block pays one LDS latency.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    f4 v[CPR / 4];
+#pragma unroll
+    for (int i = 0; i < CPR / 4; ++i) {
+      const int e = i * 64 + lane;  // row e / CPR (< 16), chunk e % CPR
+      v[i] = *(const f4*)(stage + (e / CPR) * kStageRow + 4 * (e % CPR));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (direct) {
+      if (mark_done && g16 == 0 && map.real(nb, l16)) {
+        const size_t pitem = item_of(nb, l16) + map.row(nb, l16);
+        a.part_ml[pitem * 2 + 0] = -INFINITY;
+        a.part_ml[pitem * 2 + 1] = -1.f;
+      }
+#pragma unroll
+      for (int i = 0; i < CPR / 4; ++i) {
+        const int e = i * 64 + lane;
+        const int rs = e / CPR;
+        if (map.real(nb, rs)) {
+          const int r = map.row(nb, rs);
+          const int qi = r / a.group;
+          const int gg = r - qi * a.group;
+          _Float16* op = a.out + ((size_t)(b * a.q_len + qi) * a.hq +
+                                  map.head(nb, rs) * a.group + gg) * HD + 4 * (e % CPR);
+          const float o[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
+          *(u2*)op = E::pack4(o);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < CPR / 4; ++i) {
+        const int e = i * 64 + lane;
+        const int rs = e / CPR;
+        if (map.real(nb, rs))
+          *(f4*)(a.part_o + (item_of(nb, rs) + map.row(nb, rs)) * HD + 4 * (e % CPR)) = v[i];
+      }
+      if (g16 == 0 && map.real(nb, l16)) {
+        const size_t pitem = item_of(nb, l16) + map.row(nb, l16);
+        a.part_ml[pitem * 2 + 0] = st.m[nb];
+        a.part_ml[pitem * 2 + 1] = st.l[nb];
+      }
+    }
+  }
+}
+
+// A fixed-plan split past its sequence's pages (the balanced plan has none):
+// the merge reads every split of a sequence without its length, so the split's
+// rows say "no keys" (l = 0), or, when the sequence fitted one split and is
+// already in the output, "done" (l = -1).
+template <int NB, typename Map>
+__device__ __forceinline__ void write_empty_split(const PartialArgs& a, const Map& map,
+                                                  size_t slot, float mark) {
+  const int lane = threadIdx.x & 63;
+  if ((lane >> 4) != 0) return;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    if (map.real(nb, lane)) {
+      const size_t pitem = (slot * a.hkv + map.head(nb, lane)) * a.rows + map.row(nb, lane);
+      a.part_ml[pitem * 2 + 0] = -INFINITY;
+      a.part_ml[pitem * 2 + 1] = mark;
+    }
+  }
+}
+
+// One workgroup = one (sequence b, split) x WW waves; wave w serves the HPW kv
+// heads from (head_group * WW + w) * HPW with all of their rows (NB blocks of
+// 16; with HPW = 2 either one block, rows 0-7 of the first head and 8-15 of
+// the second, or one block per head); WPE = waves per SIMD the register
+// budget allows. All waves walk the
+// same pages in the same order, so the heads' 256-byte slices of each page are
+// requested together and HBM sees 1 KiB (4 heads) or 2 KiB (8 heads) runs; the
+// head groups of a page range are dispatch neighbours. Each wave keeps its own
+// softmax state and writes its own partials (or, with a single split, the
+// output). Every K/V byte is read by one wave only, so the loads are
+// non-temporal.
+template <int NB, int D, int WW, int WPE, int HD, typename E, typename KV, int HPW>
+__global__ __launch_bounds__(WW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
+void sqa_partial_kernel(PartialArgs a) {
+  constexpr int KK = Dims<HD>::KK, MB = Dims<HD>::MB;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g16 = lane >> 4;
+  const int l16 = lane & 15;
+
+  // blockIdx.x = item * head_groups + head_group.
+  const int head_groups = (a.hkv + WW * HPW - 1) / (WW * HPW);
+  const int hgrp = blockIdx.x % head_groups;
+  const int item = blockIdx.x / head_groups;
+  const int kvh = (hgrp * WW + wave) * HPW;  // the wave's first kv head
+  // Waves past the last kv head (hkv not a multiple of WW * HPW) idle but stay
+  // for the barrier.
+  const bool active = kvh < a.hkv;
+  const WaveRows<NB, HPW> map{kvh, a.rows, a.hkv};
+
+  // Start-up. First: the work item and the ids of its first D pages.
+  const bool balanced = is_balanced(a.pages_per_split);
+  int first_id[D];
+  const ItemRange it = work_item<D>(a, item, first_id);
   const bool single = !balanced && a.num_splits == 1;  // no merge kernel follows
   const int b = max(it.b, 0);
   const int split = it.split;
@@ -778,31 +930,13 @@ void sqa_partial_kernel(PartialArgs a) {
   const int32_t* bt_row = a.block_tables + (size_t)b * a.bt_stride;
   const int shift = a.page_shift;
   const int sub_mask = (1 << shift) - 1;
-  if (!ids_loaded) load_first_ids(b, p_begin);
-  if (it.b < 0) return;                           // uniform: no work item
+  if (it.b < 0) return;  // uniform: no work item
   // A sequence with at most one split is finished here; otherwise this
   // workgroup leaves a partial for the merge kernel.
   const bool direct = it.n_valid <= 1;
-  // Partial item of the kv head of row slot r: [slots, Hkv] items of rows rows.
-  auto item_of = [&](int nb, int r) {
-    return ((size_t)(it.slot0 + split) * a.hkv + kvh + row_head(nb, r)) * a.rows;
-  };
+  const size_t slot = (size_t)it.slot0 + split;
   if (p_begin >= p_end && !single) {
-    // A fixed-plan split past the sequence's pages (the balanced plan has none):
-    // the merge reads every split of a sequence without its length, so the
-    // split's rows say "no keys" (l = 0), or, when the sequence fitted one
-    // split and is already in the output, "done" (l = -1).
-    if (active && g16 == 0) {
-      const float mark = it.n_valid == 1 ? -1.f : 0.f;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        if (slot_real(nb, l16)) {
-          const size_t pitem = item_of(nb, l16) + row_in_head(nb, l16);
-          a.part_ml[pitem * 2 + 0] = -INFINITY;
-          a.part_ml[pitem * 2 + 1] = mark;
-        }
-      }
-    }
+    if (active) write_empty_split<NB>(a, map, slot, it.n_valid == 1 ? -1.f : 0.f);
     return;  // uniform
   }
   const int n_split = p_end - p_begin;
@@ -818,32 +952,18 @@ void sqa_partial_kernel(PartialArgs a) {
     // Loads are unconditional from an in-bounds address (padding rows and idle
     // waves read row 0 of kv head 0) and the value is selected afterwards, so
     // no lane-divergent branch splits the load stream.
-    const int r = row_in_head(nb, l16);
-    const bool real = slot_real(nb, l16);
+    const int r = map.row(nb, l16);
+    const bool real = map.real(nb, l16);
     const int qi = real ? r / a.group : 0;
     const int gg = real ? r - qi * a.group : 0;
-    const int hh = real ? (kvh + row_head(nb, l16)) * a.group + gg : 0;
+    const int hh = real ? map.head(nb, l16) * a.group + gg : 0;
     const _Float16* qp = a.q + ((size_t)(b * a.q_len + qi) * a.hq + hh) * HD;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const u4 x = *(const u4*)(qp + KV::q_dims(kk, g16));
       qreg[nb][kk] = real ? x : u4{0u, 0u, 0u, 0u};
     }
-    // Draft bits of the row: bit j = sees draft token j (the caller's mask, or
-    // the causal chain j <= qi). Both mask words are loaded unconditionally
-    // (without a mask: from seq_lens, never used), so no branch makes the
-    // compiler wait for them before the page loads below are issued.
-    const bool has_mask = a.draft_mask != nullptr;
-    const uint32_t* mp = has_mask ? a.draft_mask + (size_t)(b * a.q_len + qi) * a.mask_words
-                                  : (const uint32_t*)a.seq_lens;
-    const unsigned long long lo = mp[0];
-    const unsigned long long hi = mp[a.mask_words > 1 ? 1 : 0];
-    const unsigned long long causal = qi >= 63 ? ~0ull : (2ull << qi) - 1ull;
-    // Selections by bit masks, not by branches on loaded values.
-    const unsigned long long use_mask = 0ull - (unsigned long long)(has_mask && real);
-    const unsigned long long use_hi = 0ull - (unsigned long long)(a.mask_words > 1);
-    const unsigned long long use_causal = 0ull - (unsigned long long)(!has_mask && real);
-    dbits[nb] = ((lo | ((hi << 32) & use_hi)) & use_mask) | (causal & use_causal);
+    dbits[nb] = draft_bits(a, b, qi, real);
   }
   static_assert(2 * D + 1 <= kIdPad, "page-id table padding must cover the ring's look-ahead");
   constexpr int kIdSlots = (kMaxSplitPages + kIdPad + WW * 64 - 1) / (WW * 64);
@@ -976,87 +1096,240 @@ void sqa_partial_kernel(PartialArgs a) {
     }
   }
   if (!active) return;
+  write_results<NB, HD, E>(a, st, sm_stage + wave * 16 * (HD + 4), map, direct,
+                           !single && !balanced, b, slot);
+}
 
-  // Row sums over the four lane groups.
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) st.l[nb] = xor_sum(st.l[nb]);
+// The rows of one wave of the 8-wave kernel: rows base .. base + 31 of kv head
+// kvh (two 16-row blocks).
+struct HalfRows {
+  int kvh, rows, hkv, base;
+  __device__ __forceinline__ int head(int, int) const { return kvh; }
+  __device__ __forceinline__ int row(int nb, int r) const { return base + 16 * nb + r; }
+  __device__ __forceinline__ bool real(int nb, int r) const {
+    return kvh < hkv && row(nb, r) < rows;
+  }
+};
 
-  // Results leave through LDS one 16-row block at a time: every lane writes
-  // its dims (HD/4) (l/16) + (HD/16) rr + mb of row l % 16 row-major, then
-  // reads back 4 contiguous values of a row, so a store instruction writes
-  // whole rows (1 KiB runs of partial sums) instead of 64 scattered 16-byte
-  // pieces, which ran at a quarter of the store rate (the epilogue of a
-  // 64-row wave took 5 us).
-  constexpr int kStageRow = HD + 4;  // floats per staged row; the pad spreads rows over banks
-  constexpr int CPR = HD / 4;        // 4-value chunks per row
-  float* stage = sm_stage + wave * 16 * kStageRow;
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// One 16-byte non-temporal buffer load per lane straight into LDS (gfx950
+// buffer_load_dwordx4 ... lds): lane l's 16 bytes land at LDS byte address
+// lds + 16 l. Written as inline asm on purpose: the compiler's own wait-count
+// pass, seeing such a load, waits for all vector memory (vmcnt(0)) before every
+// later LDS read that might alias it, which would drain a ring of these loads at
+// each step; the callers place their vmcnt waits themselves and issue no other
+// vector-memory loads meanwhile. m0 (the LDS base of the load) is saved and
+// restored around it.
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, unsigned voffset,
+                                            unsigned lds) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %[saved], m0\n\t"
+      "s_mov_b32 m0, %[lds]\n\t"
+      "buffer_load_dwordx4 %[off], %[rsrc], 0 offen nt lds\n\t"
+      "s_mov_b32 m0, %[saved]"
+      : [saved] "=&s"(saved)
+      : [lds] "s"(lds), [off] "v"(voffset), [rsrc] "s"(rsrc)
+      : "memory");
+}
+
+// Byte offset of 16-byte chunk c (0..15) of token t (0..15) in a head's 4 KiB
+// page slice in LDS: chunk c of token t sits at position 16 t + (c ^ t), so the
+// 16 tokens an MFMA operand read takes at one chunk fall in 16 bank groups.
+__device__ __forceinline__ unsigned swz(int t, int c) { return (unsigned)(16 * t + (c ^ t)) * 16u; }
+
+// 33..64 query rows per kv head (q_len 16 at GQA 4) at head dim 128 over 16-bit
+// caches. Eight waves per workgroup: two per kv head, each with 32 of the head's
+// rows in two 16-row blocks (the 32-row math), so no wave holds the 128
+// accumulator registers of 64 rows, and two waves share each SIMD, one's MFMAs
+// under the other's softmax. The two waves of a head read each page once
+// between them: the workgroup's K and V of 4 heads (32 KiB a page) arrive in a
+// ring of D LDS slots by direct buffer loads (buffer_load_dwordx4 ... lds; four
+// per thread and page, 1 KiB of a head's page slice each, chunks swizzled as
+// swz()), so the bytes in flight take no registers. Per page: wait for this
+// thread's loads of the page (manual vmcnt: nothing else in the loop touches
+// vector memory), a barrier (the page is in LDS), read the wave's K and V into
+// registers, a second barrier (every wave has read the slot), refill the slot
+// with the page D ahead, then the math: a slot is refilled before its page's
+// math, so D pages stay in flight. Pages past the split load through a
+// zero-length resource (zeros, no memory traffic), as in sqa_partial_kernel.
+template <int D, typename E>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+void sqa_partial_lds_kernel(PartialArgs a) {
+  constexpr int HD = 128, NB = 2, KK = Dims<HD>::KK, MB = Dims<HD>::MB;
+  using KV = KvNative<HD>;
+  constexpr int kHeadSlice = 16 * HD * 2;        // one head's K (or V) of a page: 4 KiB
+  constexpr int kSlot = 2 * 4 * kHeadSlice;      // K and V of 4 heads: 32 KiB
+  constexpr int kThreads = 512;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g16 = lane >> 4;
+  const int l16 = lane & 15;
+
+  // blockIdx.x = item * head_groups + head_group; wave = half * 4 + head slot.
+  const int head_groups = (a.hkv + 3) / 4;
+  const int hgrp = blockIdx.x % head_groups;
+  const int item = blockIdx.x / head_groups;
+  const int hs = wave & 3;
+  const int kvh = hgrp * 4 + hs;
+  const HalfRows map{kvh, a.rows, a.hkv, 32 * (wave >> 2)};
+  // Waves without rows (a head past the last, or no rows past 32) still load
+  // and meet the barriers; they skip the math.
+  const bool active = kvh < a.hkv && map.base < a.rows;
+
+  const bool balanced = is_balanced(a.pages_per_split);
+  int first_id[D];
+  const ItemRange it = work_item<D>(a, item, first_id);
+  const bool single = !balanced && a.num_splits == 1;
+  const int b = max(it.b, 0);
+  const int len = it.len;
+  const int p_begin = it.p_begin;
+  const int p_end = it.p_end;
+  const int32_t* bt_row = a.block_tables + (size_t)b * a.bt_stride;
+  const int shift = a.page_shift;
+  const int sub_mask = (1 << shift) - 1;
+  if (it.b < 0) return;  // uniform
+  const bool direct = it.n_valid <= 1;
+  const size_t slot = (size_t)it.slot0 + it.split;
+  if (p_begin >= p_end && !single) {
+    write_empty_split<NB>(a, map, slot, it.n_valid == 1 ? -1.f : 0.f);
+    return;  // uniform
+  }
+  const int n_split = p_end > p_begin ? p_end - p_begin : 0;
+
+  // Q fragments (kept in registers), draft bits, then the split's page ids.
+  u4 qreg[NB][KK];
+  unsigned long long dbits[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    if (row_in_head(nb, 0) >= a.rows) break;  // uniform
-    const float inv = st.l[nb] > 0.f ? a.out_scale / st.l[nb] : 0.f;
-    const float sc = direct ? inv : 1.f;
-    if (slot_real(nb, l16)) {
-      float* dst = stage + l16 * kStageRow + (HD / 4) * g16;
+    const int r = map.row(nb, l16);
+    const bool real = map.real(nb, l16);
+    const int qi = real ? r / a.group : 0;
+    const int gg = real ? r - qi * a.group : 0;
+    const int hh = real ? kvh * a.group + gg : 0;
+    const _Float16* qp = a.q + ((size_t)(b * a.q_len + qi) * a.hq + hh) * HD;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-#pragma unroll
-        for (int h = 0; h < MB / 4; ++h) {
-          f4 o;
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) o[mb] = st.acc[4 * h + mb][nb][rr] * sc;
-          *(f4*)(dst + MB * rr + 4 * h) = o;
-        }
-      }
+    for (int kk = 0; kk < KK; ++kk) {
+      const u4 x = *(const u4*)(qp + KV::q_dims(kk, g16));
+      qreg[nb][kk] = real ? x : u4{0u, 0u, 0u, 0u};
     }
-    // The staging rows are this wave's own: LDS keeps a wave's accesses in
-    // order, the fences keep the compiler from moving them. All reads are
-    // issued before the first store, so the block pays one LDS latency.
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    f4 v[CPR / 4];
+    dbits[nb] = draft_bits(a, b, qi, real);
+  }
+  static_assert(D + 1 <= kIdPad, "page-id table padding must cover the ring's look-ahead");
+  constexpr int kIdSlots = (kMaxSplitPages + kIdPad + kThreads - 1) / kThreads;
+  int idreg[kIdSlots];
+  const int last_id = n_split > 0 ? n_split - 1 : 0;
 #pragma unroll
-    for (int i = 0; i < CPR / 4; ++i) {
-      const int e = i * 64 + lane;  // row e / CPR (< 16), chunk e % CPR
-      v[i] = *(const f4*)(stage + (e / CPR) * kStageRow + 4 * (e % CPR));
-    }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    if (direct) {
-      // A fixed plan with several splits merges every split of the sequence:
-      // l = -1 tells the merge kernel this row is already in the output.
-      if (!single && !balanced && g16 == 0 && slot_real(nb, l16)) {
-        const size_t pitem = item_of(nb, l16) + row_in_head(nb, l16);
-        a.part_ml[pitem * 2 + 0] = -INFINITY;
-        a.part_ml[pitem * 2 + 1] = -1.f;
-      }
+  for (int k = 0; k < kIdSlots; ++k) {
+    const int i = threadIdx.x + k * kThreads;
+    const int x = bt_row[(p_begin + min(i, last_id)) >> shift];
+    idreg[k] = i < n_split ? x : -1;
+  }
+
+  // The ring and, after the loop, the waves' output staging.
+  __shared__ __attribute__((aligned(16))) char sm_ring[D * kSlot];
+  __shared__ int sm_ids[kIdSlots * kThreads];
+  // Load i (0..3) of a thread fills 1 KiB chunk ci = 8 i + wave of a slot: K
+  // (ci < 16) or V of head slot (ci / 4) % 4, tokens 4 (ci % 4) .. + 3; lane l
+  // holds position 64 (ci % 4) + l of the head's slice, token t = position / 16,
+  // chunk (position % 16) ^ t.
+  const unsigned tok_bytes = a.token_stride;
+  unsigned voff[4];
 #pragma unroll
-      for (int i = 0; i < CPR / 4; ++i) {
-        const int e = i * 64 + lane;
-        const int slot = e / CPR;
-        if (slot_real(nb, slot)) {
-          const int r = row_in_head(nb, slot);
-          const int qi = r / a.group;
-          const int gg = r - qi * a.group;
-          _Float16* op = a.out + ((size_t)(b * a.q_len + qi) * a.hq +
-                                  (kvh + row_head(nb, slot)) * a.group + gg) * HD +
-                         4 * (e % CPR);
-          const float o[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
-          *(u2*)op = E::pack4(o);
+  for (int i = 0; i < 4; ++i) {
+    const int ci = 8 * i + wave;
+    const int pos = 64 * (ci & 3) + lane;
+    const int t = pos >> 4, c = (pos & 15) ^ t;
+    voff[i] = t * tok_bytes + (hgrp * 4 + ((ci >> 2) & 3)) * a.head_stride + 16 * c;
+  }
+  const size_t sub_bytes = (size_t)kPageSize * tok_bytes;
+  auto issue_page = [&](int pid, int p, int j) {
+    const size_t off =
+        pid >= 0 ? (size_t)pid * (size_t)a.page_stride + (size_t)(p & sub_mask) * sub_bytes : 0;
+    const int nrec = pid >= 0 ? (int)a.page_extent : 0;
+    const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const char*)a.k + off), (short)0, nrec, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const char*)a.v + off), (short)0, nrec, kBufferFlags);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      load_to_lds(i < 2 ? kr : vr, voff[i],
+                  (unsigned)(size_t)(sm_ring + j * kSlot + (8 * i + wave) * 1024));
+  };
+#pragma unroll
+  for (int j = 0; j < D; ++j)
+    issue_page(j < n_split ? clamp_page(first_id[j], a.num_pages) : -1, p_begin + j, j);
+#pragma unroll
+  for (int k = 0; k < kIdSlots; ++k) {
+    const int i = threadIdx.x + k * kThreads;
+    sm_ids[i] = idreg[k] >= 0 ? clamp_page(idreg[k], a.num_pages) : -1;
+  }
+  const int mask_from = len - a.q_len;
+
+  WaveState<NB, HD> st;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    st.m[nb] = -INFINITY;
+    st.l[nb] = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) st.acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();  // sm_ids written
+
+  int next_pid = sm_ids[D];
+  for (int i = 0; i < n_split; i += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int ii = i + j;
+      if (ii < n_split) {  // uniform over the workgroup
+        wait_vmcnt<4 * (D - 1)>();  // this thread's loads of page ii
+        __syncthreads();             // everyone's: page ii is in slot j
+        const char* ks = sm_ring + j * kSlot + hs * kHeadSlice;
+        const char* vs = ks + 4 * kHeadSlice;
+        PageK<HD, 1> kf;
+        PageV<HD, 1> pv;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) kf.k[0][kk] = *(const u4*)(ks + swz(l16, 4 * kk + g16));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const u4 x = *(const u4*)(vs + swz(4 * g16 + e, l16));
+#pragma unroll
+          for (int w = 0; w < 4; ++w) pv.v[0][e][w] = x[w];
         }
-      }
-    } else {
+        __syncthreads();  // every wave has read slot j
+        const int pid = next_pid;
+        next_pid = sm_ids[ii + D + 1];
+        issue_page(pid, p_begin + ii + D, j);
+        if (active) {
+          const int p = p_begin + ii;
+          const bool masked = (p + 1) * kPageSize > mask_from;
+          f4 sc[NB];
 #pragma unroll
-      for (int i = 0; i < CPR / 4; ++i) {
-        const int e = i * 64 + lane;
-        const int slot = e / CPR;
-        if (slot_real(nb, slot))
-          *(f4*)(a.part_o + (item_of(nb, slot) + row_in_head(nb, slot)) * HD + 4 * (e % CPR)) = v[i];
-      }
-      if (g16 == 0 && slot_real(nb, l16)) {
-        const size_t pitem = item_of(nb, l16) + row_in_head(nb, l16);
-        a.part_ml[pitem * 2 + 0] = st.m[nb];
-        a.part_ml[pitem * 2 + 1] = st.l[nb];
+          for (int nb = 0; nb < NB; ++nb) {
+            sc[nb] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) sc[nb] = E::mma_qk(kf.k[0][kk], qreg[nb][kk], sc[nb]);
+          }
+          page_finish<NB, HD, E, KV, 1>(st, sc, pv, false, dbits, mask_from,
+                                        p * kPageSize + 4 * g16, len, masked, a.scale_log2);
+        }
       }
     }
   }
+  // Loads past the split still write (zeros) into the ring: drain them before
+  // the ring becomes the output staging.
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (!active) return;
+  write_results<NB, HD, E>(a, st, (float*)sm_ring + wave * 16 * (HD + 4), map, direct,
+                           !single && !balanced, b, slot);
 }
 
 // Log-sum-exp merge of split partials (reference: csrc/small_q_attention_ext.cu:339-366):
@@ -1262,6 +1535,9 @@ void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, d
   } else if (sh.row_blocks == 2) {
     hipLaunchKernelGGL((sqa_partial_kernel<2, D4, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
                        a);
+  } else if constexpr (HD == 128 && KV::kBytes == 2) {
+    // 33..64 rows over 16-bit caches: two waves per kv head sharing an LDS ring.
+    hipLaunchKernelGGL((sqa_partial_lds_kernel<4, E>), grid, dim3(512), 0, stream, a);
   } else if constexpr (HD != 256) {
     hipLaunchKernelGGL((sqa_partial_kernel<4, D3, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
                        a);
