@@ -1140,34 +1140,85 @@ __device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, unsigne
       : "memory");
 }
 
-// Byte offset of 16-byte chunk c (0..15) of token t (0..15) in a head's 4 KiB
-// page slice in LDS: chunk c of token t sits at position 16 t + (c ^ t), so the
-// 16 tokens an MFMA operand read takes at one chunk fall in 16 bank groups.
-__device__ __forceinline__ unsigned swz(int t, int c) { return (unsigned)(16 * t + (c ^ t)) * 16u; }
+// LDS layout of one head's page slice (16 tokens x HD elements of the cache's
+// type) for the 8-wave kernel, and the reads that turn it into the register
+// form KV::load gives the main kernel (KV::Regs), so the math is shared.
+// 16-bit caches: 16 chunks of 16 bytes per token; chunk c of token t sits at
+// position 16 t + (c ^ t), so the 16 tokens an MFMA operand read takes at one
+// chunk fall in 16 different bank groups.
+template <typename KV>
+struct LdsSlice;
 
-// 33..64 query rows per kv head (q_len 16 at GQA 4) at head dim 128 over 16-bit
-// caches. Eight waves per workgroup: two per kv head, each with 32 of the head's
-// rows in two 16-row blocks (the 32-row math), so no wave holds the 128
-// accumulator registers of 64 rows, and two waves share each SIMD, one's MFMAs
-// under the other's softmax. The two waves of a head read each page once
-// between them: the workgroup's K and V of 4 heads (32 KiB a page) arrive in a
-// ring of D LDS slots by direct buffer loads (buffer_load_dwordx4 ... lds; four
-// per thread and page, 1 KiB of a head's page slice each, chunks swizzled as
-// swz()), so the bytes in flight take no registers. Per page: wait for this
+template <>
+struct LdsSlice<KvNative<128>> {
+  static constexpr int kChunks = 16;  // 16-byte chunks per token row (256 bytes)
+  __device__ __forceinline__ static int pos(int t, int c) { return 16 * t + (c ^ t); }
+  __device__ __forceinline__ static int token_of(int p) { return p >> 4; }
+  __device__ __forceinline__ static int chunk_of(int p) { return (p & 15) ^ (p >> 4); }
+  // K fragment kk of lane (g, l16): token l16, dims 32 kk + 8 g (chunk 4 kk + g);
+  // V: tokens 4 g + e, dims 8 l16 .. + 7 (chunk l16).
+  __device__ __forceinline__ static void read(KvNative<128>::Regs& r, const char* ks,
+                                              const char* vs, int g, int l16) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) r.k[kk] = *(const u4*)(ks + 16 * pos(l16, 4 * kk + g));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const u4 x = *(const u4*)(vs + 16 * pos(4 * g + e, l16));
+#pragma unroll
+      for (int w = 0; w < 4; ++w) r.v[e][w] = x[w];
+    }
+  }
+};
+
+// OCP e4m3 caches: 8 chunks of 16 bytes per token; chunk c of token t at
+// position 8 t + (c ^ ((t >> 1) & 7)): the K reads (16 tokens at one chunk) hit
+// 16 bank groups, the V reads (two tokens of 128 bytes per half-wave) two ways.
+template <>
+struct LdsSlice<KvFp8<128>> {
+  static constexpr int kChunks = 8;  // 16-byte chunks per token row (128 bytes)
+  __device__ __forceinline__ static int pos(int t, int c) { return 8 * t + (c ^ ((t >> 1) & 7)); }
+  __device__ __forceinline__ static int token_of(int p) { return p >> 3; }
+  __device__ __forceinline__ static int chunk_of(int p) { return (p & 7) ^ ((p >> 4) & 7); }
+  // K load i of lane (g, l16): token l16, bytes 64 i + 16 g (chunk 4 i + g);
+  // V: tokens 4 g + e, bytes 8 l16 .. + 7 (half l16 & 1 of chunk l16 / 2).
+  __device__ __forceinline__ static void read(KvFp8<128>::Regs& r, const char* ks, const char* vs,
+                                              int g, int l16) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) r.k[i] = *(const u4*)(ks + 16 * pos(l16, 4 * i + g));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const u2 x = *(const u2*)(vs + 16 * pos(4 * g + e, l16 >> 1) + 8 * (l16 & 1));
+      r.v[e][0] = x[0];
+      r.v[e][1] = x[1];
+    }
+  }
+};
+
+// 33..64 query rows per kv head (q_len 16 at GQA 4) at head dim 128. Eight
+// waves per workgroup: two per kv head, each with 32 of the head's rows in two
+// 16-row blocks (the 32-row math), so no wave holds the 128 accumulator
+// registers of 64 rows, and two waves share each SIMD, one's MFMAs under the
+// other's softmax. The two waves of a head read each page once between them:
+// the workgroup's K and V of 4 heads (32 KiB a page for 16-bit caches, 16 KiB
+// for e4m3) arrive in a ring of D LDS slots by direct buffer loads
+// (load_to_lds: 1 KiB of a head's page slice per wave and load, in the layout of
+// LdsSlice), so the bytes in flight take no registers. Per page: wait for this
 // thread's loads of the page (manual vmcnt: nothing else in the loop touches
 // vector memory), a barrier (the page is in LDS), read the wave's K and V into
 // registers, a second barrier (every wave has read the slot), refill the slot
 // with the page D ahead, then the math: a slot is refilled before its page's
 // math, so D pages stay in flight. Pages past the split load through a
 // zero-length resource (zeros, no memory traffic), as in sqa_partial_kernel.
-template <int D, typename E>
+template <int D, typename E, typename KV>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void sqa_partial_lds_kernel(PartialArgs a) {
   constexpr int HD = 128, NB = 2, KK = Dims<HD>::KK, MB = Dims<HD>::MB;
-  using KV = KvNative<HD>;
-  constexpr int kHeadSlice = 16 * HD * 2;        // one head's K (or V) of a page: 4 KiB
-  constexpr int kSlot = 2 * 4 * kHeadSlice;      // K and V of 4 heads: 32 KiB
+  using L = LdsSlice<KV>;
+  constexpr int kHeadSlice = 16 * L::kChunks * 16;  // one head's K (or V) of a page
+  constexpr int kSlot = 2 * 4 * kHeadSlice;         // K and V of 4 heads
+  constexpr int kLoads = kSlot / (512 * 16);        // loads per thread and page
   constexpr int kThreads = 512;
+  static_assert(HD * KV::kBytes == 16 * L::kChunks, "a token row is kChunks 16-byte chunks");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g16 = lane >> 4;
@@ -1236,21 +1287,24 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   // The ring and, after the loop, the waves' output staging.
   __shared__ __attribute__((aligned(16))) char sm_ring[D * kSlot];
   __shared__ int sm_ids[kIdSlots * kThreads];
-  // Load i (0..3) of a thread fills 1 KiB chunk ci = 8 i + wave of a slot: K
-  // (ci < 16) or V of head slot (ci / 4) % 4, tokens 4 (ci % 4) .. + 3; lane l
-  // holds position 64 (ci % 4) + l of the head's slice, token t = position / 16,
-  // chunk (position % 16) ^ t.
+  // Load i of a thread fills 1 KiB piece ci = 8 i + wave of a slot: K (first
+  // half of the pieces) or V, head slot (ci / parts) % 4, part ci % parts of the
+  // head's slice; lane l fills position 64 part + l, i.e. chunk
+  // L::chunk_of(position) of token L::token_of(position).
+  constexpr int kParts = kHeadSlice / 1024;  // 1 KiB pieces per head slice
   const unsigned tok_bytes = a.token_stride;
-  unsigned voff[4];
+  unsigned voff[kLoads];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kLoads; ++i) {
     const int ci = 8 * i + wave;
-    const int pos = 64 * (ci & 3) + lane;
-    const int t = pos >> 4, c = (pos & 15) ^ t;
-    voff[i] = t * tok_bytes + (hgrp * 4 + ((ci >> 2) & 3)) * a.head_stride + 16 * c;
+    const int pos = 64 * (ci % kParts) + lane;
+    voff[i] = L::token_of(pos) * tok_bytes + (hgrp * 4 + (ci / kParts) % 4) * a.head_stride +
+              16 * L::chunk_of(pos);
   }
   const size_t sub_bytes = (size_t)kPageSize * tok_bytes;
   auto issue_page = [&](int pid, int p, int j) {
+    // The page is the same for the whole workgroup: its resource lives in SGPRs.
+    pid = __builtin_amdgcn_readfirstlane(pid);
     const size_t off =
         pid >= 0 ? (size_t)pid * (size_t)a.page_stride + (size_t)(p & sub_mask) * sub_bytes : 0;
     const int nrec = pid >= 0 ? (int)a.page_extent : 0;
@@ -1259,8 +1313,8 @@ void sqa_partial_lds_kernel(PartialArgs a) {
     const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)((const char*)a.v + off), (short)0, nrec, kBufferFlags);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      load_to_lds(i < 2 ? kr : vr, voff[i],
+    for (int i = 0; i < kLoads; ++i)
+      load_to_lds(i < kLoads / 2 ? kr : vr, voff[i],
                   (unsigned)(size_t)(sm_ring + j * kSlot + (8 * i + wave) * 1024));
   };
 #pragma unroll
@@ -1289,20 +1343,11 @@ void sqa_partial_lds_kernel(PartialArgs a) {
     for (int j = 0; j < D; ++j) {
       const int ii = i + j;
       if (ii < n_split) {  // uniform over the workgroup
-        wait_vmcnt<4 * (D - 1)>();  // this thread's loads of page ii
-        __syncthreads();             // everyone's: page ii is in slot j
+        wait_vmcnt<kLoads * (D - 1)>();  // this thread's loads of page ii
+        __syncthreads();                  // everyone's: page ii is in slot j
         const char* ks = sm_ring + j * kSlot + hs * kHeadSlice;
-        const char* vs = ks + 4 * kHeadSlice;
-        PageK<HD, 1> kf;
-        PageV<HD, 1> pv;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) kf.k[0][kk] = *(const u4*)(ks + swz(l16, 4 * kk + g16));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const u4 x = *(const u4*)(vs + swz(4 * g16 + e, l16));
-#pragma unroll
-          for (int w = 0; w < 4; ++w) pv.v[0][e][w] = x[w];
-        }
+        typename KV::Regs raw[1];
+        L::read(raw[0], ks, ks + 4 * kHeadSlice, g16, l16);
         __syncthreads();  // every wave has read slot j
         const int pid = next_pid;
         next_pid = sm_ids[ii + D + 1];
@@ -1310,6 +1355,8 @@ void sqa_partial_lds_kernel(PartialArgs a) {
         if (active) {
           const int p = p_begin + ii;
           const bool masked = (p + 1) * kPageSize > mask_from;
+          const PageK<HD, 1> kf = widen_k<E, KV, HD, 1>(raw);
+          PageV<HD, 1> pv = widen_v<E, KV, HD, 1>(raw);
           f4 sc[NB];
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
@@ -1535,9 +1582,11 @@ void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, d
   } else if (sh.row_blocks == 2) {
     hipLaunchKernelGGL((sqa_partial_kernel<2, D4, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
                        a);
-  } else if constexpr (HD == 128 && KV::kBytes == 2) {
-    // 33..64 rows over 16-bit caches: two waves per kv head sharing an LDS ring.
-    hipLaunchKernelGGL((sqa_partial_lds_kernel<4, E>), grid, dim3(512), 0, stream, a);
+  } else if constexpr (HD == 128) {
+    // 33..64 rows: two waves per kv head sharing an LDS ring of 128 KiB (4 pages
+    // of 16-bit K and V, 8 of e4m3).
+    constexpr int DL = KV::kBytes == 2 ? 4 : 8;
+    hipLaunchKernelGGL((sqa_partial_lds_kernel<DL, E, KV>), grid, dim3(512), 0, stream, a);
   } else if constexpr (HD != 256) {
     hipLaunchKernelGGL((sqa_partial_kernel<4, D3, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
                        a);

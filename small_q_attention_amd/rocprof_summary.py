@@ -113,7 +113,7 @@ def main(argv=None):
         ratio = fbytes / args.kv_bytes
         lines.append(f"{name} | {calls} | {avg:.2f} | {mn:.2f} | {mx:.2f} | {fbytes:.4e} | "
                      f"{wbytes:.4e} | {ratio:.4f}")
-        if name.startswith("sqa_partial_kernel"):
+        if name.startswith("sqa_partial"):
             partial_traffic = fbytes + wbytes
             lines.append(f"partial_kernel_avg_us: {avg:.2f}")
             lines.append(f"partial_kernel_kv_GBps: {args.kv_bytes / (avg * 1e-6) / 1e9:.1f}")
