@@ -236,8 +236,8 @@ int run_attention(const sqa_attention_args& a) {
                   sqa::kMaxBalancedBatch, batch);
     if (kernel_pages >= (1LL << 24))
       return fail(SQA_ERR_INVALID, "balanced plan needs block-table rows under 2^28 tokens");
-    if ((long long)batch * kernel_pages >= (1LL << 31))
-      return fail(SQA_ERR_INVALID, "balanced plan needs batch * pages per row under 2^31");
+    if ((long long)batch * kernel_pages >= (1LL << 30))
+      return fail(SQA_ERR_INVALID, "balanced plan needs batch * pages per row under 2^30");
     const long long cap = ceil_div((long long)batch * kernel_pages, sqa::kMaxSplitPages);
     if ((long long)num_splits - batch < (cap > 1 ? cap : 1))
       return fail(SQA_ERR_INVALID,
@@ -295,10 +295,8 @@ int run_attention(const sqa_attention_args& a) {
   pa.pages_per_split = balanced ? 0 : pages_per_split;
   pa.num_splits = num_splits;
   pa.spec_pages = spec_pages;
-  pa.spec_pps = pa.spec_splits = 0;
-  if (spec_pages > 0)
-    sqa::uniform_balanced_plan(batch, num_splits - batch, spec_pages, &pa.spec_pps,
-                               &pa.spec_splits);
+  pa.spec_pps =
+      spec_pages > 0 ? sqa::packed_item_pages(batch * spec_pages, num_splits - batch) : 0;
   pa.scale_log2 = (float)(1.4426950408889634 * (double)a.scale);
   pa.out_scale = a.out_scale;
   pa.bf16 = a.dtype == SQA_DTYPE_BF16;
@@ -326,7 +324,7 @@ int run_attention(const sqa_attention_args& a) {
     ma.pages_per_split = pa.pages_per_split;
     ma.num_splits = num_splits;
     ma.spec_pages = spec_pages;
-    ma.spec_splits = pa.spec_splits;
+    ma.spec_pps = pa.spec_pps;
     ma.out_scale = a.out_scale;
     ma.bf16 = pa.bf16;
     if ((e = sqa::launch_merge(ma, s)) != hipSuccess) return hip_fail(e, "merge kernel launch");

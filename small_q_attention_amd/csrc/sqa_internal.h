@@ -29,23 +29,24 @@ struct SeqSplits {
 //
 // Two split plans. Fixed (pages_per_split > 0): sequence b owns slots
 // b * num_splits + s, split s covering pages [s * pages_per_split, ...).
-// Balanced (pages_per_split == 0, batch <= kMaxBalancedBatch): num_splits is
-// the number of work-item slots; every workgroup derives, from all seq_lens,
-// one split size for the whole batch (total pages / (num_splits - batch),
-// rounded up) and the (sequence, split) of its item, so all items carry the
-// same number of pages whatever the length distribution. Partial slot of
-// (sequence, split) = first slot of the sequence + split; sequences whose
-// pages fit one split are written straight to the output.
+// Balanced (pages_per_split <= 0, batch <= kMaxBalancedBatch): num_splits =
+// T + batch slots for T work items. Every workgroup derives, from all seq_lens,
+// the batch's pages laid end to end and one item size P = ceil(total / T)
+// (packed_item_pages); item i takes global pages [i P, (i + 1) P), crossing
+// sequence ends where they fall, so all items carry the same number of pages
+// whatever the length distribution. The part of item i in sequence b (a piece)
+// leaves its partial in slot i + b; a sequence inside one piece is written
+// straight to the output. The kernel records each sequence's (first slot,
+// count) for the merge.
 //
 // spec_pages > 0 (balanced plan only): the page count the caller expects every
-// sequence to have (from max_seq_len), with the plan for that case computed by
-// the host (uniform_balanced_plan: spec_pps pages per split, spec_splits splits
-// per sequence, sequence b's splits in slots b * spec_splits + s). Workgroups
-// take their item from it and issue their first page-id loads together with the
-// lengths; a length that does not match sends the workgroup back to the plan
-// from the loaded lengths. Either way the plan is the one the lengths give
-// (for equal page counts both rules pick the same split size): the expectation
-// only saves a memory round trip and the plan's wave reductions when it holds.
+// sequence to have (from max_seq_len), with that case's item size computed by
+// the host (spec_pps = packed_item_pages(batch * spec_pages, T)). Workgroups
+// then know their first piece without the lengths and issue its page-id loads
+// together with them; a length that does not match sends the workgroup back to
+// the plan from the loaded lengths. Either way the plan is the one the lengths
+// give: the expectation only saves a memory round trip and the plan's wave
+// reductions when it holds.
 //
 // The C ABI carries spec_pages in pages_per_split: 0 is the balanced plan,
 // -P the balanced plan expecting P pages per sequence.
@@ -73,7 +74,7 @@ struct PartialArgs {
   int max_pages;              // kernel pages a block-table row addresses (bt_stride << page_shift)
   int pages_per_split, num_splits;
   int spec_pages;             // balanced plan: expected pages of every sequence (0: none)
-  int spec_pps, spec_splits;  // the balanced plan when every sequence spans spec_pages pages
+  int spec_pps;               // the balanced plan's item size when every sequence spans spec_pages
   float scale_log2;           // softmax scale * log2(e)
   float out_scale;            // multiplier applied to the normalised output
   int bf16;                   // element type of Q and out (and of K, V unless kv_fp8): 0 fp16, 1 bf16
@@ -103,39 +104,18 @@ struct MergeArgs {
   int max_pages;  // kernel pages a block-table row addresses
   int pages_per_split, num_splits;
   int spec_pages;   // balanced plan: expected pages of every sequence (0: none)
-  int spec_splits;  // splits per sequence of the balanced plan when that holds
+  int spec_pps;     // the balanced plan's item size when that holds
   float out_scale;
   int bf16;
 };
 
-// The balanced plan's split size and split count when all `batch` sequences span
-// `pages` pages and `target` (= num_splits - batch) work items are to be filled:
-// the smallest size from ceil(total / target) up (clamped to [kMinSplitPages,
-// kMaxSplitPages], at most ceil(total / (target - batch)) when target > batch)
-// whose split counts fit the target. The kernels' balanced plan applies the same
-// rule to the loaded page counts (requires batch * pages < 2^31).
-inline void uniform_balanced_plan(int batch, int target, int pages, int* pps_out,
-                                  int* splits_out) {
-  const int total = batch * pages;
-  const int lo = std::min(std::max((total + target - 1) / target, kMinSplitPages), kMaxSplitPages);
-  int hi = lo;
-  if (target > batch)
-    hi = std::min(std::max((total + target - batch - 1) / (target - batch), lo), kMaxSplitPages);
-  auto count = [&](int size) { return (long long)batch * ((pages + size - 1) / size); };
-  int pps = lo;
-  if (hi > lo && count(lo) > target) {
-    int l = lo + 1, h = hi;
-    while (l < h) {
-      const int mid = (l + h) >> 1;
-      if (count(mid) <= target)
-        h = mid;
-      else
-        l = mid + 1;
-    }
-    pps = h;
-  }
-  *pps_out = pps;
-  *splits_out = (pages + pps - 1) / pps;
+// The balanced plan's item size: pages per work item when `total` pages are
+// shared by `target` (= num_splits - batch) items, clamped to [kMinSplitPages,
+// kMaxSplitPages]. ceil(total / P) <= target when target >= ceil(total /
+// kMaxSplitPages), which the C ABI checks.
+__host__ __device__ inline int packed_item_pages(int total, int target) {
+  const int p = (total + target - 1) / target;
+  return p < kMinSplitPages ? kMinSplitPages : (p > kMaxSplitPages ? kMaxSplitPages : p);
 }
 
 // Launch shape of the partial kernel for a given number of query rows per kv

@@ -531,6 +531,15 @@ __device__ __forceinline__ ItemRange fixed_item(const PartialArgs& a, int item) 
   return r;
 }
 
+// threadIdx.x through an empty asm statement: what a piece of work derives from
+// it is computed inside that piece, not hoisted by the compiler in front of the
+// loop over pieces, where it would hold registers through every page loop.
+__device__ __forceinline__ int piece_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 __device__ __forceinline__ int wave_sum_int(int v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -547,120 +556,111 @@ __device__ __forceinline__ int wave_inclusive_scan_int(int v) {
   return v;
 }
 
-// Balanced plan (batch <= kMaxBalancedBatch = 4 x 64). num_splits = T + batch
-// slots, T = the work items one wave of resident workgroups holds. Every wave
-// derives the same plan on its own, with wave reductions only (no LDS, no
-// barrier), from per-lane page counts: lane l holds sequences l, l + 64,
-// l + 128, l + 192, and the wave picks one split size for the batch: the
-// smallest in [ceil(total / T), ceil(total / (T - batch))] (clamped to
-// [kMinSplitPages, kMaxSplitPages]) whose per-sequence split counts sum to at
-// most T (bisection), so no workgroup waits for a second wave; the lower end
-// alone always fits the T + batch slots. A scan of the split counts gives each
-// sequence its first slot, and the lane whose sequence holds `item` hands its
-// range to the wave. With write_table, wave 0 stores every sequence's (first
-// slot, split count) for the merge kernel. The range's `len` is left for the
-// caller. Every workgroup computes the same plan from the same page counts.
+// Balanced plan (batch <= kMaxBalancedBatch = 4 x 64), packed: num_splits =
+// T + batch slots, T = the work items one wave of resident workgroups holds. The
+// pages of all sequences, concatenated in batch order (sequence b's pages start
+// at start_b, the sum of the page counts before it), are cut into items of
+// P = ceil(total / T) pages (clamped to [kMinSplitPages, kMaxSplitPages]):
+// item i is global pages [i P, min((i + 1) P, total)), whatever the lengths,
+// so every workgroup streams the same number of pages and none waits for a
+// second wave. An item visits each sequence it overlaps as a piece, with its own
+// softmax state, rows and partial slot i + b (unique: walking the pages in
+// order, each next piece has the next item or the next sequence and neither
+// index ever falls, so i + b grows strictly). Sequence b thus owns slots
+// [i0_b + b, i1_b + b], i0_b = start_b / P, i1_b = (start_b + pages_b - 1) / P;
+// a sequence inside one item is finished by the partial kernel. Lane l holds sequences l, l + 64, l + 128, l + 192:
+// every wave derives the plan on its own with wave reductions (no LDS, no
+// barrier), and wave 0 of workgroup 0 writes each sequence's (first slot,
+// count) for the merge kernel.
 constexpr int kSeqPerLane = kMaxBalancedBatch / 64;
 
-__device__ ItemRange balanced_plan(const PartialArgs& a, int item, const int (&pages)[kSeqPerLane],
-                                   bool write_table) {
-  constexpr int K = kSeqPerLane;
+// The per-lane view of the batch a packed plan works from (lane l: sequences
+// l + 64 k). Page counts are recomputed from the lengths where needed, which
+// keeps the view at two registers per sequence slot: it stays live through the
+// item's pieces.
+struct PackedBatch {
+  int start[kSeqPerLane];  // first global page of each sequence
+  int len[kSeqPerLane];    // lengths (0 past the batch)
+  int P;                   // pages per item
+  int total;               // pages of the batch
+};
+
+// Kernel pages of a sequence of `len` tokens within a block-table row.
+__device__ __forceinline__ int pages_of(const PartialArgs& a, int len) {
+  return min((len + kPageSize - 1) / kPageSize, a.max_pages);
+}
+
+__device__ __forceinline__ int wave_exclusive_scan_int(int v) {
+  return wave_inclusive_scan_int(v) - v;
+}
+
+// Prefix sums of the page counts and the item size; with write_table, the
+// merge kernel's table.
+__device__ __forceinline__ void packed_plan(const PartialArgs& a, PackedBatch& pb,
+                                            bool write_table) {
   const int lane = threadIdx.x & 63;
-  const int groups = (a.batch + 63) / 64;  // uniform; groups of 64 sequences in use
-  int total = 0;
+  int base = 0;  // pages of the groups of 64 sequences before this one
+  int pages[kSeqPerLane];
 #pragma unroll
-  for (int k = 0; k < K; ++k) total += pages[k];
-  total = wave_sum_int(total);
-  // ceil(n / size) for a uniform size: float reciprocal, then one correction
-  // each way (n < 2^24, so the estimate is off by at most one).
-  auto ceil_div_u = [](int n, int size, float inv) {
-    int q = (int)((float)n * inv);
-    q += (q + 1) * size <= n ? 1 : 0;
-    q -= q * size > n ? 1 : 0;
-    return q + (q * size < n ? 1 : 0);
-  };
-  auto count_splits = [&](int size) {
-    const float inv = 1.f / (float)size;
-    int n = 0;
-#pragma unroll
-    for (int k = 0; k < K; ++k)
-      if (k < groups) n += ceil_div_u(pages[k], size, inv);
-    return wave_sum_int(n);
-  };
-  const int target = a.num_splits - a.batch;
-  const int lo = min(max((total + target - 1) / target, kMinSplitPages), kMaxSplitPages);
-  int hi = lo;
-  if (target > a.batch)
-    hi = min(max((total + target - a.batch - 1) / (target - a.batch), lo), kMaxSplitPages);
-  int pps = lo;
-  if (hi > lo && count_splits(lo) > target) {
-    int l = lo + 1, h = hi;  // uniform bisection: smallest size in (lo, hi] that fits
-    while (l < h) {
-      const int mid = (l + h) >> 1;
-      if (count_splits(mid) <= target)
-        h = mid;
-      else
-        l = mid + 1;
-    }
-    pps = h;
+  for (int k = 0; k < kSeqPerLane; ++k) {
+    pages[k] = pages_of(a, pb.len[k]);
+    pb.start[k] = base + wave_exclusive_scan_int(pages[k]);
+    base += wave_sum_int(pages[k]);
   }
-  ItemRange r;
-  r.b = -1;  // no work item unless a sequence holds `item`
-  r.split = 0;
-  r.len = 0;
-  r.p_begin = 0;
-  r.p_end = 0;
-  r.slot0 = 0;
-  r.n_valid = 0;
-  int base = 0;  // slots of the sequences before this group of 64
+  pb.total = base;
+  pb.P = packed_item_pages(pb.total, a.num_splits - a.batch);
+  if (write_table && threadIdx.x < 64) {
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    if (k >= groups) break;
-    const int splits = (pages[k] + pps - 1) / pps;
-    const int incl = wave_inclusive_scan_int(splits);
-    const int first = base + incl - splits;
-    const int sq = 64 * k + lane;
-    if (write_table && threadIdx.x < 64 && sq < a.batch) a.seq_splits[sq] = SeqSplits{first, splits};
-    const bool mine = sq < a.batch && item >= first && item < first + splits;
+    for (int k = 0; k < kSeqPerLane; ++k) {
+      const int sq = 64 * k + lane;
+      if (sq < a.batch) {
+        const int i0 = pb.start[k] / pb.P;
+        const int count = pages[k] > 0 ? (pb.start[k] + pages[k] - 1) / pb.P - i0 + 1 : 0;
+        a.seq_splits[sq] = SeqSplits{min(i0 + sq, a.num_splits - 1), count};
+      }
+    }
+  }
+}
+
+// The piece of item `item` that holds global page g (g inside the item): its
+// sequence, page range (within the sequence), length, split count and slot.
+__device__ __forceinline__ ItemRange packed_piece(const PartialArgs& a, const PackedBatch& pb,
+                                                 int item, int g) {
+  ItemRange r;
+  r.b = -1;
+  r.split = 0;
+  r.p_begin = r.p_end = r.len = r.n_valid = r.slot0 = 0;
+  const int g_end = min((item + 1) * pb.P, pb.total);
+#pragma unroll
+  for (int k = 0; k < kSeqPerLane; ++k) {
+    // Lengths are 0 past the batch: those slots have no pages.
+    const bool mine = pb.start[k] <= g && g < pb.start[k] + pages_of(a, pb.len[k]);
     const unsigned long long hit = __ballot(mine);
     if (hit) {
       const int src = __builtin_ctzll(hit);
+      r.len = __shfl(pb.len[k], src);
+      const int st = __shfl(pb.start[k], src), np = pages_of(a, r.len);
       r.b = 64 * k + src;
-      r.split = item - __shfl(first, src);
-      r.slot0 = __shfl(first, src);
-      r.n_valid = __shfl(splits, src);
-      r.p_begin = r.split * pps;
-      r.p_end = min(r.p_begin + pps, __shfl(pages[k], src));
+      r.p_begin = g - st;
+      r.p_end = min(g_end, st + np) - st;
+      r.n_valid = (st + np - 1) / pb.P - st / pb.P + 1;
+      r.slot0 = item + r.b;
     }
-    base += __shfl(incl, 63);
   }
   return r;
 }
 
-// Lengths of sequences l, l + 64, l + 128, l + 192 in lane l (0 past the batch)
-// and their page counts (clamped to the block-table row). The loads are
-// unconditional, from clamped in-bounds addresses, and selected afterwards: a
-// load under a branch is waited for where the branch joins, which would put a
-// full memory round trip in front of whatever follows.
-__device__ __forceinline__ void load_lengths(const PartialArgs& a, int (&len)[kSeqPerLane],
-                                             int (&pages)[kSeqPerLane]) {
+// Lengths of sequences l, l + 64, l + 128, l + 192 in lane l (0 past the
+// batch). The loads are unconditional, from clamped in-bounds addresses, and
+// selected afterwards: a load under a branch is waited for where the branch
+// joins, which would put a full memory round trip in front of whatever follows.
+__device__ __forceinline__ void load_lengths(const PartialArgs& a, int (&len)[kSeqPerLane]) {
   const int lane = threadIdx.x & 63;
   int raw[kSeqPerLane];
 #pragma unroll
   for (int k = 0; k < kSeqPerLane; ++k) raw[k] = a.seq_lens[min(64 * k + lane, a.batch - 1)];
 #pragma unroll
-  for (int k = 0; k < kSeqPerLane; ++k) {
-    len[k] = 64 * k + lane < a.batch ? max(raw[k], 0) : 0;
-    pages[k] = min((len[k] + kPageSize - 1) / kPageSize, a.max_pages);
-  }
-}
-
-// The length of sequence b (uniform) from the per-lane lengths.
-__device__ __forceinline__ int length_of(const int (&len)[kSeqPerLane], int b) {
-  int v = len[0];
-#pragma unroll
-  for (int k = 1; k < kSeqPerLane; ++k) v = (b >> 6) == k ? len[k] : v;
-  return __shfl(v, b & 63);
+  for (int k = 0; k < kSeqPerLane; ++k) len[k] = 64 * k + lane < a.batch ? max(raw[k], 0) : 0;
 }
 
 // The rows of a wave: row slot r (0..15) of 16-row block nb is row row(nb, r)
@@ -684,77 +684,96 @@ struct WaveRows {
   }
 };
 
-// The work item of workgroup item `item` under either plan, with the ids of its
-// first D pages loaded (index clamped into the block-table row; ids past the
-// split are never used). Fixed plan: the page range follows from `item` alone,
-// so those ids are issued before the sequence length is read and both arrive
-// in one round trip. Balanced plan: all lengths, the plan's wave reductions,
-// then the ids; with an expected page count, the host's plan for it gives the
-// item at once and the ids go out with the lengths. The fields are the same in
-// every lane (readfirstlane): the item, and the buffer-resource addresses built
-// from it, stay in scalar registers.
-template <int D>
-__device__ __forceinline__ ItemRange work_item(const PartialArgs& a, int item, int (&first_id)[D]) {
+// Runs `piece(range, first_id)` for every piece of workgroup item `item`, with
+// the ids of the piece's first D pages loaded (index clamped into the
+// block-table row; ids past the piece are never used). Fixed plan: one piece
+// whose page range follows from `item` alone, so its ids are issued before the
+// sequence length is read and both arrive in one round trip. Balanced plan:
+// all lengths, the packed plan's wave reductions, then each piece's ids; with
+// an expected page count (every sequence spec_pages pages, item size spec_pps
+// from the host) the plan needs no lengths, so the first piece's ids go out
+// with them, and a length that does not match falls back to the plan from the
+// loaded lengths. Piece fields are the same in every lane (readfirstlane): the
+// piece, and the buffer-resource addresses built from it, stay in scalar
+// registers. Consecutive pieces are separated by a barrier (they reuse the
+// workgroup's LDS).
+template <int D, typename Piece>
+__device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, Piece&& piece) {
   const int lane = threadIdx.x & 63;
+  const bool balanced = is_balanced(a.pages_per_split);
+  int first_id[D];
   auto load_first_ids = [&](int seq, int p0) {
-    const int32_t* row = a.block_tables + (size_t)seq * a.bt_stride;
+    const int32_t* row = a.block_tables + (size_t)max(seq, 0) * a.bt_stride;
 #pragma unroll
     for (int j = 0; j < D; ++j)
       first_id[j] = row[min(max(p0 + j, 0), a.max_pages - 1) >> a.page_shift];
   };
-  const bool balanced = is_balanced(a.pages_per_split);
+  PackedBatch pb;
   ItemRange it;
-  bool ids_loaded = !balanced;  // uniform
+  bool ids_loaded = false;
+  int g = 0, g_end = 1;  // global pages still to visit (fixed plan: one piece)
   if (!balanced) {
     const int seq = item / a.num_splits;
     load_first_ids(seq, (item - seq * a.num_splits) * a.pages_per_split);
+    ids_loaded = true;
     it = fixed_item(a, item);
   } else {
-    int len[kSeqPerLane], pages[kSeqPerLane];
     if (a.spec_pages > 0) {
-      // The item from the host's plan for the expected page count (sequence b's
-      // splits in slots b * spec_splits + s), then its first page ids and all
-      // lengths in one round trip.
-      const int ks = a.spec_splits, P = a.spec_pages;
-      it.b = item < a.batch * ks ? item / ks : -1;
-      it.split = it.b >= 0 ? item - it.b * ks : 0;
-      it.p_begin = it.split * a.spec_pps;
-      it.p_end = it.b >= 0 ? min(it.p_begin + a.spec_pps, P) : 0;
-      it.slot0 = it.b >= 0 ? it.b * ks : 0;
-      it.n_valid = it.b >= 0 ? ks : 0;
+      // Every sequence spec_pages pages: sequence b starts at b * spec_pages;
+      // the item size comes from the host. The first piece's ids go out with
+      // the lengths (index clamped: an item past the batch never uses them).
+      const int P = a.spec_pages;
+#pragma unroll
+      for (int k = 0; k < kSeqPerLane; ++k) pb.start[k] = min(64 * k + lane, a.batch) * P;
+      pb.total = a.batch * P;
+      pb.P = a.spec_pps;
       if (blockIdx.x == 0 && threadIdx.x < 64) {
 #pragma unroll
         for (int k = 0; k < kSeqPerLane; ++k) {
           const int sq = 64 * k + lane;
-          if (sq < a.batch) a.seq_splits[sq] = SeqSplits{sq * ks, ks};
+          if (sq < a.batch) {
+            const int i0 = pb.start[k] / pb.P;
+            a.seq_splits[sq] = SeqSplits{i0 + sq, (pb.start[k] + P - 1) / pb.P - i0 + 1};
+          }
         }
       }
-      load_first_ids(max(it.b, 0), it.p_begin);
-      load_lengths(a, len, pages);
+      const int g0 = item * pb.P;
+      const int b0 = min(g0 / P, a.batch - 1);
+      load_first_ids(b0, g0 - b0 * P);
+      load_lengths(a, pb.len);
       bool differs = false;
 #pragma unroll
       for (int k = 0; k < kSeqPerLane; ++k)
-        differs |= 64 * k + lane < a.batch && pages[k] != P;
+        differs |= 64 * k + lane < a.batch && pages_of(a, pb.len[k]) != P;
       if (__any(differs)) {
-        it = balanced_plan(a, item, pages, blockIdx.x == 0);  // rewrites the table
+        packed_plan(a, pb, blockIdx.x == 0);  // rewrites the table
       } else {
         ids_loaded = true;
       }
     } else {
-      load_lengths(a, len, pages);
-      it = balanced_plan(a, item, pages, blockIdx.x == 0);
+      load_lengths(a, pb.len);
+      packed_plan(a, pb, blockIdx.x == 0);
     }
-    it.len = it.b >= 0 ? length_of(len, it.b) : 0;
+    g = item * pb.P;
+    g_end = min(g + pb.P, pb.total);
   }
-  it.b = __builtin_amdgcn_readfirstlane(it.b);
-  it.split = __builtin_amdgcn_readfirstlane(it.split);
-  it.p_begin = __builtin_amdgcn_readfirstlane(it.p_begin);
-  it.p_end = __builtin_amdgcn_readfirstlane(it.p_end);
-  it.len = __builtin_amdgcn_readfirstlane(it.len);
-  it.n_valid = __builtin_amdgcn_readfirstlane(it.n_valid);
-  it.slot0 = __builtin_amdgcn_readfirstlane(it.slot0);
-  if (!ids_loaded) load_first_ids(max(it.b, 0), it.p_begin);
-  return it;
+  for (bool first = true; g < g_end; first = false) {  // uniform
+    if (balanced) {
+      it = packed_piece(a, pb, item, g);
+      if (!ids_loaded) load_first_ids(it.b, it.p_begin);
+    }
+    ids_loaded = false;
+    it.b = __builtin_amdgcn_readfirstlane(it.b);
+    it.split = __builtin_amdgcn_readfirstlane(it.split);
+    it.p_begin = __builtin_amdgcn_readfirstlane(it.p_begin);
+    it.p_end = __builtin_amdgcn_readfirstlane(it.p_end);
+    it.len = __builtin_amdgcn_readfirstlane(it.len);
+    it.n_valid = __builtin_amdgcn_readfirstlane(it.n_valid);
+    it.slot0 = __builtin_amdgcn_readfirstlane(it.slot0);
+    if (!first) __syncthreads();  // the previous piece is done with the LDS
+    piece(it, first_id);
+    g += balanced ? it.p_end - it.p_begin : 1;
+  }
 }
 
 // Draft bits of a row of sequence b, draft row qi: bit j = the row sees draft
@@ -796,7 +815,7 @@ __device__ __forceinline__ void write_results(const PartialArgs& a, WaveState<NB
   constexpr int MB = Dims<HD>::MB;
   constexpr int kStageRow = HD + 4;  // floats per staged row
   constexpr int CPR = HD / 4;        // 4-value chunks per row
-  const int lane = threadIdx.x & 63;
+  const int lane = piece_tid() & 63;
   const int g16 = lane >> 4, l16 = lane & 15;
   auto item_of = [&](int nb, int r) { return (slot * a.hkv + map.head(nb, r)) * a.rows; };
   // Row sums over the four lane groups.
@@ -875,7 +894,7 @@ __device__ __forceinline__ void write_results(const PartialArgs& a, WaveState<NB
 template <int NB, typename Map>
 __device__ __forceinline__ void write_empty_split(const PartialArgs& a, const Map& map,
                                                   size_t slot, float mark) {
-  const int lane = threadIdx.x & 63;
+  const int lane = piece_tid() & 63;
   if ((lane >> 4) != 0) return;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -902,10 +921,7 @@ template <int NB, int D, int WW, int WPE, int HD, typename E, typename KV, int H
 __global__ __launch_bounds__(WW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void sqa_partial_kernel(PartialArgs a) {
   constexpr int KK = Dims<HD>::KK, MB = Dims<HD>::MB;
-  const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g16 = lane >> 4;
-  const int l16 = lane & 15;
 
   // blockIdx.x = item * head_groups + head_group.
   const int head_groups = (a.hkv + WW * HPW - 1) / (WW * HPW);
@@ -917,11 +933,28 @@ void sqa_partial_kernel(PartialArgs a) {
   const bool active = kvh < a.hkv;
   const WaveRows<NB, HPW> map{kvh, a.rows, a.hkv};
 
-  // Start-up. First: the work item and the ids of its first D pages.
   const bool balanced = is_balanced(a.pages_per_split);
-  int first_id[D];
-  const ItemRange it = work_item<D>(a, item, first_id);
   const bool single = !balanced && a.num_splits == 1;  // no merge kernel follows
+  static_assert(2 * D + 1 <= kIdPad, "page-id table padding must cover the ring's look-ahead");
+  constexpr int kIdSlots = (kMaxSplitPages + kIdPad + WW * 64 - 1) / (WW * 64);
+  // LDS: the Q fragments of this wave's rows, [wave][nb][kk][lane] (the
+  // B-operand layout; each lane stores exactly the fragments it reads back),
+  // and the piece's page ids: ids of [p_begin, p_end) clamped into the pool,
+  // then -1 for the ring's look-ahead. Waves read ids back a step ahead of
+  // use, so no page waits on a block-table load from memory. sm_stage holds
+  // each wave's results on their way out (the epilogue below).
+  __shared__ u4 sm_q[WW * NB * KK * 64];
+  __shared__ float sm_stage[WW * 16 * (HD + 4)];
+  __shared__ int sm_ids[kIdSlots * WW * 64];
+
+  // Each piece of the work item (one, except where a balanced item spans the
+  // end of a sequence): its page range of one sequence, with the ids of its
+  // first D pages already requested.
+  for_each_piece<D>(a, item, [&](const ItemRange& it, const int (&first_id)[D]) {
+  const int tid = piece_tid();
+  const int lane = tid & 63;
+  const int g16 = lane >> 4;
+  const int l16 = lane & 15;
   const int b = max(it.b, 0);
   const int split = it.split;
   const int len = it.len;
@@ -935,7 +968,7 @@ void sqa_partial_kernel(PartialArgs a) {
   // workgroup leaves a partial for the merge kernel.
   const bool direct = it.n_valid <= 1;
   const size_t slot = (size_t)it.slot0 + split;
-  if (p_begin >= p_end && !single) {
+  if (p_begin >= p_end && !single) {  // fixed plan only
     if (active) write_empty_split<NB>(a, map, slot, it.n_valid == 1 ? -1.f : 0.f);
     return;  // uniform
   }
@@ -965,13 +998,11 @@ void sqa_partial_kernel(PartialArgs a) {
     }
     dbits[nb] = draft_bits(a, b, qi, real);
   }
-  static_assert(2 * D + 1 <= kIdPad, "page-id table padding must cover the ring's look-ahead");
-  constexpr int kIdSlots = (kMaxSplitPages + kIdPad + WW * 64 - 1) / (WW * 64);
   int idreg[kIdSlots];
   const int last_id = n_split > 0 ? n_split - 1 : 0;  // p_begin + last_id < max_pages
 #pragma unroll
   for (int k = 0; k < kIdSlots; ++k) {
-    const int i = threadIdx.x + k * WW * 64;
+    const int i = tid + k * WW * 64;
     const int x = bt_row[(p_begin + min(i, last_id)) >> shift];
     idreg[k] = i < n_split ? x : -1;
   }
@@ -1011,15 +1042,6 @@ void sqa_partial_kernel(PartialArgs a) {
     load_page(j < n_pages ? clamp_page(first_id[j], a.num_pages) : -1, p_begin + j, ring[j]);
   }
 
-  // LDS: the Q fragments of this wave's rows, [wave][nb][kk][lane] (the
-  // B-operand layout; each lane stores exactly the fragments it reads back),
-  // and the split's page ids: ids of [p_begin, p_end) clamped into the pool,
-  // then -1 for the ring's look-ahead. Waves read ids back a step ahead of
-  // use, so no page waits on a block-table load from memory. sm_stage holds
-  // each wave's results on their way out (the epilogue below).
-  __shared__ u4 sm_q[WW * NB * KK * 64];
-  __shared__ float sm_stage[WW * 16 * (HD + 4)];
-  __shared__ int sm_ids[kIdSlots * WW * 64];
   u4* my_q = sm_q + wave * NB * KK * 64;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -1028,7 +1050,7 @@ void sqa_partial_kernel(PartialArgs a) {
   }
 #pragma unroll
   for (int k = 0; k < kIdSlots; ++k) {
-    const int i = threadIdx.x + k * WW * 64;
+    const int i = tid + k * WW * 64;
     sm_ids[i] = idreg[k] >= 0 ? clamp_page(idreg[k], a.num_pages) : -1;
   }
   auto page_id = [&](int i) -> int { return active ? sm_ids[i] : -1; };
@@ -1095,9 +1117,10 @@ void sqa_partial_kernel(PartialArgs a) {
       load_page(pid, p_begin + ii + D, ring[j]);
     }
   }
-  if (!active) return;
-  write_results<NB, HD, E>(a, st, sm_stage + wave * 16 * (HD + 4), map, direct,
-                           !single && !balanced, b, slot);
+  if (active)
+    write_results<NB, HD, E>(a, st, sm_stage + wave * 16 * (HD + 4), map, direct,
+                             !single && !balanced, b, slot);
+  });
 }
 
 // The rows of one wave of the 8-wave kernel: rows base .. base + 31 of kv head
@@ -1219,10 +1242,7 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   constexpr int kLoads = kSlot / (512 * 16);        // loads per thread and page
   constexpr int kThreads = 512;
   static_assert(HD * KV::kBytes == 16 * L::kChunks, "a token row is kChunks 16-byte chunks");
-  const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g16 = lane >> 4;
-  const int l16 = lane & 15;
 
   // blockIdx.x = item * head_groups + head_group; wave = half * 4 + head slot.
   const int head_groups = (a.hkv + 3) / 4;
@@ -1236,9 +1256,32 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   const bool active = kvh < a.hkv && map.base < a.rows;
 
   const bool balanced = is_balanced(a.pages_per_split);
-  int first_id[D];
-  const ItemRange it = work_item<D>(a, item, first_id);
   const bool single = !balanced && a.num_splits == 1;
+  static_assert(D + 1 <= kIdPad, "page-id table padding must cover the ring's look-ahead");
+  constexpr int kIdSlots = (kMaxSplitPages + kIdPad + kThreads - 1) / kThreads;
+  // The ring and, after a piece's page loop, the waves' output staging.
+  __shared__ __attribute__((aligned(16))) char sm_ring[D * kSlot];
+  __shared__ int sm_ids[kIdSlots * kThreads];
+  // Load i of a thread fills 1 KiB piece ci = 8 i + wave of a slot: K (first
+  // half of the pieces) or V, head slot (ci / parts) % 4, part ci % parts of the
+  // head's slice; lane l fills position 64 part + l, i.e. chunk
+  // L::chunk_of(position) of token L::token_of(position).
+  constexpr int kParts = kHeadSlice / 1024;  // 1 KiB pieces per head slice
+  const unsigned tok_bytes = a.token_stride;
+  unsigned voff[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int ci = 8 * i + wave;
+    const int pos = 64 * (ci % kParts) + (threadIdx.x & 63);
+    voff[i] = L::token_of(pos) * tok_bytes + (hgrp * 4 + (ci / kParts) % 4) * a.head_stride +
+              16 * L::chunk_of(pos);
+  }
+
+  for_each_piece<D>(a, item, [&](const ItemRange& it, const int (&first_id)[D]) {
+  const int tid = piece_tid();
+  const int lane = tid & 63;
+  const int g16 = lane >> 4;
+  const int l16 = lane & 15;
   const int b = max(it.b, 0);
   const int len = it.len;
   const int p_begin = it.p_begin;
@@ -1249,7 +1292,7 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   if (it.b < 0) return;  // uniform
   const bool direct = it.n_valid <= 1;
   const size_t slot = (size_t)it.slot0 + it.split;
-  if (p_begin >= p_end && !single) {
+  if (p_begin >= p_end && !single) {  // fixed plan only
     write_empty_split<NB>(a, map, slot, it.n_valid == 1 ? -1.f : 0.f);
     return;  // uniform
   }
@@ -1273,34 +1316,15 @@ void sqa_partial_lds_kernel(PartialArgs a) {
     }
     dbits[nb] = draft_bits(a, b, qi, real);
   }
-  static_assert(D + 1 <= kIdPad, "page-id table padding must cover the ring's look-ahead");
-  constexpr int kIdSlots = (kMaxSplitPages + kIdPad + kThreads - 1) / kThreads;
   int idreg[kIdSlots];
   const int last_id = n_split > 0 ? n_split - 1 : 0;
 #pragma unroll
   for (int k = 0; k < kIdSlots; ++k) {
-    const int i = threadIdx.x + k * kThreads;
+    const int i = tid + k * kThreads;
     const int x = bt_row[(p_begin + min(i, last_id)) >> shift];
     idreg[k] = i < n_split ? x : -1;
   }
 
-  // The ring and, after the loop, the waves' output staging.
-  __shared__ __attribute__((aligned(16))) char sm_ring[D * kSlot];
-  __shared__ int sm_ids[kIdSlots * kThreads];
-  // Load i of a thread fills 1 KiB piece ci = 8 i + wave of a slot: K (first
-  // half of the pieces) or V, head slot (ci / parts) % 4, part ci % parts of the
-  // head's slice; lane l fills position 64 part + l, i.e. chunk
-  // L::chunk_of(position) of token L::token_of(position).
-  constexpr int kParts = kHeadSlice / 1024;  // 1 KiB pieces per head slice
-  const unsigned tok_bytes = a.token_stride;
-  unsigned voff[kLoads];
-#pragma unroll
-  for (int i = 0; i < kLoads; ++i) {
-    const int ci = 8 * i + wave;
-    const int pos = 64 * (ci % kParts) + lane;
-    voff[i] = L::token_of(pos) * tok_bytes + (hgrp * 4 + (ci / kParts) % 4) * a.head_stride +
-              16 * L::chunk_of(pos);
-  }
   const size_t sub_bytes = (size_t)kPageSize * tok_bytes;
   auto issue_page = [&](int pid, int p, int j) {
     // The page is the same for the whole workgroup: its resource lives in SGPRs.
@@ -1322,7 +1346,7 @@ void sqa_partial_lds_kernel(PartialArgs a) {
     issue_page(j < n_split ? clamp_page(first_id[j], a.num_pages) : -1, p_begin + j, j);
 #pragma unroll
   for (int k = 0; k < kIdSlots; ++k) {
-    const int i = threadIdx.x + k * kThreads;
+    const int i = tid + k * kThreads;
     sm_ids[i] = idreg[k] >= 0 ? clamp_page(idreg[k], a.num_pages) : -1;
   }
   const int mask_from = len - a.q_len;
@@ -1370,13 +1394,14 @@ void sqa_partial_lds_kernel(PartialArgs a) {
       }
     }
   }
-  // Loads past the split still write (zeros) into the ring: drain them before
+  // Loads past the piece still write (zeros) into the ring: drain them before
   // the ring becomes the output staging.
   wait_vmcnt<0>();
   __syncthreads();
-  if (!active) return;
-  write_results<NB, HD, E>(a, st, (float*)sm_ring + wave * 16 * (HD + 4), map, direct,
-                           !single && !balanced, b, slot);
+  if (active)
+    write_results<NB, HD, E>(a, st, (float*)sm_ring + wave * 16 * (HD + 4), map, direct,
+                             !single && !balanced, b, slot);
+  });
 }
 
 // Log-sum-exp merge of split partials (reference: csrc/small_q_attention_ext.cu:339-366):
@@ -1415,7 +1440,8 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   // sequence, no length needed (splits past its pages hold l = 0, and l = -1
   // in split 0 says the partial kernel already wrote the row). Balanced plan:
   // the (first slot, count) table the partial kernel wrote; when every
-  // sequence was expected to span spec_pages pages, the uniform layout is
+  // sequence was expected to span spec_pages pages, the layout of that case
+  // (sequence b's pages from b * spec_pages on, items of spec_pps pages) is
   // assumed while the table is read, and the row is merged again from the
   // table if the two differ.
   const bool balanced = is_balanced(a.pages_per_split);
@@ -1425,8 +1451,10 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   int n_valid, slot0;
   SeqSplits table = {0, 0};
   if (expect) {
-    n_valid = a.spec_splits;
-    slot0 = b * n_valid;
+    const int start = b * a.spec_pages;
+    const int i0 = start / a.spec_pps;
+    n_valid = (start + a.spec_pages - 1) / a.spec_pps - i0 + 1;
+    slot0 = i0 + b;
   } else if (balanced) {
     table = a.seq_splits[b];
     n_valid = table.count;
@@ -1634,7 +1662,12 @@ void launch_merge_as(const MergeArgs& a, int per_row, hipStream_t stream) {
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
   const LaunchShape sh = launch_shape(a.rows, a.hkv, a.head_dim);
   const int head_groups = (a.hkv + sh.heads - 1) / sh.heads;
-  const dim3 grid((unsigned)(plan_slots(a.batch, a.num_splits, a.pages_per_split) * head_groups));
+  // Work items: fixed plan, one per slot; balanced, num_splits - batch (a
+  // sequence's share of the spare slots comes from the item it ends in).
+  const long long items = is_balanced(a.pages_per_split)
+                              ? (long long)(a.num_splits - a.batch)
+                              : (long long)a.batch * a.num_splits;
+  const dim3 grid((unsigned)(items * head_groups));
   const dim3 block(sh.waves() * 64);
   if (a.bf16) {
     if (a.kv_fp8)
@@ -1652,9 +1685,10 @@ hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
 
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream) {
   // The balanced plan's split count per sequence is known only on the
-  // device: use the batch average.
+  // device: use the batch average (items / batch, plus the piece a sequence
+  // may start inside an item).
   const int per_row = is_balanced(a.pages_per_split)
-                          ? (a.num_splits - a.batch + a.batch - 1) / a.batch
+                          ? (a.num_splits - a.batch + a.batch - 1) / a.batch + 1
                           : a.num_splits;
   if (a.bf16)
     launch_merge_as<ElemBF16>(a, per_row, stream);

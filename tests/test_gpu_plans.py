@@ -105,3 +105,70 @@ def test_fixed_plan_merge_markers(q_len):
         out, ws = _run(tensors, ns, pps, ws=ws)
         assert torch.isfinite(out.float()).all(), lens
         assert_parity(out, _oracle(tensors), label=f"fixed q{q_len} run {i}")
+
+
+def _plan_table(ws, tensors, ns):
+    """The (first slot, count) table the partial kernel leaves in the workspace
+    behind the partial sums and (max, sum) pairs of every slot."""
+    q, k = tensors[0], tensors[1]
+    batch, q_len, hq, hd = q.shape
+    hkv = k.shape[2]
+    items = ns * hkv * q_len * (hq // hkv)
+    off = items * (hd + 2)
+    return ws[off:off + 2 * batch].view(torch.int32).view(batch, 2).cpu().tolist()
+
+
+def _packed_layout(lens, items, page=16):
+    """Brute force from the plan's definition: pages laid end to end in batch order,
+    cut into items of P = clamp(ceil(total / items), 4, 2048) pages; the part of
+    item i in sequence b goes to slot i + b. Returns P and each sequence's slots."""
+    pages = [(n + page - 1) // page for n in lens]
+    total = sum(pages)
+    P = min(max(-(-total // items), 4), 2048)
+    slots, g = [], 0
+    for b, n in enumerate(pages):
+        slots.append(sorted({(g + j) // P + b for j in range(n)}))
+        g += n
+    return P, slots
+
+
+@pytest.mark.parametrize("q_len", [4, 8, 16])
+def test_packed_items_cross_sequences(q_len):
+    """Balanced plans with few work items: items span the ends of many sequences
+    (dozens of pieces in one workgroup when there are one or two items), sequences
+    inside one piece go straight to the output, empty ones are zeros. The table the
+    merge reads must match the plan's definition, slots must be distinct and below
+    num_splits, and the output must match the oracle; with an expected page count
+    (every sequence the same length) the bits must equal the plain plan's."""
+    g = torch.Generator().manual_seed(1400 + q_len)
+    lens = torch.randint(0, 700, (40,), generator=g).tolist()
+    lens[3] = lens[17] = 0
+    lens[5], lens[6] = 1, 16
+    ragged = _gpu(inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=1410 + q_len))
+    ref = _oracle(ragged)
+    for n_items in (1, 2, 3, 7, 64):
+        ns = len(lens) + n_items
+        out, ws = _run(ragged, ns, 0)
+        assert_parity(out, ref, label=f"ragged items {n_items} q{q_len}")
+        assert torch.all(out[3] == 0) and torch.all(out[17] == 0)
+        _, slots = _packed_layout(lens, n_items)
+        table = _plan_table(ws, ragged, ns)
+        used = []
+        for b, (first, count) in enumerate(table):
+            assert count == len(slots[b]), (n_items, b)
+            if count:
+                assert list(range(first, first + count)) == slots[b], (n_items, b)
+                used += slots[b]
+        assert len(used) == len(set(used)) and max(used) < ns
+
+    same = [333] * 9
+    uni = _gpu(inputs.Case(batch=len(same), q_len=q_len, seq_lens=same, seed=1420 + q_len))
+    pages = (333 + 15) // 16
+    for n_items in (1, 2, 4, 5):
+        ns = len(same) + n_items
+        spec, ws = _run(uni, ns, -pages)
+        plain, _ = _run(uni, ns, 0)
+        assert torch.equal(spec, plain), n_items
+        _, slots = _packed_layout(same, n_items)
+        assert [list(range(f, f + c)) for f, c in _plan_table(ws, uni, ns)] == slots
+        assert_parity(spec, _oracle(uni), label=f"uniform items {n_items} q{q_len}")
