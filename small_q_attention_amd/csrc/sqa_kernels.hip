@@ -607,7 +607,10 @@ __device__ __forceinline__ void packed_plan(const PartialArgs& a, PackedBatch& p
     pb.start[k] = base + wave_exclusive_scan_int(pages[k]);
     base += wave_sum_int(pages[k]);
   }
-  pb.total = base;
+  // Wave sums are the same in every lane; readfirstlane says so to the
+  // compiler, which keeps the loop over pieces (and the page ids loaded in it)
+  // uniform rather than wrapping each buffer load in a waterfall loop.
+  pb.total = __builtin_amdgcn_readfirstlane(base);
   pb.P = packed_item_pages(pb.total, a.num_splits - a.batch);
   if (write_table && threadIdx.x < 64) {
 #pragma unroll
@@ -758,11 +761,7 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
     g_end = min(g + pb.P, pb.total);
   }
   for (bool first = true; g < g_end; first = false) {  // uniform
-    if (balanced) {
-      it = packed_piece(a, pb, item, g);
-      if (!ids_loaded) load_first_ids(it.b, it.p_begin);
-    }
-    ids_loaded = false;
+    if (balanced) it = packed_piece(a, pb, item, g);
     it.b = __builtin_amdgcn_readfirstlane(it.b);
     it.split = __builtin_amdgcn_readfirstlane(it.split);
     it.p_begin = __builtin_amdgcn_readfirstlane(it.p_begin);
@@ -770,6 +769,10 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
     it.len = __builtin_amdgcn_readfirstlane(it.len);
     it.n_valid = __builtin_amdgcn_readfirstlane(it.n_valid);
     it.slot0 = __builtin_amdgcn_readfirstlane(it.slot0);
+    // Uniform addresses (the fields above) make the ids uniform values: the
+    // buffer resources built from them stay in scalar registers.
+    if (!ids_loaded) load_first_ids(it.b, it.p_begin);
+    ids_loaded = false;
     if (!first) __syncthreads();  // the previous piece is done with the LDS
     piece(it, first_id);
     g += balanced ? it.p_end - it.p_begin : 1;
@@ -1024,6 +1027,8 @@ void sqa_partial_kernel(PartialArgs a) {
   // block_tables[b][p >> shift].
   const size_t sub_bytes = (size_t)kPageSize * tok_bytes;
   auto load_page = [&](int pid, int p, typename KV::Regs (&pg)[HPW]) {
+    // The page is the same for the whole wave: its resource lives in SGPRs.
+    pid = __builtin_amdgcn_readfirstlane(pid);
     const size_t off =
         pid >= 0 ? (size_t)pid * (size_t)a.page_stride + (size_t)(p & sub_mask) * sub_bytes : 0;
     const int nrec = pid >= 0 ? (int)a.page_extent : 0;
