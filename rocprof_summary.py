@@ -1,6 +1,6 @@
 """Summarises rocprofv3 CSV output of ``bench.py`` into the text kept under ``profiles/``.
 
-    python -m small_q_attention_amd.rocprof_summary --trace DIR --fetch DIR \\
+    python rocprof_summary.py --trace DIR --fetch DIR \\
         --write DIR [--mfma DIR] --kv-bytes N --command "..." --out profiles/FILE.txt
 
 Inputs are the directories rocprofv3 wrote with ``--output-format csv``:
@@ -33,7 +33,7 @@ def _one(pattern):
 
 
 def _short(name):
-    name = name.replace("void ", "").replace("sqa::(anonymous namespace)::", "")
+    name = name.replace("void ", "").replace("sqa::", "").replace("(anonymous namespace)::", "")
     return name.split("(")[0]
 
 
