@@ -1689,11 +1689,13 @@ hipError_t launch_partial(const PartialArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream) {
-  // The balanced plan's split count per sequence is known only on the
-  // device: use the batch average (items / batch, plus the piece a sequence
-  // may start inside an item).
+  // Splits per sequence, for the choice of merge variant: a fixed plan's
+  // num_splits; the balanced plan's count per sequence is known only on the
+  // device: the batch average, items / batch. It depends on the slot count
+  // alone, so the plain balanced plan and the one with an expected page count
+  // merge with the same variant (and give the same bits).
   const int per_row = is_balanced(a.pages_per_split)
-                          ? (a.num_splits - a.batch + a.batch - 1) / a.batch + 1
+                          ? (a.num_splits - a.batch + a.batch - 1) / a.batch
                           : a.num_splits;
   if (a.bf16)
     launch_merge_as<ElemBF16>(a, per_row, stream);
