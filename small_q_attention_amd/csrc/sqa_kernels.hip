@@ -627,13 +627,11 @@ __device__ __forceinline__ void packed_plan(const PartialArgs& a, PackedBatch& p
 
 // The piece of item `item` that holds global page g (g inside the item): its
 // sequence, page range (within the sequence), length, split count and slot.
+// The wave finds the lane holding that sequence with one ballot per sequence
+// slot; everything after is scalar.
 __device__ __forceinline__ ItemRange packed_piece(const PartialArgs& a, const PackedBatch& pb,
                                                  int item, int g) {
-  ItemRange r;
-  r.b = -1;
-  r.split = 0;
-  r.p_begin = r.p_end = r.len = r.n_valid = r.slot0 = 0;
-  const int g_end = min((item + 1) * pb.P, pb.total);
+  int b = -1, st = 0, len = 0;
 #pragma unroll
   for (int k = 0; k < kSeqPerLane; ++k) {
     // Lengths are 0 past the batch: those slots have no pages.
@@ -641,15 +639,21 @@ __device__ __forceinline__ ItemRange packed_piece(const PartialArgs& a, const Pa
     const unsigned long long hit = __ballot(mine);
     if (hit) {
       const int src = __builtin_ctzll(hit);
-      r.len = __shfl(pb.len[k], src);
-      const int st = __shfl(pb.start[k], src), np = pages_of(a, r.len);
-      r.b = 64 * k + src;
-      r.p_begin = g - st;
-      r.p_end = min(g_end, st + np) - st;
-      r.n_valid = (st + np - 1) / pb.P - st / pb.P + 1;
-      r.slot0 = item + r.b;
+      b = 64 * k + src;
+      st = __builtin_amdgcn_readfirstlane(__shfl(pb.start[k], src));
+      len = __builtin_amdgcn_readfirstlane(__shfl(pb.len[k], src));
     }
   }
+  ItemRange r;
+  const int np = pages_of(a, len);
+  const int g_end = min((item + 1) * pb.P, pb.total);
+  r.b = b;
+  r.split = 0;
+  r.len = len;
+  r.p_begin = g - st;
+  r.p_end = min(g_end, st + np) - st;
+  r.n_valid = (st + np - 1) / pb.P - st / pb.P + 1;
+  r.slot0 = item + b;
   return r;
 }
 
@@ -760,6 +764,10 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
     g = item * pb.P;
     g_end = min(g + pb.P, pb.total);
   }
+  // The same in every lane (readfirstlane tells the compiler, which otherwise
+  // runs the loop under an exec mask).
+  g = __builtin_amdgcn_readfirstlane(g);
+  g_end = __builtin_amdgcn_readfirstlane(g_end);
   for (bool first = true; g < g_end; first = false) {  // uniform
     if (balanced) it = packed_piece(a, pb, item, g);
     it.b = __builtin_amdgcn_readfirstlane(it.b);
@@ -775,7 +783,7 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
     ids_loaded = false;
     if (!first) __syncthreads();  // the previous piece is done with the LDS
     piece(it, first_id);
-    g += balanced ? it.p_end - it.p_begin : 1;
+    g = __builtin_amdgcn_readfirstlane(g + (balanced ? it.p_end - it.p_begin : 1));
   }
 }
 
