@@ -172,3 +172,57 @@ def test_packed_items_cross_sequences(q_len):
         _, slots = _packed_layout(same, n_items)
         assert [list(range(f, f + c)) for f, c in _plan_table(ws, uni, ns)] == slots
         assert_parity(spec, _oracle(uni), label=f"uniform items {n_items} q{q_len}")
+
+
+@pytest.mark.parametrize("qdt,fp8,layout,page,tree,q_len", [
+    (torch.bfloat16, False, "HND", 64, True, 8),
+    (torch.float16, True, "NHD", 32, True, 16),
+    (torch.bfloat16, True, "HND", 256, False, 4),
+    (torch.float16, False, "NHD", 128, True, 5),
+])
+def test_packed_items_through_the_general_entry(qdt, fp8, layout, page, tree, q_len):
+    """Items crossing many sequence ends with the general entry's options: bf16
+    queries, e4m3 caches, interleaved NHD / HND caches, cache pages of 32 to 256
+    tokens (item boundaries inside a cache page) and tree masks (every piece reads
+    its own sequence's mask rows), at 1, 3 and 16 work items."""
+    from small_q_attention_amd.masks import as_words, pack_draft_mask
+
+    f8 = torch.float8_e4m3fn
+    g = torch.Generator().manual_seed(1500 + page + q_len)
+    lens = [q_len + int(x) for x in torch.randint(0, 900, (23,), generator=g)]
+    lens[4] = q_len
+    case = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=1510 + page,
+                       page_size=page)
+    q, k, v, bt, sl = inputs.make_inputs(case)
+    q = q.to(qdt)
+    if fp8:
+        k, v = k.to(f8), v.to(f8)
+        kv = torch.stack([k.view(torch.uint8), v.view(torch.uint8)], 1).view(f8)
+    else:
+        k, v = k.to(qdt), v.to(qdt)
+        kv = torch.stack([k, v], 1)
+    if layout == "HND":
+        kv = kv.permute(0, 1, 3, 2, 4).contiguous()
+        kview, vview = kv[:, 0].transpose(1, 2), kv[:, 1].transpose(1, 2)
+    else:
+        kv = kv.contiguous()
+        kview, vview = kv[:, 0], kv[:, 1]
+    kview, vview = kview.cuda(), vview.cuda()
+    mask = words = None
+    if tree:
+        vis = torch.rand(len(lens), q_len, q_len, generator=g) < 0.4
+        vis[:, torch.arange(q_len), torch.arange(q_len)] = True
+        mask = pack_draft_mask(vis)
+        words = as_words(mask, len(lens), q_len).cuda()
+    ref = attention_c64(q, k, v, bt, sl, page, 8, draft_mask=mask)
+    qd, btd, sld = q.cuda(), bt.cuda(), sl.cuda()
+    for n_items in (1, 3, 16):
+        ns = len(lens) + n_items
+        nbytes = _lib.workspace_bytes(len(lens), q_len, 32, 8, 128, ns, 0)
+        ws = torch.full((nbytes // 4,), float("nan"), dtype=torch.float32, device="cuda")
+        out = torch.full_like(qd, float("nan"))
+        _lib.launch_general(qd, out, kview, vview, btd, sld, words, 128 ** -0.5, 1.0, ns, 0, ws,
+                            torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert_parity(out, ref, label=f"{qdt} fp8={fp8} {layout} page{page} tree={tree} "
+                                      f"q{q_len} items {n_items}")
