@@ -50,17 +50,6 @@ const char* sqa_last_error(void) { return g_last_error.c_str(); }
 #endif
 const char* sqa_version(void) { return "sqa 0.2.0 gfx950 sqa-src-hash:" SQA_SOURCE_HASH; }
 
-int sqa_read_probe(const void* data, size_t bytes, unsigned* sink, int blocks, void* stream) {
-  if (!data || !sink) return fail(SQA_ERR_INVALID, "null pointer");
-  if (blocks < 1 || blocks > 65536) return fail(SQA_ERR_INVALID, "blocks must be 1..65536");
-  if ((uintptr_t)data % 16 || (uintptr_t)sink % 4)
-    return fail(SQA_ERR_INVALID, "data must be 16-byte and sink 4-byte aligned");
-  if (bytes == 0 || bytes % (16 * (size_t)blocks))
-    return fail(SQA_ERR_INVALID, "bytes must be a positive multiple of 16 * blocks");
-  hipError_t e = sqa::launch_read_probe(data, bytes, sink, blocks, (hipStream_t)stream);
-  return e == hipSuccess ? SQA_OK : hip_fail(e, "read probe launch");
-}
-
 int sqa_device_cu_count(int device) {
   std::lock_guard<std::mutex> lock(g_cu_mutex);
   if (device < 0) return -1;

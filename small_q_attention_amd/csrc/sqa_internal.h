@@ -58,7 +58,9 @@ struct PartialArgs {
   const int32_t* seq_lens;      // [B]
   const uint32_t* draft_mask;   // NULL (causal draft chain) or [B, Q, mask_words]
   _Float16* out;              // [B, Q, Hq, head_dim]; written directly when num_splits == 1
-  float* part_o;              // [slots, Hkv, rows, head_dim] unnormalised sums
+  float* part_o;              // [slots, Hkv, rows, head_dim]: fp32 unnormalised sums, or for
+                              // fp16 outputs fp16 rows divided by their sum (the first half
+                              // of the same region)
   float* part_ml;             // [slots, Hkv, rows, 2] (max in log2 units, sum)
   SeqSplits* seq_splits;      // [B] (balanced plan only)
   long long num_pages;        // pages in the cache pool; ids outside are clamped to 0
@@ -159,9 +161,5 @@ inline LaunchShape launch_shape(int rows, int hkv, int head_dim) {
 
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream);
 hipError_t launch_merge(const MergeArgs& a, hipStream_t stream);
-// Streaming read of `bytes` (a multiple of 16 * blocks) in `blocks` contiguous
-// chunks, one dword per thread (blocks * 256) written to `sink`.
-hipError_t launch_read_probe(const void* data, size_t bytes, unsigned* sink, int blocks,
-                             hipStream_t stream);
 
 }  // namespace sqa

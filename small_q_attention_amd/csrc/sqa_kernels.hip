@@ -55,6 +55,10 @@ typedef __bf16 b4 __attribute__((ext_vector_type(4)));
 // Element types of Q, K, V and the output. Operands travel as raw 16-bit
 // lanes (u4 = 8 elements, u2 = 4); the traits pick the MFMA and the rounding.
 struct ElemF16 {
+  // Split partials leave as fp16 rows normalised by their sum (a convex
+  // combination of V rows, so within V's fp16 range), with (max, sum) in fp32:
+  // half the partial bytes written and merged.
+  static constexpr bool kHalfPartials = true;
   // S^T += K . Q^T over 32 head dims.
   static __device__ __forceinline__ f4 mma_qk(u4 k, u4 q, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, k),
@@ -107,6 +111,9 @@ struct ElemF16 {
 };
 
 struct ElemBF16 {
+  // bf16 V can exceed fp16's range and bf16's 8 bits would cost accuracy:
+  // partials stay unnormalised fp32.
+  static constexpr bool kHalfPartials = false;
   // One bf16 P (relative error 2^-9) would cost up to ~1% on rows that average
   // a few keys; P goes in as hi + lo bf16 parts (~2^-17), both in one PV
   // product.
@@ -835,8 +842,8 @@ __device__ __forceinline__ void write_results(const PartialArgs& a, WaveState<NB
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     if (map.row(nb, 0) >= a.rows) break;  // uniform
-    const float inv = st.l[nb] > 0.f ? a.out_scale / st.l[nb] : 0.f;
-    const float sc = direct ? inv : 1.f;
+    const float inv_l = st.l[nb] > 0.f ? 1.f / st.l[nb] : 0.f;
+    const float sc = direct ? a.out_scale * inv_l : (E::kHalfPartials ? inv_l : 1.f);
     if (map.real(nb, l16)) {
       float* dst = stage + l16 * kStageRow + (HD / 4) * g16;
 #pragma unroll
@@ -886,8 +893,15 @@ __device__ __forceinline__ void write_results(const PartialArgs& a, WaveState<NB
       for (int i = 0; i < CPR / 4; ++i) {
         const int e = i * 64 + lane;
         const int rs = e / CPR;
-        if (map.real(nb, rs))
-          *(f4*)(a.part_o + (item_of(nb, rs) + map.row(nb, rs)) * HD + 4 * (e % CPR)) = v[i];
+        if (map.real(nb, rs)) {
+          const size_t at = (item_of(nb, rs) + map.row(nb, rs)) * HD + 4 * (e % CPR);
+          if constexpr (E::kHalfPartials) {
+            const float o[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
+            *(u2*)((_Float16*)a.part_o + at) = E::pack4(o);
+          } else {
+            *(f4*)(a.part_o + at) = v[i];
+          }
+        }
       }
       if (g16 == 0 && map.real(nb, l16)) {
         const size_t pitem = item_of(nb, l16) + map.row(nb, l16);
@@ -1420,6 +1434,7 @@ void sqa_partial_lds_kernel(PartialArgs a) {
 // Log-sum-exp merge of split partials (reference: csrc/small_q_attention_ext.cu:339-366):
 // M = max_s m_s; O = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M); splits
 // with l_s <= 0 are skipped and a row with no visible key is written as 0.
+// fp16 partials hold acc_s / l_s (so acc_s = l_s times the stored row).
 //
 // One pass, every load of a round in flight at once: TPR threads serve one
 // output row; thread t owns 4 dims (chunk t % (HD/4)) and the splits
@@ -1487,12 +1502,17 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   // row again, weight 0), so rounds need no branch around their loads.
   auto load_round = [&](int s0, int nv, int sb) {
     const float* ml = a.part_ml + ((size_t)s0 * stride + row_item) * 2;
-    const float* po = a.part_o + ((size_t)s0 * stride + row_item) * HD + 4 * c;
+    const size_t o0 = ((size_t)s0 * stride + row_item) * HD + 4 * c;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int sp = sb + u * SG;
       const size_t it = (size_t)(sp < nv ? sp : 0) * stride;
-      o[u] = *(const f4*)(po + it * HD);
+      if constexpr (E::kHalfPartials) {
+        const h4 x = __builtin_bit_cast(h4, *(const u2*)((const _Float16*)a.part_o + o0 + it * HD));
+        o[u] = f4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+      } else {
+        o[u] = *(const f4*)(a.part_o + o0 + it * HD);
+      }
       m[u] = ml[it * 2];
       l[u] = ml[it * 2 + 1];
       if (sp >= nv) l[u] = 0.f;
@@ -1514,8 +1534,10 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
         const bool use = l[u] > 0.f;
         const float w = use ? fast_exp2(m[u] - nm) : 0.f;
         den += w * l[u];
+        // Normalised partials weigh in with their sum.
+        const float wo = E::kHalfPartials ? w * l[u] : w;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = use ? fmaf(w, o[u][i], acc[i]) : acc[i];
+        for (int i = 0; i < 4; ++i) acc[i] = use ? fmaf(wo, o[u][i], acc[i]) : acc[i];
       }
       mt = nm;
     }
