@@ -50,9 +50,10 @@ extern "C" {
  *     [s * pages_per_split, (s + 1) * pages_per_split).
  *   chunk_keys == 0: automatic, sized from the device's compute-unit count.
  *     For 2 <= batch <= 256 this is the balanced plan, *pages_per_split <= 0:
- *     *num_splits work-item slots are shared by the whole batch and the kernel
- *     sizes the splits on the device from the sum of seq_lens, so ragged
- *     batches spread evenly over the chip without a host sync. With
+ *     *num_splits slots are shared by the whole batch; on the device the
+ *     kernel lays all sequences' pages end to end (from seq_lens) and cuts them
+ *     into num_splits - batch equal work items that cross sequence ends, so
+ *     ragged batches spread evenly over the chip without a host sync. With
  *     max_seq_len > 0 it is -P, P = ceil(max_seq_len / 16) (at most max_pages):
  *     the kernels first assume every sequence spans P pages, which saves a
  *     memory round trip when it holds, and verify it (the result is the same
@@ -62,7 +63,7 @@ extern "C" {
  * max_seq_len <= 0 means "unknown": a fixed plan covers max_pages * 16 tokens.
  * head_dim: as passed to the attention call (it sets the kernel's heads per
  * workgroup, hence the split count of the automatic plans).
- * Writes *num_splits >= 1 and *pages_per_split >= 0.
+ * Writes *num_splits >= 1 and *pages_per_split (> 0 fixed plan, 0 or -P balanced).
  */
 int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int num_kv_heads,
                     int head_dim, int max_seq_len, int max_pages, int chunk_keys,
@@ -208,17 +209,6 @@ typedef struct sqa_attention_args {
  * Same plan, workspace, status codes and asynchrony as sqa_paged_mtp_attention.
  */
 int sqa_paged_attention(const sqa_attention_args* args);
-
-/*
- * Streaming-read probe. No counterpart in the reference: a measurement aid that
- * gives the practical HBM read rate the attention kernels are compared with.
- * Reads the `bytes` bytes at `data` once (`blocks` workgroups of 256 threads,
- * each over one contiguous chunk, 16-byte non-temporal loads) and writes one
- * dword per thread to `sink` (blocks * 256 dwords). `data` 16-byte aligned,
- * `bytes` a positive multiple of 16 * blocks, 1 <= blocks <= 65536, `sink` 4-byte
- * aligned. Asynchronous on `stream`; SQA_ERR_INVALID or SQA_ERR_HIP otherwise.
- */
-int sqa_read_probe(const void* data, size_t bytes, unsigned* sink, int blocks, void* stream);
 
 /* Compute units of `device` (256 on MI355X), or -1 on error. */
 int sqa_device_cu_count(int device);
