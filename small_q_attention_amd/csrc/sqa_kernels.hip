@@ -177,12 +177,6 @@ __device__ __forceinline__ float xor_max(float x) {
   return fmaxf(x, __shfl_xor(x, 32));
 }
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
-
 __device__ __forceinline__ float xor_sum(float x) {
   x += __shfl_xor(x, 16);
   return x + __shfl_xor(x, 32);
