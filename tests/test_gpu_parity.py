@@ -114,9 +114,9 @@ def test_ragged_batch_on_scattered_pool(q_len):
 @pytest.mark.parametrize("q_len", [2, 8, 16])
 def test_balanced_plan_on_a_skewed_batch(q_len):
     """The automatic plan for 2..256 sequences (pages_per_split 0): one long sequence
-    among empty, tiny and short ones. Splits are sized on the device from the sum of
-    seq_lens; sequences with one split are written by the partial kernel, the rest by
-    the merge, sequences without pages as zeros."""
+    among empty, tiny and short ones. The batch's pages are cut into equal work items
+    on the device from seq_lens; sequences inside one item are written by the partial
+    kernel, the rest by the merge, sequences without pages as zeros."""
     lens = [0, 1, q_len - 1, q_len, 16, 17, 200, 37000, 5, 0, 900, 4096]
     case = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=400 + q_len)
     tensors = _to_gpu(inputs.make_inputs(case))
