@@ -14,9 +14,10 @@ are appended to ``--output`` as they complete. Added columns:
   after ~0.1 s of back-to-back calls (clocks settled);
 * ``kv_bytes``, ``kv_GBps`` and ``pct_peak`` (KV bytes over ``kernel_p50_us``),
   ``call_GBps`` (over ``p50_us``), ``num_splits``, ``pages_per_split``;
-* ``pools``: KV sets smaller than the 256 MB MALL are rotated through this many
-  distinct pools (together at least twice the MALL) so repeats do not read from
-  the cache (``mall_resident`` says whether one pool alone would fit);
+* ``pools``: cases whose calls read less KV than twice the 256 MB MALL rotate
+  through this many distinct pools (their reads together at least twice the
+  MALL) so repeats do not read from the cache (``mall_resident`` says whether
+  one call's KV alone would fit);
 * ``b2b_us``: mean time per call over ``repeats`` calls issued back to back
   through the C ABI (events only around the batch of calls), rotating the
   pools: what a decode loop sees, without the per-call synchronisation of
@@ -112,10 +113,13 @@ def measure_case(torch, variant, case, page_mode, chunk_keys, warmup, repeats, s
 
     c = inputs.uniform_case(case["batch_size"], case["q_len"], case["kv_len"], page_mode=page_mode,
                             seed=seed)
-    pool_bytes = 2 * inputs.pool_pages_for(c) * c.page_size * c.num_kv_heads * c.head_dim * 2
+    # KV bytes one call reads (its pool holds twice the pages); sets that read
+    # less than twice the MALL rotate, so no call finds its pages cached by
+    # the call before.
+    read_bytes = inputs.kv_bytes(c.seq_lens, c.num_kv_heads, c.head_dim)
     pools = 1
-    if pool_bytes < MALL_BYTES:
-        pools = min(max_pools, max(2, -(-2 * MALL_BYTES // pool_bytes)))
+    if read_bytes < 2 * MALL_BYTES:
+        pools = min(max_pools, max(2, -(-2 * MALL_BYTES // read_bytes)))
     sets = []
     for i in range(pools):
         c.seed = seed + 7919 * i
@@ -180,7 +184,7 @@ def measure_case(torch, variant, case, page_mode, chunk_keys, warmup, repeats, s
         "pct_peak": 100.0 * kvb / (kern * 1e-6) / 1e9 / PEAK_HBM_GBPS,
         "call_GBps": kvb / (p50 * 1e-6) / 1e9,
         "num_splits": ns, "pages_per_split": pps, "pools": pools,
-        "mall_resident": pool_bytes / 2 <= MALL_BYTES,
+        "mall_resident": read_bytes <= MALL_BYTES,
     }
     if check:
         row.update(check_case(torch, forward, sets[0], page, c.num_kv_heads))
