@@ -226,3 +226,18 @@ def test_packed_items_through_the_general_entry(qdt, fp8, layout, page, tree, q_
         torch.cuda.synchronize()
         assert_parity(out, ref, label=f"{qdt} fp8={fp8} {layout} page{page} tree={tree} "
                                       f"q{q_len} items {n_items}")
+
+
+def test_balanced_plan_with_no_pages_at_all():
+    """Every sequence empty: no work item has a piece, the table counts are all 0
+    and the merge writes zeros over a NaN output and workspace (plain plan and the
+    expected-page one, whose expectation fails)."""
+    lens = [0] * 5
+    tensors = _gpu(inputs.Case(batch=5, q_len=4, seq_lens=[16] * 5, seed=1600))
+    q, k, v, bt, _ = tensors
+    sl = torch.zeros(5, dtype=torch.int32, device="cuda")
+    for pps in (0, -1):
+        ns = 5 + 7
+        out, ws = _run((q, k, v, bt, sl), ns, pps)
+        assert torch.all(out == 0), pps
+        assert [c for _, c in _plan_table(ws, (q, k, v, bt, sl), ns)] == [0] * len(lens)
