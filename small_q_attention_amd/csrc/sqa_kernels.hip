@@ -569,10 +569,10 @@ __device__ __forceinline__ int wave_inclusive_scan_int(int v) {
 // order, each next piece has the next item or the next sequence and neither
 // index ever falls, so i + b grows strictly). Sequence b thus owns slots
 // [i0_b + b, i1_b + b], i0_b = start_b / P, i1_b = (start_b + pages_b - 1) / P;
-// a sequence inside one item is finished by the partial kernel. Lane l holds sequences l, l + 64, l + 128, l + 192:
-// every wave derives the plan on its own with wave reductions (no LDS, no
-// barrier), and wave 0 of workgroup 0 writes each sequence's (first slot,
-// count) for the merge kernel.
+// a sequence inside one item is finished by the partial kernel. Lane l holds
+// sequences l, l + 64, l + 128, l + 192: every wave derives the plan on its own
+// with wave reductions (no LDS, no barrier), and wave 0 of workgroup 0 writes
+// each sequence's (first slot, count) for the merge kernel.
 constexpr int kSeqPerLane = kMaxBalancedBatch / 64;
 
 // The per-lane view of the batch a packed plan works from (lane l: sequences
@@ -778,6 +778,9 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
     it.len = __builtin_amdgcn_readfirstlane(it.len);
     it.n_valid = __builtin_amdgcn_readfirstlane(it.n_valid);
     it.slot0 = __builtin_amdgcn_readfirstlane(it.slot0);
+    // Every page of [0, total) lies in some sequence, so a piece always has one
+    // and at least one page; the check keeps the loop finite whatever the inputs.
+    if (balanced && (it.b < 0 || it.p_end <= it.p_begin)) break;
     // Uniform addresses (the fields above) make the ids uniform values: the
     // buffer resources built from them stay in scalar registers.
     if (!ids_loaded) load_first_ids(it.b, it.p_begin);
