@@ -12,8 +12,8 @@ mean duration from HIP events the library records around it on the launch
 stream; ``cpu_baseline`` times the loop-faithful CPU oracle on a bounded
 sample of the same workload. ``per_q_len`` repeats the timing at q_len 2, 4
 and 16 on the same KV pool. ``roofline.read_probe`` is the practical read
-ceiling: the library's streaming-read probe over ~2 GiB of the same resident
-pool (``frac_of_read_probe`` = the partial kernel's rate over it).
+ceiling: the streaming-read probe (``read_probe.hip``) over ~2 GiB of the same
+resident pool (``frac_of_read_probe`` = the partial kernel's rate over it).
 """
 
 from __future__ import annotations
@@ -184,9 +184,13 @@ def time_calls(torch, lib, sets, plan, steps, warmup):
 
 
 def read_probe(torch, lib, pool, steps):
-    """The practical HBM read ceiling: ``sqa_read_probe`` (one workgroup per CU,
-    contiguous chunks, 16-byte non-temporal loads) over the first ~2 GiB of the
-    resident K pool, `steps` passes between two events. Returns (GB/s, bytes, us)."""
+    """The practical HBM read ceiling: ``sqa_read_probe`` of ``read_probe.hip`` (one
+    workgroup per CU, contiguous chunks, 16-byte non-temporal loads) over the first
+    ~2 GiB of the resident K pool, `steps` passes between two events. Returns (GB/s,
+    bytes, us)."""
+    import read_probe as probe
+
+    probe_lib = probe.load(build_if_missing=False)
     blocks = lib.load().sqa_device_cu_count(0)
     flat = pool.view(-1).view(torch.uint8)
     unit = 16 * 256 * blocks
@@ -195,11 +199,11 @@ def read_probe(torch, lib, pool, steps):
     sink = torch.empty(blocks * 256, dtype=torch.int32, device=pool.device)
     handle = torch.cuda.current_stream().cuda_stream
     for _ in range(3):
-        lib.read_probe(data, sink, blocks, handle)
+        probe.read_probe(data, sink, blocks, handle, probe_lib)
     start, end = _events(torch, 2)
     start.record()
     for _ in range(steps):
-        lib.read_probe(data, sink, blocks, handle)
+        probe.read_probe(data, sink, blocks, handle, probe_lib)
     end.record()
     torch.cuda.synchronize()
     us = start.elapsed_time(end) * 1e3 / steps

@@ -30,7 +30,6 @@ _SIGNATURES = [
     ("sqa_paged_mtp_attention_noalloc", _C.c_int,
      [_C.c_void_p] * 6 + [_C.c_int] * 5 + [_C.c_int64] + [_C.c_int] * 4 + [_C.c_void_p]),
     ("sqa_paged_attention", _C.c_int, [_C.c_void_p]),
-    ("sqa_read_probe", _C.c_int, [_C.c_void_p, _C.c_size_t, _C.c_void_p, _C.c_int, _C.c_void_p]),
     ("sqa_device_cu_count", _C.c_int, [_C.c_int]),
     ("sqa_last_error", _C.c_char_p, []),
     ("sqa_version", _C.c_char_p, []),
@@ -135,19 +134,6 @@ def workspace_bytes(batch: int, q_len: int, num_query_heads: int, num_kv_heads: 
     """Workspace of a plan from :func:`plan_splits` (``pages_per_split`` 0 = balanced)."""
     return int(load().sqa_workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, head_dim,
                                           num_splits, pages_per_split))
-
-
-def read_probe(data, sink, blocks: int, stream_handle: int) -> None:
-    """One pass of ``sqa_read_probe`` over the bytes of the contiguous tensor ``data``
-    (its size a multiple of ``16 * blocks``); ``sink`` is an int32 tensor of
-    ``blocks * 256`` entries. Asynchronous on ``stream_handle``."""
-    lib = load()
-    if not data.is_contiguous() or sink.numel() < blocks * 256:
-        raise ValueError("data must be contiguous and sink hold blocks * 256 dwords")
-    rc = lib.sqa_read_probe(data.data_ptr(), data.numel() * data.element_size(), sink.data_ptr(),
-                            blocks, stream_handle)
-    if rc != 0:
-        raise RuntimeError(f"sqa_read_probe failed: {last_error(lib)}")
 
 
 def raw_stream(device_index: int) -> int:

@@ -28,7 +28,7 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 LIB_PATH = PKG_DIR / "libsqa.so"
-SOURCES = [CSRC / "sqa_kernels.hip", CSRC / "sqa_capi.hip", CSRC / "sqa_probe.hip"]
+SOURCES = [CSRC / "sqa_kernels.hip", CSRC / "sqa_capi.hip"]
 HEADERS = [CSRC / "sqa_internal.h", INCLUDE / "sqa.h"]
 ARCH = "gfx950"
 

@@ -193,22 +193,6 @@ def test_general_entry_struct_matches_the_header(lib):
     assert _general(lib, num_splits=2) == SQA_ERR_WORKSPACE
 
 
-@pytest.mark.parametrize("args,msg", [
-    ((0, 4096, 4096, 1), "null pointer"),
-    ((4096, 4096, 0, 1), "null pointer"),
-    ((4096, 4096, 4096, 0), "blocks"),
-    ((4096, 4096, 4096, 65537), "blocks"),
-    ((4104, 4096, 4096, 1), "aligned"),
-    ((4096, 4096, 4098, 1), "aligned"),
-    ((4096, 0, 4096, 1), "multiple"),
-    ((4096, 4096 + 16, 4096, 2), "multiple"),
-])
-def test_read_probe_rejects_bad_arguments_without_a_gpu(lib, args, msg):
-    data, nbytes, sink, blocks = args
-    assert lib.sqa_read_probe(data, nbytes, sink, blocks, None) == SQA_ERR_INVALID
-    assert msg in lib.sqa_last_error().decode()
-
-
 def test_noalloc_rejects_plans_beyond_its_scratch_before_any_device_call(lib):
     """SQA_NOALLOC_SCRATCH_BYTES (64 MiB) bounds the plan; larger plans fail with
     SQA_ERR_WORKSPACE before the library touches a device (so this runs without a GPU)."""

@@ -1,5 +1,5 @@
-"""GPU check of the streaming-read probe (``sqa_read_probe``), the measurement aid
-bench.py reports beside the roofline: every dword of the buffer is read exactly
+"""GPU check of the streaming-read probe (``sqa_read_probe`` of ``read_probe.hip``),
+the measurement aid bench.py reports beside the roofline: every dword of the buffer is read exactly
 once, by the thread the chunked layout assigns it to. Thread t of workgroup b
 folds (xor) the 16-byte elements t, t + 256, ... of chunk b, so the sink equals
 an xor-reduction of the buffer viewed as [blocks, rounds, 256, 4] dwords.
@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from small_q_attention_amd import _lib
+import read_probe
 
 pytestmark = pytest.mark.gpu
 
@@ -32,7 +32,7 @@ def test_read_probe_reads_every_dword_once(blocks, per_block):
     host = host.to(torch.int32)
     data = host.cuda()
     sink = torch.full((blocks * 256,), -1, dtype=torch.int32, device="cuda")
-    _lib.read_probe(data, sink, blocks, torch.cuda.current_stream().cuda_stream)
+    read_probe.read_probe(data, sink, blocks, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     words = host.numpy().view(np.uint32).reshape(blocks, per_block // 256, 256, 4)
     want = np.bitwise_xor.reduce(np.bitwise_xor.reduce(words, axis=3), axis=1).reshape(-1)
@@ -43,4 +43,4 @@ def test_read_probe_rejects_a_ragged_size():
     data = torch.zeros(4 * 256 + 1, dtype=torch.int32, device="cuda")
     sink = torch.zeros(256, dtype=torch.int32, device="cuda")
     with pytest.raises(RuntimeError, match="multiple"):
-        _lib.read_probe(data, sink, 1, torch.cuda.current_stream().cuda_stream)
+        read_probe.read_probe(data, sink, 1, torch.cuda.current_stream().cuda_stream)
