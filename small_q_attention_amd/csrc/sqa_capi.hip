@@ -286,6 +286,7 @@ int run_attention(const sqa_attention_args& a) {
   pa.spec_pages = spec_pages;
   pa.spec_pps =
       spec_pages > 0 ? sqa::packed_item_pages(batch * spec_pages, num_splits - batch) : 0;
+  pa.seam_pages = balanced ? sqa::seam_pages((int)rows, num_kv_heads, head_dim, (int)kv_bytes) : 0;
   pa.scale_log2 = (float)(1.4426950408889634 * (double)a.scale);
   pa.out_scale = a.out_scale;
   pa.bf16 = a.dtype == SQA_DTYPE_BF16;

@@ -39,6 +39,15 @@ struct SeqSplits {
 // straight to the output. The kernel records each sequence's (first slot,
 // count) for the merge.
 //
+// Seams: a workgroup whose item spans the start of a sequence runs a second
+// piece, which costs it about seam_pages pages' time (the first piece's
+// results written, the second's Q, page ids and first pages fetched). When the
+// lengths differ (a ragged batch), every sequence start that does not fall on an
+// item boundary of that layout is preceded by seam_pages pages of nothing, and
+// the items are cut from the pages laid end to end with those gaps: an item that
+// spans such a start then carries seam_pages fewer pages. Batches whose lengths
+// are all equal (and so every plan with spec_pages) get no gaps.
+//
 // spec_pages > 0 (balanced plan only): the page count the caller expects every
 // sequence to have (from max_seq_len), with that case's item size computed by
 // the host (spec_pps = packed_item_pages(batch * spec_pages, T)). Workgroups
@@ -77,6 +86,7 @@ struct PartialArgs {
   int pages_per_split, num_splits;
   int spec_pages;             // balanced plan: expected pages of every sequence (0: none)
   int spec_pps;               // the balanced plan's item size when every sequence spans spec_pages
+  int seam_pages;             // balanced plan: pages a second piece costs a workgroup (0: no gaps)
   float scale_log2;           // softmax scale * log2(e)
   float out_scale;            // multiplier applied to the normalised output
   int bf16;                   // element type of Q and out (and of K, V unless kv_fp8): 0 fp16, 1 bf16
@@ -157,6 +167,18 @@ inline LaunchShape launch_shape(int rows, int hkv, int head_dim) {
   if (rows <= 16) return {1, 4, 1, 1};
   if (rows <= 32) return {2, 4, 1, 1};
   return {4, 4, 1, 1};
+}
+
+// What a second piece costs a workgroup of the balanced plan, in pages of its
+// own: ~5.6 us measured at 16 ragged sequences of 2K-32K tokens (q_len 8, head
+// dim 128, fp16), where one page of the workgroup's (16 tokens of K and V for 4
+// kv heads, 32 KiB) takes ~1.15 us; scaled by the bytes of a workgroup's page
+// for other shapes and element types.
+inline int seam_pages(int rows, int hkv, int head_dim, int kv_bytes) {
+  const LaunchShape sh = launch_shape(rows, hkv, head_dim);
+  const int wg_page = 16 * sh.heads * head_dim * 2 * kv_bytes;
+  const int c = (5 * 32768 + wg_page / 2) / wg_page;
+  return c < 1 ? 1 : (c > 32 ? 32 : c);
 }
 
 hipError_t launch_partial(const PartialArgs& a, hipStream_t stream);

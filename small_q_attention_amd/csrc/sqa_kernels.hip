@@ -516,6 +516,7 @@ struct ItemRange {
   int len;      // seq_lens[b], clamped to >= 0
   int n_valid;  // splits of this sequence that own pages
   int slot0;    // partial slot of split 0 of this sequence
+  int g_end;    // balanced plan: where the piece ends along the item's pages
 };
 
 // Fixed plan: sequence b owns slots b * num_splits + s.
@@ -529,6 +530,7 @@ __device__ __forceinline__ ItemRange fixed_item(const PartialArgs& a, int item) 
   r.p_end = min(r.p_begin + a.pages_per_split, pages);
   r.n_valid = min((pages + a.pages_per_split - 1) / a.pages_per_split, a.num_splits);
   r.slot0 = r.b * a.num_splits;
+  r.g_end = 0;
   return r;
 }
 
@@ -541,20 +543,18 @@ __device__ __forceinline__ int piece_tid() {
   return t;
 }
 
-__device__ __forceinline__ int wave_sum_int(int v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-__device__ __forceinline__ int wave_inclusive_scan_int(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(v, o);
-    if (lane >= o) v += y;
-  }
-  return v;
+// Inclusive prefix sum over the wave's 64 lanes with DPP: within rows of 16
+// lanes by shifts of 1, 2, 4 and 8 (lanes past the row start add 0), then each
+// row's total broadcast into the rows after it (lane 15 into rows 1 and 3, lane
+// 31 into rows 2 and 3). Six VALU operations instead of six LDS permutes.
+__device__ __forceinline__ int wave_inclusive_scan_int(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);   // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);   // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
 }
 
 // Balanced plan (batch <= kMaxBalancedBatch = 4 x 64), packed: num_splits =
@@ -569,7 +569,9 @@ __device__ __forceinline__ int wave_inclusive_scan_int(int v) {
 // order, each next piece has the next item or the next sequence and neither
 // index ever falls, so i + b grows strictly). Sequence b thus owns slots
 // [i0_b + b, i1_b + b], i0_b = start_b / P, i1_b = (start_b + pages_b - 1) / P;
-// a sequence inside one item is finished by the partial kernel. Lane l holds
+// a sequence inside one item is finished by the partial kernel. In a ragged
+// batch the positions include the seam gaps (start_b then counts the gaps
+// before sequence b too; an item may end inside a gap). Lane l holds
 // sequences l, l + 64, l + 128, l + 192: every wave derives the plan on its own
 // with wave reductions (no LDS, no barrier), and wave 0 of workgroup 0 writes
 // each sequence's (first slot, count) for the merge kernel.
@@ -591,28 +593,62 @@ __device__ __forceinline__ int pages_of(const PartialArgs& a, int len) {
   return min((len + kPageSize - 1) / kPageSize, a.max_pages);
 }
 
-__device__ __forceinline__ int wave_exclusive_scan_int(int v) {
-  return wave_inclusive_scan_int(v) - v;
-}
-
 // Prefix sums of the page counts and the item size; with write_table, the
 // merge kernel's table.
 __device__ __forceinline__ void packed_plan(const PartialArgs& a, PackedBatch& pb,
                                             bool write_table) {
   const int lane = threadIdx.x & 63;
+  // Groups of 64 sequences past the batch hold no pages: their scans are skipped
+  // (a uniform branch), and a group's sum is the last lane of its scan.
+  const int groups = (a.batch + 63) / 64;
   int base = 0;  // pages of the groups of 64 sequences before this one
   int pages[kSeqPerLane];
 #pragma unroll
   for (int k = 0; k < kSeqPerLane; ++k) {
     pages[k] = pages_of(a, pb.len[k]);
-    pb.start[k] = base + wave_exclusive_scan_int(pages[k]);
-    base += wave_sum_int(pages[k]);
+    pb.start[k] = base;
+    if (k < groups) {
+      const int incl = wave_inclusive_scan_int(pages[k]);
+      pb.start[k] += incl - pages[k];
+      base += __builtin_amdgcn_readlane(incl, 63);
+    }
   }
   // Wave sums are the same in every lane; readfirstlane says so to the
   // compiler, which keeps the loop over pieces (and the page ids loaded in it)
   // uniform rather than wrapping each buffer load in a waterfall loop.
   pb.total = __builtin_amdgcn_readfirstlane(base);
-  pb.P = packed_item_pages(pb.total, a.num_splits - a.batch);
+  const int target = a.num_splits - a.batch;
+  pb.P = packed_item_pages(pb.total, target);
+  // Seams (ragged batches): seam_pages of nothing before every sequence start
+  // that is not on an item boundary of the layout without them, so an item that
+  // spans the start carries fewer pages; skipped where the gaps would need
+  // items over kMaxSplitPages pages, or items are too short for them to matter.
+  const int first_pages = __builtin_amdgcn_readfirstlane(pages[0]);
+  bool ragged = false;
+#pragma unroll
+  for (int k = 0; k < kSeqPerLane; ++k) ragged |= 64 * k + lane < a.batch && pages[k] != first_pages;
+  const int seam = a.seam_pages;
+  if (seam > 0 && pb.P >= 4 * seam && __any(ragged)) {  // uniform
+    int gap_base = 0;
+    int vstart[kSeqPerLane];
+#pragma unroll
+    for (int k = 0; k < kSeqPerLane; ++k) {
+      const int gap = pages[k] > 0 && pb.start[k] % pb.P != 0 ? seam : 0;
+      vstart[k] = pb.start[k] + gap_base;
+      if (k < groups) {
+        const int incl = wave_inclusive_scan_int(gap);
+        vstart[k] += incl;
+        gap_base += __builtin_amdgcn_readlane(incl, 63);
+      }
+    }
+    const int total = pb.total + __builtin_amdgcn_readfirstlane(gap_base);
+    if (total <= target * kMaxSplitPages) {  // uniform
+#pragma unroll
+      for (int k = 0; k < kSeqPerLane; ++k) pb.start[k] = vstart[k];
+      pb.total = total;
+      pb.P = packed_item_pages(total, target);
+    }
+  }
   if (write_table && threadIdx.x < 64) {
 #pragma unroll
     for (int k = 0; k < kSeqPerLane; ++k) {
@@ -626,23 +662,26 @@ __device__ __forceinline__ void packed_plan(const PartialArgs& a, PackedBatch& p
   }
 }
 
-// The piece of item `item` that holds global page g (g inside the item): its
-// sequence, page range (within the sequence), length, split count and slot.
-// The wave finds the lane holding that sequence with one ballot per sequence
-// slot; everything after is scalar.
+// The piece of item `item` from position g on (g inside the item): the first
+// sequence with pages that end after g (the one holding g, or the next one if g
+// lies in the gap before a sequence start), its page range (within the
+// sequence), length, split count and slot, and where the piece ends. The wave
+// finds the lane holding that sequence with one ballot per sequence slot;
+// everything after is scalar.
 __device__ __forceinline__ ItemRange packed_piece(const PartialArgs& a, const PackedBatch& pb,
                                                  int item, int g) {
   int b = -1, st = 0, len = 0;
 #pragma unroll
   for (int k = 0; k < kSeqPerLane; ++k) {
     // Lengths are 0 past the batch: those slots have no pages.
-    const bool mine = pb.start[k] <= g && g < pb.start[k] + pages_of(a, pb.len[k]);
+    const int np = pages_of(a, pb.len[k]);
+    const bool mine = np > 0 && g < pb.start[k] + np;
     const unsigned long long hit = __ballot(mine);
-    if (hit) {
+    if (hit && b < 0) {
       const int src = __builtin_ctzll(hit);
       b = 64 * k + src;
-      st = __builtin_amdgcn_readfirstlane(__shfl(pb.start[k], src));
-      len = __builtin_amdgcn_readfirstlane(__shfl(pb.len[k], src));
+      st = __builtin_amdgcn_readlane(pb.start[k], src);  // src is uniform
+      len = __builtin_amdgcn_readlane(pb.len[k], src);
     }
   }
   ItemRange r;
@@ -651,10 +690,11 @@ __device__ __forceinline__ ItemRange packed_piece(const PartialArgs& a, const Pa
   r.b = b;
   r.split = 0;
   r.len = len;
-  r.p_begin = g - st;
-  r.p_end = min(g_end, st + np) - st;
+  r.p_begin = max(g - st, 0);
+  r.p_end = min(g_end, st + np) - st;  // <= p_begin: the item ends in the gap
   r.n_valid = (st + np - 1) / pb.P - st / pb.P + 1;
   r.slot0 = item + b;
+  r.g_end = st + r.p_end;
   return r;
 }
 
@@ -778,8 +818,9 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
     it.len = __builtin_amdgcn_readfirstlane(it.len);
     it.n_valid = __builtin_amdgcn_readfirstlane(it.n_valid);
     it.slot0 = __builtin_amdgcn_readfirstlane(it.slot0);
-    // Every page of [0, total) lies in some sequence, so a piece always has one
-    // and at least one page; the check keeps the loop finite whatever the inputs.
+    // A piece has a sequence and at least one page unless the item ends in the
+    // gap before a sequence start (no further pieces then); the check also keeps
+    // the loop finite whatever the inputs.
     if (balanced && (it.b < 0 || it.p_end <= it.p_begin)) break;
     // Uniform addresses (the fields above) make the ids uniform values: the
     // buffer resources built from them stay in scalar registers.
@@ -787,7 +828,7 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
     ids_loaded = false;
     if (!first) __syncthreads();  // the previous piece is done with the LDS
     piece(it, first_id);
-    g = __builtin_amdgcn_readfirstlane(g + (balanced ? it.p_end - it.p_begin : 1));
+    g = __builtin_amdgcn_readfirstlane(balanced ? it.g_end : g + 1);
   }
 }
 
@@ -1440,6 +1481,14 @@ void sqa_partial_lds_kernel(PartialArgs a) {
 // sums when the max grows (as the online softmax does), so no pass over the
 // maxima precedes the sums; the SG groups then meet by shuffles (TPR = 64, one
 // wave per row) or in LDS (TPR = 256, a workgroup per row for many splits).
+// A (first slot, count) entry held to the slots that exist, whatever the table
+// holds (the partial kernel writes it within them).
+__device__ __forceinline__ SeqSplits in_range(SeqSplits t, int num_splits) {
+  t.first = min(max(t.first, 0), num_splits - 1);
+  t.count = min(max(t.count, 0), num_splits - t.first);
+  return t;
+}
+
 template <int TPR, int HD, typename E>
 __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   constexpr int CH = HD / 4;       // 4-dim chunks of a row
@@ -1481,7 +1530,7 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
     n_valid = (start + a.spec_pages - 1) / a.spec_pps - i0 + 1;
     slot0 = i0 + b;
   } else if (balanced) {
-    table = a.seq_splits[b];
+    table = in_range(a.seq_splits[b], a.num_splits);
     n_valid = table.count;
     slot0 = table.first;
   } else {
@@ -1546,7 +1595,7 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
     den = 0.f;
     acc = f4{0.f, 0.f, 0.f, 0.f};
     load_round(s0, nv, g);
-    if (expect) table = a.seq_splits[b];
+    if (expect) table = in_range(a.seq_splits[b], a.num_splits);
     const float first_l = l[0];  // split g (split 0 for group 0)
     add_round();
     for (int sb = g + U * SG; sb < nv; sb += U * SG) {

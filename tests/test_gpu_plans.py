@@ -118,17 +118,29 @@ def _plan_table(ws, tensors, ns):
     return ws[off:off + 2 * batch].view(torch.int32).view(batch, 2).cpu().tolist()
 
 
-def _packed_layout(lens, items, page=16):
+# Seam gap of the balanced plan at head dim 128 with 16-bit K/V (four kv heads, a
+# 32 KiB page per workgroup): what a second piece costs a workgroup, in pages.
+SEAM_PAGES = 5
+
+
+def _packed_layout(lens, items, page=16, seam=SEAM_PAGES):
     """Brute force from the plan's definition: pages laid end to end in batch order,
     cut into items of P = clamp(ceil(total / items), 4, 2048) pages; the part of
-    item i in sequence b goes to slot i + b. Returns P and each sequence's slots."""
+    item i in sequence b goes to slot i + b. In a ragged batch (and when P >= 4 *
+    seam), every sequence start off an item boundary of that layout is preceded by
+    `seam` empty positions first (unless that needs items over 2048 pages). Returns
+    P and each sequence's slots."""
     pages = [(n + page - 1) // page for n in lens]
+    start = [sum(pages[:b]) for b in range(len(pages))]
     total = sum(pages)
     P = min(max(-(-total // items), 4), 2048)
-    slots, g = [], 0
-    for b, n in enumerate(pages):
-        slots.append(sorted({(g + j) // P + b for j in range(n)}))
-        g += n
+    if seam and P >= 4 * seam and any(n != pages[0] for n in pages):
+        gaps = [seam if n > 0 and start[b] % P else 0 for b, n in enumerate(pages)]
+        vstart = [start[b] + sum(gaps[:b + 1]) for b in range(len(pages))]
+        if total + sum(gaps) <= items * 2048:
+            start, total = vstart, total + sum(gaps)
+            P = min(max(-(-total // items), 4), 2048)
+    slots = [sorted({(start[b] + j) // P + b for j in range(n)}) for b, n in enumerate(pages)]
     return P, slots
 
 
