@@ -216,21 +216,67 @@ def launch_general(query, output, k_view, v_view, block_tables, seq_lens, draft_
 
 def run(query, key_cache, value_cache, block_tables, seq_lens, num_splits: int,
         pages_per_split: int):
-    """Allocate the output and workspace with torch's caching allocator and launch on the
-    current stream of the query's device. Returns the output."""
+    """Allocate the output with torch's caching allocator, take a workspace from
+    :func:`workspace_for`, and launch on the current stream of the query's device.
+    Returns the output."""
     import torch
 
     out = torch.empty_like(query)
     b, q_len, hq, d = query.shape
     nbytes = workspace_bytes(b, q_len, hq, key_cache.shape[2], d, num_splits, pages_per_split)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=query.device) if nbytes else None
     stream = raw_stream(query.device.index)
+    ws = workspace_for(nbytes, query.device, query.device.index, stream) if nbytes else None
     if query.dtype == torch.float16:
         launch(query, key_cache, value_cache, block_tables, seq_lens, out, ws, num_splits,
                pages_per_split, stream)
     else:  # bf16: the general entry point carries the element type
         launch_general(query, out, key_cache, value_cache, block_tables, seq_lens, None,
                        query.shape[-1] ** -0.5, 1.0, num_splits, pages_per_split, ws, stream)
+    return out
+
+
+# Workspaces kept per (device, stream) for eager calls: a stream runs its calls in
+# order, so one buffer serves them all and the per-call allocation is saved.
+# Plans past WORKSPACE_CACHE_BYTES, and calls under graph capture (whose buffers
+# belong to the graph's pool), allocate their own.
+WORKSPACE_CACHE_BYTES = 64 << 20
+_WORKSPACES = {}
+
+
+def workspace_for(nbytes: int, device, device_index: int, stream_handle: int):
+    """A workspace of at least ``nbytes`` for a call on ``stream_handle``."""
+    import torch
+
+    if nbytes > WORKSPACE_CACHE_BYTES or torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    key = (device_index, stream_handle)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def run_fp16(query, key_cache, value_cache, block_tables, seq_lens, batch: int, q_len: int,
+             num_query_heads: int, num_kv_heads: int, num_pages: int, page_size: int,
+             max_pages: int, num_splits: int, pages_per_split: int, device_index: int):
+    """:func:`run` for the fp16, head-dim-128 call whose shapes the caller has already
+    checked and unpacked: the same allocation and launch with fewer Python steps."""
+    import torch
+
+    out = torch.empty_like(query)
+    nbytes = workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, 128, num_splits,
+                             pages_per_split)
+    stream = raw_stream(device_index)
+    ws = workspace_for(nbytes, query.device, device_index, stream) if nbytes else None
+    rc = _LIB.sqa_paged_mtp_attention(
+        query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+        block_tables.data_ptr(), seq_lens.data_ptr(), out.data_ptr(),
+        ws.data_ptr() if ws is not None else None, nbytes, batch, q_len, num_query_heads,
+        num_kv_heads, 128, num_pages, page_size, max_pages, num_splits, pages_per_split,
+        stream, None)
+    if rc != SQA_OK:
+        raise RuntimeError(f"sqa_paged_mtp_attention failed: {last_error(_LIB)}")
     return out
 
 

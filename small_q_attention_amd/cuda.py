@@ -96,16 +96,17 @@ load_v1 = load_v2 = load_v3 = load_v4 = load_v5 = load_v0
 
 
 _GPU_SEEN_BY = None  # the torch.cuda.is_available function that last reported a GPU
+_TORCH = None  # the torch module, once a GPU has been seen
 
 
 def _gpu_present(torch) -> bool:
     """``torch.cuda.is_available()``, remembered once true (it costs ~1 us per call)."""
-    global _GPU_SEEN_BY
+    global _GPU_SEEN_BY, _TORCH
     probe = torch.cuda.is_available
     if _GPU_SEEN_BY is probe:
         return True
     if probe():
-        _GPU_SEEN_BY = probe
+        _GPU_SEEN_BY, _TORCH = probe, torch
         return True
     return False
 
@@ -214,6 +215,61 @@ def _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
     return _lib.run(query, key_cache, value_cache, block_tables, seq_lens, num_splits, pps)
 
 
+def _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, chunk_keys,
+          max_seq_len: int, gqa4: bool):
+    """The common valid call (fp16 Q/K/V, head dim 128, one device, contiguous, consistent
+    shapes, eager, library loaded) checked in one pass, then planned and launched;
+    ``None`` when anything differs, and the full checks then run (and raise as the
+    reference does). Accepts exactly what those checks accept."""
+    torch = _TORCH
+    if torch is None or _GPU_SEEN_BY is not torch.cuda.is_available or _lib._LIB is None:
+        return None
+    tensor = torch.Tensor  # plain tensors only (subclasses and stand-ins take the full way)
+    if not (type(query) is tensor and type(key_cache) is tensor and type(value_cache) is tensor
+            and type(block_tables) is tensor and type(seq_lens) is tensor):
+        return None
+    f16, i32 = torch.float16, torch.int32
+    if not (query.dtype is f16 and key_cache.dtype is f16 and value_cache.dtype is f16
+            and block_tables.dtype is i32 and seq_lens.dtype is i32
+            and query.is_cuda and key_cache.is_cuda and value_cache.is_cuda
+            and block_tables.is_cuda and seq_lens.is_cuda):
+        return None
+    dev = query.get_device()
+    if not (key_cache.get_device() == dev and value_cache.get_device() == dev
+            and block_tables.get_device() == dev and seq_lens.get_device() == dev
+            and query.is_contiguous() and key_cache.is_contiguous()
+            and value_cache.is_contiguous() and block_tables.is_contiguous()
+            and seq_lens.is_contiguous()):
+        return None
+    qs, ks = query.shape, key_cache.shape
+    if len(qs) != 4 or len(ks) != 4 or value_cache.shape != ks or block_tables.dim() != 2:
+        return None
+    batch, q_len, hq, dim = qs
+    num_pages, page, hkv, kdim = ks
+    bt_rows, bt_cols = block_tables.shape
+    if not (dim == HEAD_DIM and kdim == HEAD_DIM and q_len in SUPPORTED_Q_LENS
+            and page == page_size and page in SUPPORTED_PAGE_SIZES and hkv > 0
+            and hq % hkv == 0 and batch > 0 and bt_rows == batch
+            and seq_lens.numel() == batch and num_pages > 0 and bt_cols > 0):
+        return None
+    group = hq // hkv
+    if (gqa4 and group != 4) or q_len * group > MAX_ROWS:
+        return None
+    if chunk_keys is not None and chunk_keys <= 0:
+        return None
+    if _tracing():
+        return None
+    if max_seq_len == -1:
+        max_seq_len = int(seq_lens.max().item())
+        if max_seq_len <= 0:
+            raise RuntimeError("seq_lens must be positive")
+    num_splits, pps = _lib.plan_splits(dev, batch, q_len, hq, hkv, HEAD_DIM, int(max_seq_len),
+                                       bt_cols * (page // PAGE_SIZE),
+                                       0 if chunk_keys is None else int(chunk_keys))
+    return _lib.run_fp16(query, key_cache, value_cache, block_tables, seq_lens, batch, q_len,
+                         hq, hkv, num_pages, page, bt_cols, num_splits, pps, dev)
+
+
 def _tracing() -> bool:
     import torch
 
@@ -243,6 +299,9 @@ def paged_mtp_attention(query, key_cache, value_cache, block_tables, seq_lens,
 def forward_v0(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
                verbose: bool = False):
     """Reference ``forward_v0`` (``cuda.py:61-78``); automatic split plan, no host sync."""
+    out = _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, None, 0, False)
+    if out is not None:
+        return out
     _check_python_contract("v0", query, key_cache, value_cache, block_tables, seq_lens, False)
     return load_v0(verbose=verbose).forward(query, key_cache, value_cache, block_tables,
                                             seq_lens, page_size)
@@ -251,6 +310,9 @@ def forward_v0(query, key_cache, value_cache, block_tables, seq_lens, page_size:
 def forward_v1(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
                verbose: bool = False):
     """Reference ``forward_v1`` (``cuda.py:81-96``); same kernels as v0."""
+    out = _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, None, 0, False)
+    if out is not None:
+        return out
     _check_python_contract("v1", query, key_cache, value_cache, block_tables, seq_lens, False)
     return load_v1(verbose=verbose).forward_v1(query, key_cache, value_cache, block_tables,
                                                seq_lens, page_size)
@@ -259,6 +321,10 @@ def forward_v1(query, key_cache, value_cache, block_tables, seq_lens, page_size:
 def forward_v2(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
                chunk_keys: Optional[int] = 512, verbose: bool = False):
     """Reference ``forward_v2`` (``cuda.py:120-153``): ``chunk_keys`` KV entries per split."""
+    out = _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, chunk_keys, -1,
+                False)
+    if out is not None:
+        return out
     _check_python_contract("v2", query, key_cache, value_cache, block_tables, seq_lens, False)
     if chunk_keys is not None and chunk_keys <= 0:
         raise ValueError("chunk_keys must be positive")
@@ -269,6 +335,10 @@ def forward_v2(query, key_cache, value_cache, block_tables, seq_lens, page_size:
 def forward_v3(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
                chunk_keys: Optional[int] = 512, max_seq_len: int = 0, verbose: bool = False):
     """Reference ``forward_v3`` (``cuda.py:177-214``); ``max_seq_len=0`` measures it (sync)."""
+    out = _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, chunk_keys,
+                max_seq_len or -1, True)
+    if out is not None:
+        return out
     _check_python_contract("v3", query, key_cache, value_cache, block_tables, seq_lens, True)
     if chunk_keys is not None and chunk_keys <= 0:
         raise ValueError("chunk_keys must be positive")
@@ -279,6 +349,10 @@ def forward_v3(query, key_cache, value_cache, block_tables, seq_lens, page_size:
 def forward_v4(query, key_cache, value_cache, block_tables, seq_lens, page_size: int,
                chunk_keys: Optional[int] = 512, max_seq_len: int = 0, verbose: bool = False):
     """Reference ``forward_v4`` (``cuda.py:238-273``); same kernels as v3."""
+    out = _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, chunk_keys,
+                max_seq_len or -1, True)
+    if out is not None:
+        return out
     _check_python_contract("v4", query, key_cache, value_cache, block_tables, seq_lens, True)
     if chunk_keys is not None and chunk_keys <= 0:
         raise ValueError("chunk_keys must be positive")
@@ -290,6 +364,11 @@ def forward_v5(query, key_cache, value_cache, block_tables, seq_lens, page_size:
                chunk_keys: Optional[int] = 512, token_group: int = 2, max_seq_len: int = 0,
                verbose: bool = False):
     """Reference ``forward_v5`` (``cuda.py:297-336``); ``token_group`` checked, then unused."""
+    if token_group in (2, 4):
+        out = _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, chunk_keys,
+                    max_seq_len or -1, True)
+        if out is not None:
+            return out
     _check_python_contract("v5", query, key_cache, value_cache, block_tables, seq_lens, True)
     if token_group not in (2, 4):
         raise ValueError("v5 token_group must be 2 or 4")

@@ -325,3 +325,46 @@ def test_parity_stats_flags_a_planted_mistake():
     q, k, v, bt, sl = (t.cpu() for t in tensors)
     wrong = attention_c64(q, k, v, bt, sl - 1, 16, 8)  # every row sees one key less
     assert not parity_stats(out, wrong)["ok"]
+
+
+def test_one_pass_fast_path_matches_the_checked_path(monkeypatch):
+    """``forward_v0..v5`` check a valid fp16 call in one pass before launching: the
+    result must be bit-equal to the fully checked path's, the full checks must not
+    run for it, and invalid GPU inputs must still raise the reference's errors."""
+    case = inputs.Case(batch=3, q_len=4, seq_lens=[700, 33, 1500], seed=1500)
+    q, k, v, bt, sl = inputs.make_inputs(case, device="cuda")
+    sqa.forward_v3(q, k, v, bt, sl, 16)  # first call: library loaded, GPU seen
+    checked = {
+        "v0": sqa.load_v0().forward(q, k, v, bt, sl, 16),
+        "v2": sqa.load_v2().forward_v2(q, k, v, bt, sl, 16, 256),
+        "v3": sqa.load_v3().forward_v3(q, k, v, bt, sl, 16, 512, 1500),
+        "v5": sqa.load_v5().forward_v5(q, k, v, bt, sl, 16, None, 4, 0),
+    }
+
+    def no_full_checks(*args, **kwargs):
+        raise AssertionError("the full checks ran for a valid call")
+
+    with monkeypatch.context() as m:
+        m.setattr(sqa, "_check_python_contract", no_full_checks)
+        m.setattr(sqa, "_check_launcher_contract", no_full_checks)
+        fast = {
+            "v0": sqa.forward_v0(q, k, v, bt, sl, 16),
+            "v2": sqa.forward_v2(q, k, v, bt, sl, 16, 256),
+            "v3": sqa.forward_v3(q, k, v, bt, sl, 16, 512, 1500),
+            "v5": sqa.forward_v5(q, k, v, bt, sl, 16, None, 4),
+        }
+    for name in checked:
+        assert torch.equal(fast[name], checked[name]), name
+    assert_parity(fast["v3"], _oracle((q, k, v, bt, sl)), label="fast path v3")
+    with pytest.raises(ValueError):
+        sqa.forward_v3(q.transpose(1, 2).contiguous().transpose(1, 2), k, v, bt, sl, 16)
+    with pytest.raises(ValueError):
+        sqa.forward_v3(q.bfloat16(), k, v, bt, sl, 16)
+    with pytest.raises(ValueError):
+        sqa.forward_v3(q[:, :, :16].contiguous(), k, v, bt, sl, 16)  # GQA group 2
+    with pytest.raises(ValueError):
+        sqa.forward_v5(q, k, v, bt, sl, 16, 512, 3)
+    with pytest.raises(RuntimeError):
+        sqa.forward_v3(q, k, v, bt, sl.long(), 16)
+    with pytest.raises(RuntimeError):
+        sqa.forward_v0(q, k, v[:-1], bt, sl, 16)
