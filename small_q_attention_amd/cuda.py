@@ -287,6 +287,11 @@ def paged_mtp_attention(query, key_cache, value_cache, block_tables, seq_lens,
     head_dim 64 or 256 (the ``forward_vN`` names keep the reference's fp16,
     head_dim 128 contract).
     """
+    if max_seq_len >= -1:
+        out = _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, chunk_keys,
+                    int(max_seq_len), False)
+        if out is not None:
+            return out
     _check_python_contract("sqa", query, key_cache, value_cache, block_tables, seq_lens, False,
                            allow_bf16=True, head_dims=HEAD_DIMS)
     if chunk_keys is not None and chunk_keys <= 0:

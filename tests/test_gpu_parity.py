@@ -328,9 +328,10 @@ def test_parity_stats_flags_a_planted_mistake():
 
 
 def test_one_pass_fast_path_matches_the_checked_path(monkeypatch):
-    """``forward_v0..v5`` check a valid fp16 call in one pass before launching: the
-    result must be bit-equal to the fully checked path's, the full checks must not
-    run for it, and invalid GPU inputs must still raise the reference's errors."""
+    """``forward_v0..v5`` and the native entry check a valid fp16 call in one pass
+    before launching: the result must be bit-equal to the fully checked path's, the
+    full checks must not run for it, and invalid GPU inputs must still raise the
+    reference's errors."""
     case = inputs.Case(batch=3, q_len=4, seq_lens=[700, 33, 1500], seed=1500)
     q, k, v, bt, sl = inputs.make_inputs(case, device="cuda")
     sqa.forward_v3(q, k, v, bt, sl, 16)  # first call: library loaded, GPU seen
@@ -339,6 +340,7 @@ def test_one_pass_fast_path_matches_the_checked_path(monkeypatch):
         "v2": sqa.load_v2().forward_v2(q, k, v, bt, sl, 16, 256),
         "v3": sqa.load_v3().forward_v3(q, k, v, bt, sl, 16, 512, 1500),
         "v5": sqa.load_v5().forward_v5(q, k, v, bt, sl, 16, None, 4, 0),
+        "native": sqa._run(q, k, v, bt, sl, 16, None, 1500),
     }
 
     def no_full_checks(*args, **kwargs):
@@ -352,6 +354,7 @@ def test_one_pass_fast_path_matches_the_checked_path(monkeypatch):
             "v2": sqa.forward_v2(q, k, v, bt, sl, 16, 256),
             "v3": sqa.forward_v3(q, k, v, bt, sl, 16, 512, 1500),
             "v5": sqa.forward_v5(q, k, v, bt, sl, 16, None, 4),
+            "native": sqa.paged_mtp_attention(q, k, v, bt, sl, 16, 1500),
         }
     for name in checked:
         assert torch.equal(fast[name], checked[name]), name
