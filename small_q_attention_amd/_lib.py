@@ -247,7 +247,10 @@ def workspace_for(nbytes: int, device, device_index: int, stream_handle: int):
     """A workspace of at least ``nbytes`` for a call on ``stream_handle``."""
     import torch
 
-    if nbytes > WORKSPACE_CACHE_BYTES or torch.cuda.is_current_stream_capturing():
+    # The capture check reads the current device's stream: the cache serves only
+    # calls on that device.
+    if (nbytes > WORKSPACE_CACHE_BYTES or device_index != torch.cuda.current_device()
+            or torch.cuda.is_current_stream_capturing()):
         return torch.empty(nbytes, dtype=torch.uint8, device=device)
     key = (device_index, stream_handle)
     ws = _WORKSPACES.get(key)
