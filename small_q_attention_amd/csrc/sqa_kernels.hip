@@ -1489,12 +1489,12 @@ __device__ __forceinline__ SeqSplits in_range(SeqSplits t, int num_splits) {
   return t;
 }
 
-template <int TPR, int HD, typename E>
+template <int TPR, int HD, typename E, int U>
 __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   constexpr int CH = HD / 4;       // 4-dim chunks of a row
   constexpr int SG = TPR / CH;     // split groups of a row
   constexpr int RPW = 256 / TPR;   // rows per workgroup
-  constexpr int U = 8;             // splits per thread per round
+  // U: splits per thread per round (a round covers U * SG splits of a row)
   static_assert(SG >= 1 && TPR % CH == 0, "a row's threads must cover its dims");
   const int t = threadIdx.x;
   const int tr = t % TPR;
@@ -1559,8 +1559,9 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
       } else {
         o[u] = *(const f4*)(a.part_o + o0 + it * HD);
       }
-      m[u] = ml[it * 2];
-      l[u] = ml[it * 2 + 1];
+      const float2 p = *(const float2*)(ml + it * 2);  // (max, sum) in one load
+      m[u] = p.x;
+      l[u] = p.y;
       if (sp >= nv) l[u] = 0.f;
     }
   };
@@ -1716,14 +1717,18 @@ void launch_partial_as(const PartialArgs& a, const LaunchShape& sh, dim3 grid, d
 template <int HD, typename E>
 void launch_merge_hd(const MergeArgs& a, int per_row, hipStream_t stream) {
   // A wave per row while its split groups take all of the row's splits in two
-  // rounds of loads; a workgroup per row beyond that.
-  constexpr int kSplitsPerWaveRound = 8 * (64 / (HD / 4));
+  // rounds of loads; a workgroup per row beyond that. Rows whose splits fit one
+  // round of 4 loads per thread take that round (half the load instructions of
+  // the 8-load round, whose extra slots would reload split 0 for nothing).
+  constexpr int kGroups = 64 / (HD / 4);
   const int total = a.batch * a.q_len * a.hq;
-  if (per_row <= 2 * kSplitsPerWaveRound) {
-    hipLaunchKernelGGL((sqa_merge_kernel<64, HD, E>), dim3((unsigned)((total + 3) / 4)),
-                       dim3(256), 0, stream, a);
+  const dim3 waves((unsigned)((total + 3) / 4));
+  if (per_row <= 4 * kGroups) {
+    hipLaunchKernelGGL((sqa_merge_kernel<64, HD, E, 4>), waves, dim3(256), 0, stream, a);
+  } else if (per_row <= 2 * 8 * kGroups) {
+    hipLaunchKernelGGL((sqa_merge_kernel<64, HD, E, 8>), waves, dim3(256), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((sqa_merge_kernel<256, HD, E>), dim3((unsigned)total), dim3(256), 0,
+    hipLaunchKernelGGL((sqa_merge_kernel<256, HD, E, 8>), dim3((unsigned)total), dim3(256), 0,
                        stream, a);
   }
 }
