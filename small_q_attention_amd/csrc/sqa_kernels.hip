@@ -1258,37 +1258,13 @@ struct LdsSlice<KvNative<128>> {
   }
 };
 
-// OCP e4m3 caches: 8 chunks of 16 bytes per token; chunk c of token t at
-// position 8 t + (c ^ ((t >> 1) & 7)): the K reads (16 tokens at one chunk) hit
-// 16 bank groups, the V reads (two tokens of 128 bytes per half-wave) two ways.
-template <>
-struct LdsSlice<KvFp8<128>> {
-  static constexpr int kChunks = 8;  // 16-byte chunks per token row (128 bytes)
-  __device__ __forceinline__ static int pos(int t, int c) { return 8 * t + (c ^ ((t >> 1) & 7)); }
-  __device__ __forceinline__ static int token_of(int p) { return p >> 3; }
-  __device__ __forceinline__ static int chunk_of(int p) { return (p & 7) ^ ((p >> 4) & 7); }
-  // K load i of lane (g, l16): token l16, bytes 64 i + 16 g (chunk 4 i + g);
-  // V: tokens 4 g + e, bytes 8 l16 .. + 7 (half l16 & 1 of chunk l16 / 2).
-  __device__ __forceinline__ static void read(KvFp8<128>::Regs& r, const char* ks, const char* vs,
-                                              int g, int l16) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) r.k[i] = *(const u4*)(ks + 16 * pos(l16, 4 * i + g));
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const u2 x = *(const u2*)(vs + 16 * pos(4 * g + e, l16 >> 1) + 8 * (l16 & 1));
-      r.v[e][0] = x[0];
-      r.v[e][1] = x[1];
-    }
-  }
-};
-
 // 33..64 query rows per kv head (q_len 16 at GQA 4) at head dim 128. Eight
 // waves per workgroup: two per kv head, each with 32 of the head's rows in two
 // 16-row blocks (the 32-row math), so no wave holds the 128 accumulator
 // registers of 64 rows, and two waves share each SIMD, one's MFMAs under the
 // other's softmax. The two waves of a head read each page once between them:
-// the workgroup's K and V of 4 heads (32 KiB a page for 16-bit caches, 16 KiB
-// for e4m3) arrive in a ring of D LDS slots by direct buffer loads
+// the workgroup's K and V of 4 heads (32 KiB a page of 16-bit K and V) arrive
+// in a ring of D LDS slots by direct buffer loads
 // (load_to_lds: 1 KiB of a head's page slice per wave and load, in the layout of
 // LdsSlice), so the bytes in flight take no registers. Per page: wait for this
 // thread's loads of the page (manual vmcnt: nothing else in the loop touches
@@ -1692,11 +1668,12 @@ void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, d
   } else if (sh.row_blocks == 2) {
     hipLaunchKernelGGL((sqa_partial_kernel<2, D4, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
                        a);
-  } else if constexpr (HD == 128) {
-    // 33..64 rows: two waves per kv head sharing an LDS ring of 128 KiB (4 pages
-    // of 16-bit K and V, 8 of e4m3).
-    constexpr int DL = KV::kBytes == 2 ? 4 : 8;
-    hipLaunchKernelGGL((sqa_partial_lds_kernel<DL, E, KV>), grid, dim3(512), 0, stream, a);
+  } else if constexpr (HD == 128 && KV::kBytes == 2) {
+    // 33..64 rows of 16-bit K and V: two waves per kv head sharing an LDS ring
+    // of 128 KiB (4 pages). e4m3 caches take the one-wave-per-head kernel below:
+    // it widens each page once per head where two waves would both widen it
+    // (cfg3 shape q16: 256.3 -> 246.6 us; B4 KV 8K 34.8 -> 33.6 us).
+    hipLaunchKernelGGL((sqa_partial_lds_kernel<4, E, KV>), grid, dim3(512), 0, stream, a);
   } else if constexpr (HD != 256) {
     hipLaunchKernelGGL((sqa_partial_kernel<4, D3, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
                        a);
