@@ -73,7 +73,11 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
  * Device workspace bytes sqa_paged_mtp_attention needs for a plan from
  * sqa_plan_splits and a head_dim (0 for a fixed plan with num_splits == 1). Replaces the
  * per-call torch::empty of the partial buffers in the reference launchers
- * (csrc/small_q_attention_ext.cu:1102-1104).
+ * (csrc/small_q_attention_ext.cu:1102-1104). A balanced plan's workspace also
+ * carries a small record from call to call (measured page-loop times of the
+ * 64-row kernel, which set the next call's work-item sizes); whatever it holds,
+ * including uninitialised memory, results are the same, so a fresh or reused
+ * workspace is equally valid.
  */
 size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv_heads,
                            int head_dim, int num_splits, int pages_per_split);

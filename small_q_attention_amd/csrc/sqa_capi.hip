@@ -136,7 +136,10 @@ size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv
   const size_t rows = (size_t)q_len * (num_query_heads / num_kv_heads);
   const size_t items = (size_t)sqa::plan_slots(batch, num_splits, pages_per_split) * num_kv_heads * rows;
   size_t bytes = items * ((size_t)head_dim + 2) * sizeof(float);
-  if (balanced) bytes += (size_t)batch * sizeof(sqa::SeqSplits);
+  // Balanced plans: the merge table, then the paired items' delta record (16
+  // bytes) and one 8-byte loop-time record per workgroup (two per slot).
+  if (balanced)
+    bytes += (size_t)batch * sizeof(sqa::SeqSplits) + 16 + (size_t)num_splits * 2 * 8;
   return bytes;
 }
 
@@ -287,6 +290,14 @@ int run_attention(const sqa_attention_args& a) {
   pa.spec_pps =
       spec_pages > 0 ? sqa::packed_item_pages(batch * spec_pages, num_splits - batch) : 0;
   pa.seam_pages = balanced ? sqa::seam_pages((int)rows, num_kv_heads, head_dim, (int)kv_bytes) : 0;
+  // Paired items: the 64-row kernel (33..64 rows, head dim 128, 16-bit K/V)
+  // with two head groups of four kv heads, an expected page count that pairs
+  // of items divide, and an even item count.
+  pa.tune = balanced ? (float*)(pa.seq_splits + batch) : nullptr;
+  pa.pair_items = balanced && spec_pages > 0 && pa.spec_pps > 0 &&
+                  spec_pages % (2 * pa.spec_pps) == 0 && (num_splits - batch) % 2 == 0 &&
+                  head_dim == 128 && kv_bytes == 2 && rows > 32 && rows <= 64 &&
+                  num_kv_heads == 8;
   pa.scale_log2 = (float)(1.4426950408889634 * (double)a.scale);
   pa.out_scale = a.out_scale;
   pa.bf16 = a.dtype == SQA_DTYPE_BF16;
@@ -317,6 +328,8 @@ int run_attention(const sqa_attention_args& a) {
     ma.spec_pps = pa.spec_pps;
     ma.out_scale = a.out_scale;
     ma.bf16 = pa.bf16;
+    ma.tune = pa.pair_items ? pa.tune : nullptr;
+    ma.tune_records = (num_splits - batch) * 2;
     if ((e = sqa::launch_merge(ma, s)) != hipSuccess) return hip_fail(e, "merge kernel launch");
   }
   if (ev && (e = hipEventRecord(ev[2], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");

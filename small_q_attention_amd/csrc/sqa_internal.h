@@ -59,6 +59,21 @@ struct SeqSplits {
 //
 // The C ABI carries spec_pages in pages_per_split: 0 is the balanced plan,
 // -P the balanced plan expecting P pages per sequence.
+//
+// Paired items (pair_items != 0; the 64-row kernel with two head groups, every
+// length as expected and two items of P pages dividing a sequence): items
+// 2k and 2k + 1 share 2P pages, the even one taking P + d and the odd one
+// P - d, d = round(P * delta), and both workgroups of item i (one per head
+// group) run on XCDs of i's parity (blockIdx.x = 4k + 2 head_group + (i & 1);
+// workgroups are dealt to the XCDs in turn). The XCDs of one parity stream
+// faster than the others on these boxes, by a margin that depends on the box
+// and the access pattern, so delta is measured rather than fixed: each
+// workgroup records its page-loop time and pages, and the merge kernel sets
+// delta for the next call from the per-page times of even and odd items.
+// Any delta gives the same items' keys in some split, so results do not depend
+// on it; every workgroup of a call reads the same value.
+constexpr unsigned kTuneMagic = 0x51a7u << 16 | 1u;  // tune[0] when tune[1] holds a delta
+constexpr float kPairDeltaMax = 0.1f;                // |delta| bound
 struct PartialArgs {
   const _Float16* q;          // [B, Q, Hq, head_dim]
   const _Float16* k;          // K of page 0, slot 0, kv head 0
@@ -87,6 +102,8 @@ struct PartialArgs {
   int spec_pages;             // balanced plan: expected pages of every sequence (0: none)
   int spec_pps;               // the balanced plan's item size when every sequence spans spec_pages
   int seam_pages;             // balanced plan: pages a second piece costs a workgroup (0: no gaps)
+  int pair_items;             // paired items on (see above)
+  float* tune;                // paired items: {magic, delta} then per workgroup {loop ticks, pages}
   float scale_log2;           // softmax scale * log2(e)
   float out_scale;            // multiplier applied to the normalised output
   int bf16;                   // element type of Q and out (and of K, V unless kv_fp8): 0 fp16, 1 bf16
@@ -119,6 +136,8 @@ struct MergeArgs {
   int spec_pps;     // the balanced plan's item size when that holds
   float out_scale;
   int bf16;
+  float* tune;      // paired items: the delta record to update (null: none)
+  int tune_records; // workgroup records after it
 };
 
 // The balanced plan's item size: pages per work item when `total` pages are

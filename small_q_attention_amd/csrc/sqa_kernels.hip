@@ -517,6 +517,7 @@ struct ItemRange {
   int n_valid;  // splits of this sequence that own pages
   int slot0;    // partial slot of split 0 of this sequence
   int g_end;    // balanced plan: where the piece ends along the item's pages
+  int paired;   // a paired item of the expected-page plan (its loop time is recorded)
 };
 
 // Fixed plan: sequence b owns slots b * num_splits + s.
@@ -531,6 +532,7 @@ __device__ __forceinline__ ItemRange fixed_item(const PartialArgs& a, int item) 
   r.n_valid = min((pages + a.pages_per_split - 1) / a.pages_per_split, a.num_splits);
   r.slot0 = r.b * a.num_splits;
   r.g_end = 0;
+  r.paired = 0;
   return r;
 }
 
@@ -669,7 +671,7 @@ __device__ __forceinline__ void packed_plan(const PartialArgs& a, PackedBatch& p
 // finds the lane holding that sequence with one ballot per sequence slot;
 // everything after is scalar.
 __device__ __forceinline__ ItemRange packed_piece(const PartialArgs& a, const PackedBatch& pb,
-                                                 int item, int g) {
+                                                 int item, int g, int item_end) {
   int b = -1, st = 0, len = 0;
 #pragma unroll
   for (int k = 0; k < kSeqPerLane; ++k) {
@@ -686,7 +688,7 @@ __device__ __forceinline__ ItemRange packed_piece(const PartialArgs& a, const Pa
   }
   ItemRange r;
   const int np = pages_of(a, len);
-  const int g_end = min((item + 1) * pb.P, pb.total);
+  const int g_end = min(item_end, pb.total);
   r.b = b;
   r.split = 0;
   r.len = len;
@@ -695,6 +697,7 @@ __device__ __forceinline__ ItemRange packed_piece(const PartialArgs& a, const Pa
   r.n_valid = (st + np - 1) / pb.P - st / pb.P + 1;
   r.slot0 = item + b;
   r.g_end = st + r.p_end;
+  r.paired = 0;
   return r;
 }
 
@@ -760,6 +763,8 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
   ItemRange it;
   bool ids_loaded = false;
   int g = 0, g_end = 1;  // global pages still to visit (fixed plan: one piece)
+  int item_end = 0;      // balanced plan: where the item ends
+  bool paired = false;
   if (!balanced) {
     const int seq = item / a.num_splits;
     load_first_ids(seq, (item - seq * a.num_splits) * a.pages_per_split);
@@ -785,32 +790,51 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
           }
         }
       }
-      const int g0 = item * pb.P;
+      // Paired items: the shared boundary of items 2k and 2k + 1 moves by d
+      // pages; the delta record is read with the lengths, the first ids after.
+      paired = a.pair_items != 0;
+      int g0 = item * pb.P;
+      item_end = g0 + pb.P;
+      if (paired) {
+        const float2 rec = *(const float2*)a.tune;
+        load_lengths(a, pb.len);
+        float dl = __float_as_uint(rec.x) == kTuneMagic ? rec.y : 0.f;
+        dl = dl == dl ? fminf(fmaxf(dl, -kPairDeltaMax), kPairDeltaMax) : 0.f;
+        const int d = __builtin_amdgcn_readfirstlane((int)rintf((float)pb.P * dl));
+        g0 = (item >> 1) * 2 * pb.P + ((item & 1) ? pb.P + d : 0);
+        item_end = (item >> 1) * 2 * pb.P + ((item & 1) ? 2 * pb.P : pb.P + d);
+      }
       const int b0 = min(g0 / P, a.batch - 1);
       load_first_ids(b0, g0 - b0 * P);
-      load_lengths(a, pb.len);
+      if (!paired) load_lengths(a, pb.len);
       bool differs = false;
 #pragma unroll
       for (int k = 0; k < kSeqPerLane; ++k)
         differs |= 64 * k + lane < a.batch && pages_of(a, pb.len[k]) != P;
       if (__any(differs)) {
         packed_plan(a, pb, blockIdx.x == 0);  // rewrites the table
+        paired = false;
       } else {
         ids_loaded = true;
       }
+      if (paired) g = g0;
     } else {
       load_lengths(a, pb.len);
       packed_plan(a, pb, blockIdx.x == 0);
     }
-    g = item * pb.P;
-    g_end = min(g + pb.P, pb.total);
+    if (!paired) {
+      g = item * pb.P;
+      item_end = g + pb.P;
+    }
+    g_end = min(item_end, pb.total);
   }
   // The same in every lane (readfirstlane tells the compiler, which otherwise
   // runs the loop under an exec mask).
   g = __builtin_amdgcn_readfirstlane(g);
   g_end = __builtin_amdgcn_readfirstlane(g_end);
   for (bool first = true; g < g_end; first = false) {  // uniform
-    if (balanced) it = packed_piece(a, pb, item, g);
+    if (balanced) it = packed_piece(a, pb, item, g, item_end);
+    it.paired = paired;
     it.b = __builtin_amdgcn_readfirstlane(it.b);
     it.split = __builtin_amdgcn_readfirstlane(it.split);
     it.p_begin = __builtin_amdgcn_readfirstlane(it.p_begin);
@@ -1285,10 +1309,14 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   static_assert(HD * KV::kBytes == 16 * L::kChunks, "a token row is kChunks 16-byte chunks");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-  // blockIdx.x = item * head_groups + head_group; wave = half * 4 + head slot.
+  // blockIdx.x = item * head_groups + head_group; with paired items (two head
+  // groups), 4k + 2 head_group + (item & 1) for item 2k + (item & 1), so both
+  // workgroups of an item run on XCDs of the item's parity. wave = half * 4 +
+  // head slot.
   const int head_groups = (a.hkv + 3) / 4;
-  const int hgrp = blockIdx.x % head_groups;
-  const int item = blockIdx.x / head_groups;
+  const bool pairs = a.pair_items != 0;
+  const int hgrp = pairs ? (blockIdx.x & 3) >> 1 : blockIdx.x % head_groups;
+  const int item = pairs ? (blockIdx.x >> 2) * 2 + (blockIdx.x & 1) : blockIdx.x / head_groups;
   const int hs = wave & 3;
   const int kvh = hgrp * 4 + hs;
   const HalfRows map{kvh, a.rows, a.hkv, 32 * (wave >> 2)};
@@ -1402,6 +1430,9 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   }
   __syncthreads();  // sm_ids written
 
+  // Paired items: the page loop's time (100 MHz counter) for the merge kernel's
+  // choice of the next call's item sizes.
+  const unsigned long long t_loop = it.paired ? __builtin_amdgcn_s_memrealtime() : 0;
   int next_pid = sm_ids[D];
   for (int i = 0; i < n_split; i += D) {
 #pragma unroll
@@ -1435,6 +1466,11 @@ void sqa_partial_lds_kernel(PartialArgs a) {
       }
     }
   }
+  if (it.paired && threadIdx.x == 0) {
+    const unsigned long long ticks = __builtin_amdgcn_s_memrealtime() - t_loop;
+    *(int2*)(a.tune + 4 + 2 * blockIdx.x) =
+        int2{__float_as_int((float)ticks), n_split | (item & 1) << 30 | 1 << 31};
+  }
   // Loads past the piece still write (zeros) into the ring: drain them before
   // the ring becomes the output staging.
   wait_vmcnt<0>();
@@ -1465,6 +1501,60 @@ __device__ __forceinline__ SeqSplits in_range(SeqSplits t, int num_splits) {
   return t;
 }
 
+// Paired items: the next call's delta from this call's page-loop times (one
+// workgroup of 256 threads). Even items took P + d pages, odd ones P - d; with
+// per-page times t_e and t_o the two end together at delta = (t_o - t_e) /
+// (t_o + t_e), whatever this call's delta was. The new value moves halfway
+// there (one call's times are noisy), within +-kPairDeltaMax.
+__device__ __noinline__ void update_pair_delta(float* tune, int records) {
+  __shared__ float sums[4][4];
+  const int t = threadIdx.x;
+  float te = 0.f, pe = 0.f, to = 0.f, po = 0.f;
+  for (int i = t; i < records; i += 256) {
+    const int2 r = *(const int2*)(tune + 4 + 2 * i);
+    if (r.y < 0) {  // recorded by this call's partial kernel
+      const float pages = (float)(r.y & 0x3fffffff);
+      const float ticks = __int_as_float(r.x);
+      if ((r.y >> 30) & 1) {
+        to += ticks;
+        po += pages;
+      } else {
+        te += ticks;
+        pe += pages;
+      }
+    }
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    te += __shfl_xor(te, o);
+    pe += __shfl_xor(pe, o);
+    to += __shfl_xor(to, o);
+    po += __shfl_xor(po, o);
+  }
+  if ((t & 63) == 0) {
+    sums[t >> 6][0] = te;
+    sums[t >> 6][1] = pe;
+    sums[t >> 6][2] = to;
+    sums[t >> 6][3] = po;
+  }
+  __syncthreads();
+  if (t == 0) {
+    te = sums[0][0] + sums[1][0] + sums[2][0] + sums[3][0];
+    pe = sums[0][1] + sums[1][1] + sums[2][1] + sums[3][1];
+    to = sums[0][2] + sums[1][2] + sums[2][2] + sums[3][2];
+    po = sums[0][3] + sums[1][3] + sums[2][3] + sums[3][3];
+    if (pe > 0.f && po > 0.f && te > 0.f && to > 0.f) {
+      const float ue = te / pe, uo = to / po;
+      const float target = (uo - ue) / (uo + ue);
+      float old = __float_as_uint(tune[0]) == kTuneMagic ? tune[1] : 0.f;
+      old = old == old ? fminf(fmaxf(old, -kPairDeltaMax), kPairDeltaMax) : 0.f;
+      tune[1] = fminf(fmaxf(0.5f * (old + target), -kPairDeltaMax), kPairDeltaMax);
+      tune[0] = __uint_as_float(kTuneMagic);
+    }
+  }
+  // Records are marked as read: a later call that writes none changes nothing.
+  for (int i = t; i < records; i += 256) tune[4 + 2 * i + 1] = 0.f;
+}
+
 template <int TPR, int HD, typename E, int U>
 __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   constexpr int CH = HD / 4;       // 4-dim chunks of a row
@@ -1479,6 +1569,7 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   const int row = blockIdx.x * RPW + t / TPR;
   const int total = a.batch * a.q_len * a.hq;
   const bool live = row < total;  // uniform per row
+  if (a.tune != nullptr && blockIdx.x == 0) update_pair_delta(a.tune, a.tune_records);
   const int rowc = live ? row : 0;
   const int h = rowc % a.hq;
   const int qi = (rowc / a.hq) % a.q_len;

@@ -53,12 +53,15 @@ def test_workspace_bytes(lib):
     assert lib.sqa_workspace_bytes(1, 2, 32, 8, 128, 3, 4) == 1 * 8 * 3 * 8 * 130 * 4
     assert lib.sqa_workspace_bytes(0, 2, 32, 8, 128, 3, 4) == 0
     # Balanced plan (pages_per_split 0): num_splits slots shared by the batch,
-    # plus one (first slot, count) pair of int32 per sequence.
-    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 128, 272, 0) == 272 * 8 * 32 * 130 * 4 + 16 * 8
-    assert lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 1, 0) == 1 * 8 * 8 * 130 * 4 + 2 * 8
+    # plus one (first slot, count) pair of int32 per sequence, the paired items'
+    # 16-byte delta record and two 8-byte loop-time records per slot.
+    assert lib.sqa_workspace_bytes(16, 8, 32, 8, 128, 272, 0) == \
+        272 * 8 * 32 * 130 * 4 + 16 * 8 + 16 + 272 * 16
+    assert lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 1, 0) == \
+        1 * 8 * 8 * 130 * 4 + 2 * 8 + 16 + 16
     # -P: the balanced plan expecting P pages per sequence; the same workspace.
     assert lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 3, -7) == \
-        lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 3, 0) == 3 * 8 * 8 * 130 * 4 + 2 * 8
+        lib.sqa_workspace_bytes(2, 2, 32, 8, 128, 3, 0) == 3 * 8 * 8 * 130 * 4 + 2 * 8 + 16 + 48
     # Other head dims: head_dim + 2 floats per item.
     assert lib.sqa_workspace_bytes(1, 2, 32, 8, 64, 3, 4) == 1 * 8 * 3 * 8 * 66 * 4
     assert lib.sqa_workspace_bytes(1, 2, 32, 8, 256, 3, 4) == 1 * 8 * 3 * 8 * 258 * 4
