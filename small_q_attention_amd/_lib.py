@@ -225,7 +225,7 @@ def run(query, key_cache, value_cache, block_tables, seq_lens, num_splits: int,
     b, q_len, hq, d = query.shape
     nbytes = workspace_bytes(b, q_len, hq, key_cache.shape[2], d, num_splits, pages_per_split)
     stream = raw_stream(query.device.index)
-    ws = workspace_for(nbytes, query.device, query.device.index, stream) if nbytes else None
+    ws = workspace_for(nbytes, query, query.device.index, stream) if nbytes else None
     if query.dtype == torch.float16:
         launch(query, key_cache, value_cache, block_tables, seq_lens, out, ws, num_splits,
                pages_per_split, stream)
@@ -241,21 +241,37 @@ def run(query, key_cache, value_cache, block_tables, seq_lens, num_splits: int,
 # belong to the graph's pool), allocate their own.
 WORKSPACE_CACHE_BYTES = 64 << 20
 _WORKSPACES = {}
+_CUDA_STATE = None  # (current device, current stream capturing): torch's own query functions
 
 
-def workspace_for(nbytes: int, device, device_index: int, stream_handle: int):
-    """A workspace of at least ``nbytes`` for a call on ``stream_handle``."""
+def _cuda_state(torch):
+    """The functions behind ``torch.cuda.current_device`` and
+    ``torch.cuda.is_current_stream_capturing`` without their per-call
+    initialisation checks (callers hold a CUDA tensor, so CUDA is initialised);
+    the public ones where this torch lacks them."""
+    global _CUDA_STATE
+    if _CUDA_STATE is None:
+        c = torch._C
+        _CUDA_STATE = (getattr(c, "_cuda_getDevice", None) or torch.cuda.current_device,
+                       getattr(c, "_cuda_isCurrentStreamCapturing", None)
+                       or torch.cuda.is_current_stream_capturing)
+    return _CUDA_STATE
+
+
+def workspace_for(nbytes: int, like, device_index: int, stream_handle: int):
+    """A workspace of at least ``nbytes`` for a call on ``stream_handle`` (``like``: a
+    tensor on the call's device)."""
     import torch
 
+    current_device, capturing = _CUDA_STATE or _cuda_state(torch)
     # The capture check reads the current device's stream: the cache serves only
     # calls on that device.
-    if (nbytes > WORKSPACE_CACHE_BYTES or device_index != torch.cuda.current_device()
-            or torch.cuda.is_current_stream_capturing()):
-        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    if nbytes > WORKSPACE_CACHE_BYTES or device_index != current_device() or capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=like.device)
     key = (device_index, stream_handle)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=like.device)
         _WORKSPACES[key] = ws
     return ws
 
@@ -271,7 +287,7 @@ def run_fp16(query, key_cache, value_cache, block_tables, seq_lens, batch: int, 
     nbytes = workspace_bytes(batch, q_len, num_query_heads, num_kv_heads, 128, num_splits,
                              pages_per_split)
     stream = raw_stream(device_index)
-    ws = workspace_for(nbytes, query.device, device_index, stream) if nbytes else None
+    ws = workspace_for(nbytes, query, device_index, stream) if nbytes else None
     rc = _LIB.sqa_paged_mtp_attention(
         query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
         block_tables.data_ptr(), seq_lens.data_ptr(), out.data_ptr(),
