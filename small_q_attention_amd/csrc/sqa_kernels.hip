@@ -800,7 +800,10 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
         load_lengths(a, pb.len);
         float dl = __float_as_uint(rec.x) == kTuneMagic ? rec.y : 0.f;
         dl = dl == dl ? fminf(fmaxf(dl, -kPairDeltaMax), kPairDeltaMax) : 0.f;
-        const int d = __builtin_amdgcn_readfirstlane((int)rintf((float)pb.P * dl));
+        // Both items of a pair stay within kMaxSplitPages (the page-id table).
+        const int dmax = kMaxSplitPages - pb.P;
+        const int d = __builtin_amdgcn_readfirstlane(
+            min(max((int)rintf((float)pb.P * dl), -dmax), dmax));
         g0 = (item >> 1) * 2 * pb.P + ((item & 1) ? pb.P + d : 0);
         item_end = (item >> 1) * 2 * pb.P + ((item & 1) ? 2 * pb.P : pb.P + d);
       }

@@ -12,7 +12,9 @@ depend on delta:
 * after each call the record holds the magic word and a delta within the
   bound, and every loop-time record has been consumed (marked read);
 * calls in a row (delta moving between them) stay within tolerance and the
-  delta stays bounded.
+  delta stays bounded;
+* items of the largest size (2048 pages) hold the shift to 0 whatever the
+  record says, so neither item of a pair outgrows the page-id table.
 """
 
 import struct
@@ -99,3 +101,25 @@ def test_paired_items_any_delta(qdt, page, tree):
         assert_parity(out, ref, label=f"own delta, call {i}")
         m, d, _ = _record(ws, off, ns, batch)
         assert m == MAGIC and abs(d) <= 0.1 + 1e-7
+
+
+def test_paired_items_at_the_item_size_limit():
+    """Items of the largest size (2048 pages) with delta forced to its bound: the
+    shift is held to 0 so that neither item of a pair exceeds the page-id table."""
+    from tests._helpers import torch_fp32_reference
+
+    q_len, batch, seq_pages, n_items = 16, 2, 4096, 4  # P = 2048
+    lens = [seq_pages * 16] * batch
+    case = inputs.Case(batch=batch, q_len=q_len, seq_lens=lens, seed=1850)
+    q, k, v, bt, sl = inputs.make_inputs(case, device="cuda", gen_device="cuda")
+    ns, pps = batch + n_items, -seq_pages
+    ws = torch.zeros(_lib.workspace_bytes(batch, q_len, HQ, HKV, HD, ns, pps), dtype=torch.uint8,
+                     device="cuda")
+    off = _tune_offset(batch, q_len, ns)
+    _seed(ws, off, MAGIC, 0.1)
+    out = torch.full_like(q, float("nan"))
+    _lib.launch_general(q, out, k, v, bt, sl, None, HD ** -0.5, 1.0, ns, pps, ws,
+                        torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref = torch_fp32_reference(q, k, v, bt, sl, 16, HKV)
+    assert_parity(out, ref, label="P = 2048, delta 0.1")
