@@ -290,14 +290,15 @@ int run_attention(const sqa_attention_args& a) {
   pa.spec_pps =
       spec_pages > 0 ? sqa::packed_item_pages(batch * spec_pages, num_splits - batch) : 0;
   pa.seam_pages = balanced ? sqa::seam_pages((int)rows, num_kv_heads, head_dim, (int)kv_bytes) : 0;
-  // Paired items: the 64-row kernel (33..64 rows, head dim 128, 16-bit K/V)
-  // with two head groups of four kv heads, an expected page count that pairs
-  // of items divide, and an even item count.
+  // Paired items: the 64-row kernel (33..64 rows, head dim 128) with fp16 Q, K
+  // and V (bf16 measured 0.2-0.7% slower with them: more math per page, and fp32
+  // partials), two head groups of four kv heads, an expected page count that
+  // pairs of items divide, and an even item count.
   pa.tune = balanced ? (float*)(pa.seq_splits + batch) : nullptr;
   pa.pair_items = balanced && spec_pages > 0 && pa.spec_pps > 0 &&
                   spec_pages % (2 * pa.spec_pps) == 0 && (num_splits - batch) % 2 == 0 &&
-                  head_dim == 128 && kv_bytes == 2 && rows > 32 && rows <= 64 &&
-                  num_kv_heads == 8;
+                  head_dim == 128 && kv_bytes == 2 && a.dtype == SQA_DTYPE_F16 && rows > 32 &&
+                  rows <= 64 && num_kv_heads == 8;
   pa.scale_log2 = (float)(1.4426950408889634 * (double)a.scale);
   pa.out_scale = a.out_scale;
   pa.bf16 = a.dtype == SQA_DTYPE_BF16;
