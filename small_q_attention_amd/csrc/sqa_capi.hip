@@ -291,7 +291,7 @@ int run_attention(const sqa_attention_args& a) {
       spec_pages > 0 ? sqa::packed_item_pages(batch * spec_pages, num_splits - batch) : 0;
   pa.seam_pages = balanced ? sqa::seam_pages((int)rows, num_kv_heads, head_dim, (int)kv_bytes) : 0;
   // Paired items: the 64-row kernel (33..64 rows, head dim 128) with fp16 Q, K
-  // and V (bf16 measured 0.2-0.7% slower with them: more math per page, and fp32
+  // and V (bf16 measured 0.2-1.4% slower with them: more math per page, and fp32
   // partials), two head groups of four kv heads, an expected page count that
   // pairs of items divide, and an even item count.
   pa.tune = balanced ? (float*)(pa.seq_splits + batch) : nullptr;
