@@ -192,11 +192,15 @@ inline LaunchShape launch_shape(int rows, int hkv, int head_dim) {
 // own: ~5.6 us measured at 16 ragged sequences of 2K-32K tokens (q_len 8, head
 // dim 128, fp16), where one page of the workgroup's (16 tokens of K and V for 4
 // kv heads, 32 KiB) takes ~1.15 us; scaled by the bytes of a workgroup's page
-// for other shapes and element types.
+// for other shapes and element types. The 8-wave LDS kernel (33..64 rows, head
+// dim 128, 16-bit K/V) restarts a ring behind two barriers per page and writes
+// 64 rows per head: 8 pages measured best there (ragged q16 fp16 190.2 -> 187.8
+// us, bf16 194.4 -> 190.2; 12 pages 187.8 / 190.8).
 inline int seam_pages(int rows, int hkv, int head_dim, int kv_bytes) {
   const LaunchShape sh = launch_shape(rows, hkv, head_dim);
   const int wg_page = 16 * sh.heads * head_dim * 2 * kv_bytes;
-  const int c = (5 * 32768 + wg_page / 2) / wg_page;
+  const int cost = head_dim == 128 && kv_bytes == 2 && rows > 32 ? 8 : 5;
+  const int c = (cost * 32768 + wg_page / 2) / wg_page;
   return c < 1 ? 1 : (c > 32 ? 32 : c);
 }
 

@@ -119,8 +119,10 @@ def _plan_table(ws, tensors, ns):
 
 
 # Seam gap of the balanced plan at head dim 128 with 16-bit K/V (four kv heads, a
-# 32 KiB page per workgroup): what a second piece costs a workgroup, in pages.
+# 32 KiB page per workgroup): what a second piece costs a workgroup, in pages;
+# 8 for the 8-wave kernel of 33..64 rows (q_len 16 at GQA 4).
 SEAM_PAGES = 5
+SEAM_PAGES_64_ROWS = 8
 
 
 def _packed_layout(lens, items, page=16, seam=SEAM_PAGES):
@@ -163,7 +165,8 @@ def test_packed_items_cross_sequences(q_len):
         out, ws = _run(ragged, ns, 0)
         assert_parity(out, ref, label=f"ragged items {n_items} q{q_len}")
         assert torch.all(out[3] == 0) and torch.all(out[17] == 0)
-        _, slots = _packed_layout(lens, n_items)
+        _, slots = _packed_layout(lens, n_items,
+                                  seam=SEAM_PAGES_64_ROWS if q_len * 4 > 32 else SEAM_PAGES)
         table = _plan_table(ws, ragged, ns)
         used = []
         for b, (first, count) in enumerate(table):
