@@ -412,6 +412,26 @@ __device__ __forceinline__ void page_scores(f4 (&s)[NB], const PageK<HD, HPW>& k
 // t < len is seen by a row when it lies before the draft block
 // (t < draft_base = len - q_len) or when bit t - draft_base of the row's draft
 // bits is set.
+// Scores of tokens a row does not see set to -inf; tok0 = absolute index of
+// this lane's first token (4 consecutive tokens).
+template <int NB>
+__device__ __forceinline__ void mask_scores(f4 (&s)[NB], const unsigned long long (&dbits)[NB],
+                                            int draft_base, int tok0, int len) {
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // Bitwise, not short-circuit, logic: one select per score, no
+      // lane-divergent control flow around the scores.
+      const int t = tok0 + e;
+      const int j = t - draft_base;  // < q_len <= 64 whenever t < len
+      const unsigned bit = (unsigned)(dbits[nb] >> (j & 63)) & 1u;
+      const unsigned seen = (unsigned)(t < len) & ((unsigned)(j < 0) | bit);
+      s[nb][e] = seen ? s[nb][e] : -INFINITY;
+    }
+  }
+}
+
 template <int NB, int HD, typename E, typename KV, int HPW>
 __device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
                                             PageV<HD, HPW>& pv, bool upper,
@@ -420,20 +440,7 @@ __device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
                                             float c) {
   constexpr int MB = Dims<HD>::MB, VW = Dims<HD>::VW;
   if (masked) {
-    // tok0 = absolute index of this lane's first token (4 consecutive tokens).
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // Bitwise, not short-circuit, logic: one select per score, no
-        // lane-divergent control flow around the scores.
-        const int t = tok0 + e;
-        const int j = t - draft_base;  // < q_len <= 64 whenever t < len
-        const unsigned bit = (unsigned)(dbits[nb] >> (j & 63)) & 1u;
-        const unsigned seen = (unsigned)(t < len) & ((unsigned)(j < 0) | bit);
-        s[nb][e] = seen ? s[nb][e] : -INFINITY;
-      }
-    }
+    mask_scores<NB>(s, dbits, draft_base, tok0, len);
     // V rows past the sequence end may hold anything (even NaN); 0 * NaN would
     // poison the product, so zero them.
 #pragma unroll
@@ -503,6 +510,98 @@ __device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
         st.acc[mb][nb] =
             E::mma_pv(av, mine ? ph[nb] : zero, mine ? pl[nb] : zero, st.acc[mb][nb]);
       }
+    }
+  }
+}
+
+// Two pages in one softmax step: fp16 queries over an e4m3 cache at head dim
+// 128, one kv head per wave (the 64-row kernel, where the math, not the bytes,
+// sets the time). s0 / s1: the raw scores of pages p and p + 1; r0 / r1 their
+// raw K/V registers. One running-max update covers the 32 tokens, and each PV
+// product is one v_mfma_f32_16x16x32_f16 over both pages (k-slots 0-3 of a lane
+// group take its four tokens of page p, slots 4-7 the same tokens of page
+// p + 1), which costs the cycles of one 16x16x16 product over one page: half
+// the PV MFMA time. V is widened per dim block from its bytes, after the bytes
+// of tokens past the sequence end are zeroed (they may hold NaN). have1 false:
+// page p + 1 is past the piece (its slot holds a zero page); its scores become
+// -inf. Same sums as two page_finish steps up to fp32 rounding and the point
+// at which the lagging max is raised.
+template <int NB>
+__device__ __forceinline__ void pair_finish(WaveState<NB, 128>& st, f4 (&s0)[NB], f4 (&s1)[NB],
+                                            KvFp8<128>::Regs r0, KvFp8<128>::Regs r1,
+                                            bool have1, const unsigned long long (&dbits)[NB],
+                                            int draft_base, int tok0, int len, bool masked,
+                                            float c) {
+  using E = ElemF16;
+  constexpr int MB = Dims<128>::MB;
+  if (masked) {
+    mask_scores<NB>(s0, dbits, draft_base, tok0, len);
+    mask_scores<NB>(s1, dbits, draft_base, tok0 + kPageSize, len);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (tok0 + e >= len) r0.v[e][0] = r0.v[e][1] = 0u;
+      if (tok0 + kPageSize + e >= len) r1.v[e][0] = r1.v[e][1] = 0u;
+    }
+  }
+  if (!have1) {  // uniform over the wave
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) s1[nb] = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  }
+
+  float lm[NB];
+  bool grow = false;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    lm[nb] = fmaxf(max4(s0[nb]), max4(s1[nb])) * c;
+    grow |= lm[nb] > st.m[nb] + kMaxLag;
+  }
+  if (__any(grow)) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const float mn = fmaxf(st.m[nb], xor_max(lm[nb]));
+      const float alpha = fast_exp2(st.m[nb] - (mn == -INFINITY ? 0.f : mn));
+      st.m[nb] = mn;
+      st.l[nb] *= alpha;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) st.acc[mb][nb] *= alpha;
+    }
+  }
+
+  u4 pp[NB];  // P^T of both pages: this lane's 4 tokens of page p, then of p + 1
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const float mu = st.m[nb] == -INFINITY ? 0.f : st.m[nb];
+    u2 unused;
+    const u2 a0 = E::round_p(fast_exp2(fmaf(s0[nb][0], c, -mu)), fast_exp2(fmaf(s0[nb][1], c, -mu)),
+                             fast_exp2(fmaf(s0[nb][2], c, -mu)), fast_exp2(fmaf(s0[nb][3], c, -mu)),
+                             st.l[nb], unused);
+    const u2 a1 = E::round_p(fast_exp2(fmaf(s1[nb][0], c, -mu)), fast_exp2(fmaf(s1[nb][1], c, -mu)),
+                             fast_exp2(fmaf(s1[nb][2], c, -mu)), fast_exp2(fmaf(s1[nb][3], c, -mu)),
+                             st.l[nb], unused);
+    pp[nb] = u4{a0[0], a0[1], a1[0], a1[1]};
+  }
+
+  // Dim block mb takes half mb%2 of widened dword mb/2 of the lane's four token
+  // rows of each page (dword j of a token row is e4m3 dword j/2, half j%2).
+#pragma unroll
+  for (int j = 0; j < MB / 2; ++j) {
+    unsigned w0[4], w1[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w0[e] = E::widen_fp8x4(r0.v[e][j >> 1])[j & 1];
+      w1[e] = E::widen_fp8x4(r1.v[e][j >> 1])[j & 1];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int mb = 2 * j + h;
+      const u4 av = h == 0 ? u4{pack_lo(w0[0], w0[1]), pack_lo(w0[2], w0[3]),
+                                pack_lo(w1[0], w1[1]), pack_lo(w1[2], w1[3])}
+                           : u4{pack_hi(w0[0], w0[1]), pack_hi(w0[2], w0[3]),
+                                pack_hi(w1[0], w1[1]), pack_hi(w1[2], w1[3])};
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        st.acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            __builtin_bit_cast(h8, av), __builtin_bit_cast(h8, pp[nb]), st.acc[mb][nb], 0, 0, 0);
     }
   }
 }
@@ -1172,8 +1271,35 @@ void sqa_partial_kernel(PartialArgs a) {
   // and at one block there is little softmax to hide (e4m3 head dim 64 q4:
   // -1.5%).
   constexpr bool kPipelined = NB >= 2 && D >= 3 && NB * HD <= 256;
+  // fp16 queries over an e4m3 cache at 64 rows and head dim 128 take the
+  // pages two at a time (pair_finish).
+  constexpr bool kPairSteps = __is_same(E, ElemF16) && KV::kBytes == 1 && HD == 128 &&
+                              NB == 4 && HPW == 1 && D % 2 == 0;
   const bool upper = l16 >= 8;
   int next_pid = page_id(D);
+  if constexpr (kPairSteps) {
+    for (int i = 0; i < n_pages; i += D) {
+#pragma unroll
+      for (int j = 0; j < D; j += 2) {
+        const int ii = i + j;
+        if (ii < n_pages) {
+          const int p = p_begin + ii;
+          const bool masked = (p + 2) * kPageSize > mask_from;
+          f4 s0[NB], s1[NB];
+          page_scores<NB, HD, E, KV, 1>(s0, widen_k<E, KV, HD, 1>(ring[j]), my_q, lane, upper);
+          page_scores<NB, HD, E, KV, 1>(s1, widen_k<E, KV, HD, 1>(ring[j + 1]), my_q, lane,
+                                        upper);
+          pair_finish<NB>(st, s0, s1, ring[j][0], ring[j + 1][0], ii + 1 < n_pages, dbits,
+                          mask_from, p * kPageSize + 4 * g16, len, masked, a.scale_log2);
+        }
+        const int pid0 = next_pid;
+        const int pid1 = page_id(ii + D + 1);
+        next_pid = page_id(ii + D + 2);
+        load_page(pid0, p_begin + ii + D, ring[j]);
+        load_page(pid1, p_begin + ii + D + 1, ring[j + 1]);
+      }
+    }
+  } else {
   f4 s_cur[NB];
   if constexpr (kPipelined)
     page_scores<NB, HD, E, KV, HPW>(s_cur, widen_k<E, KV, HD, HPW>(ring[0]), my_q, lane, upper);
@@ -1208,6 +1334,7 @@ void sqa_partial_kernel(PartialArgs a) {
       next_pid = page_id(ii + D + 1);
       load_page(pid, p_begin + ii + D, ring[j]);
     }
+  }
   }
   if (active)
     write_results<NB, HD, E>(a, st, sm_stage + wave * 16 * (HD + 4), map, direct,
@@ -1742,7 +1869,10 @@ template <int HD, typename E, typename KV>
 void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
                        hipStream_t stream) {
   constexpr int D4 = 4 * 128 / HD, D2 = 2 * 128 / HD;
-  constexpr int D3 = KV::kBytes == 1 ? (HD == 128 ? 2 : 3) : (HD == 64 ? 4 : 3 * 128 / HD);
+  // e4m3 at head dim 128: 2 pages, or 4 under fp16 queries, whose pair steps
+  // (pair_finish) need a second pair in flight while one is computed.
+  constexpr int D3 = KV::kBytes == 1 ? (HD == 128 ? (__is_same(E, ElemF16) ? 4 : 2) : 3)
+                                     : (HD == 64 ? 4 : 3 * 128 / HD);
   if (sh.hpw == 2) {
     // Two heads per wave: half the pages in flight, each twice the bytes.
     if constexpr (HD == 64) {

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import attention_c64
-from small_q_attention_amd import decode_api as fi, inputs
+from small_q_attention_amd import _lib, decode_api as fi, inputs
 from small_q_attention_amd.masks import pack_draft_mask
 from tests._helpers import assert_parity, compact_sequences
 
@@ -79,6 +79,37 @@ def test_fp8_cache_masks_hnd_and_large_pages():
     out = _xqa(q, hnd, bt, sl, q_len, ws, kv_layout="HND", mask=mask.cuda())
     ref = attention_c64(q.cpu(), k8.cpu(), v8.cpu(), bt.cpu(), sl.cpu(), 32, 8, draft_mask=mask)
     assert_parity(out, ref, label="fp8 HND p32 tree")
+
+
+@pytest.mark.parametrize("chunk", [None, 16, 48, 1 << 20])
+def test_fp8_64_rows_page_pairs(chunk):
+    """64 rows per kv head (q_len 16, GQA 4) over an e4m3 cache under fp16 queries
+    take the pages two at a time. Plans with 1- and 3-page splits leave a last
+    pair without its second page; the lengths put the draft block and the
+    sequence end on either page of a pair; the draft mask is a random tree, and
+    the unused slots of every last page hold e4m3 NaN bytes."""
+    q_len, lens = 16, [16, 17, 31, 32, 33, 47, 48, 49, 300, 1111]
+    c = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=1400 + (chunk or 0) % 97)
+    q, k, v, bt, sl = inputs.make_inputs(c)
+    kb, vb = k.to(F8).view(torch.uint8).clone(), v.to(F8).view(torch.uint8).clone()
+    for b, n in enumerate(lens):
+        last = int(bt[b, (n - 1) // 16])
+        if n % 16:
+            kb[last, n % 16:] = 0x7F  # e4m3 NaN
+            vb[last, n % 16:] = 0x7F
+    k8, v8 = kb.view(F8), vb.view(F8)
+    g = torch.Generator().manual_seed(14)
+    vis = torch.rand(len(lens), q_len, q_len, generator=g) < 0.5
+    vis[:, torch.arange(q_len), torch.arange(q_len)] = True
+    mask = pack_draft_mask(vis)
+    plan = None if chunk is None else _lib.plan_splits(0, len(lens), q_len, 32, 8, 128,
+                                                       max(lens), bt.shape[1], chunk)
+    # No workspace buffer: the entry sizes it for the plan (1-page splits need ~190 MB).
+    out = fi._run(q.cuda().reshape(-1, 32, 128), k8.cuda(), v8.cuda(), bt.cuda(), sl.cuda(),
+                  max(lens), q_len, 128 ** -0.5, 1.0, mask.cuda(), None, None, plan=plan)
+    torch.cuda.synchronize()
+    ref = attention_c64(q, k8, v8, bt, sl, 16, 8, draft_mask=mask)
+    assert_parity(out.view_as(q), ref, label=f"e4m3 q16 pairs ck{chunk}")
 
 
 def test_fp8_full_size():
