@@ -1921,17 +1921,19 @@ void launch_merge_hd(const MergeArgs& a, int per_row, hipStream_t stream) {
   // rounds of loads; a workgroup per row beyond that. Rows whose splits fit one
   // round of 4 loads per thread take that round (half the load instructions of
   // the 8-load round, whose extra slots would reload split 0 for nothing).
-  // Under 1024 rows a wave per row leaves most CUs idle (256 workgroups of 4
-  // rows at most) while each wave waits out two rounds: a workgroup per row
-  // takes up to 4 * 256 / (HD / 4) splits in one round of 4 loads (B4 KV 8K,
-  // 32 splits per row, whole call: q2 30.7 -> 29.2 us, q4 31.2 -> 30.5 us).
+  // Under 1024 rows, where a wave per row needs its second round, it leaves
+  // most CUs idle (256 workgroups of 4 rows at most) while each wave waits out
+  // both: a workgroup per row takes up to 4 * 256 / (HD / 4) splits in one
+  // round of 4 loads (B4 KV 8K, 32 splits per row, whole call: q2 30.7 -> 29.2
+  // us, q4 31.2 -> 30.5 us). Rows that fit one round stay with a wave (B1 KV
+  // 1K, 16 splits per row: merge 3.4 us, 3.7 us a workgroup per row).
   constexpr int kGroups = 64 / (HD / 4);
   constexpr int kWgGroups = 256 / (HD / 4);
   const int total = a.batch * a.q_len * a.hq;
   const dim3 waves((unsigned)((total + 3) / 4));
   if (per_row <= 4 * kGroups) {
     hipLaunchKernelGGL((sqa_merge_kernel<64, HD, E, 4>), waves, dim3(256), 0, stream, a);
-  } else if (per_row <= 2 * 8 * kGroups && total >= 1024) {
+  } else if (per_row <= 2 * 8 * kGroups && (total >= 1024 || per_row <= 8 * kGroups)) {
     hipLaunchKernelGGL((sqa_merge_kernel<64, HD, E, 8>), waves, dim3(256), 0, stream, a);
   } else if (per_row <= 4 * kWgGroups) {
     hipLaunchKernelGGL((sqa_merge_kernel<256, HD, E, 4>), dim3((unsigned)total), dim3(256), 0,
