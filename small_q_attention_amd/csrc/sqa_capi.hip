@@ -107,11 +107,16 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
     }
     const long long splits = ceil_div(slots_target, batch);
     pps = ceil_div(pages, splits);
-    // Each split writes rows x (head_dim + 2) floats per kv head for the merge;
-    // past 16 rows that rivals a 4-page split's K/V bytes, so splits start at
-    // 8 pages there (single-sequence batches of a few thousand tokens).
+    // Each split leaves a partial row per query row for the merge. Past 16
+    // rows, sequences of more than 64 four-page splits start at 8 pages: there
+    // the merge of the extra splits costs more than the shorter splits save
+    // (one sequence, KV 8K, per call: q8 21.4 us at 64 x 8 pages, 22.4 at 128
+    // x 4; q16 25.7 / 28.3), while shorter ones gain from 4 (KV 1K-4K, q8 and
+    // q16: 0.6-2.5 us per call).
     const bool past16 = (long long)q_len * (num_query_heads / num_kv_heads) > 16;
-    const long long min_pps = past16 ? 2 * sqa::kMinSplitPages : sqa::kMinSplitPages;
+    const long long min_pps = past16 && pages > 64 * sqa::kMinSplitPages
+                                  ? 2 * sqa::kMinSplitPages
+                                  : sqa::kMinSplitPages;
     if (pps < min_pps) pps = min_pps;
   }
   if (pps > pages) pps = pages;
