@@ -73,11 +73,11 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
  * Device workspace bytes sqa_paged_mtp_attention needs for a plan from
  * sqa_plan_splits and a head_dim (0 for a fixed plan with num_splits == 1). Replaces the
  * per-call torch::empty of the partial buffers in the reference launchers
- * (csrc/small_q_attention_ext.cu:1102-1104). A balanced plan's workspace also
- * carries a small record from call to call (measured page-loop times of the
- * 64-row kernel, which set the next call's work-item sizes); whatever it holds,
- * including uninitialised memory, results are the same, so a fresh or reused
- * workspace is equally valid.
+ * (csrc/small_q_attention_ext.cu:1102-1104). A fresh (even uninitialised) or
+ * reused workspace is equally valid: without SQA_FLAG_ADAPTIVE_PAIRS no call
+ * reads what an earlier call left in it, and the same inputs and plan give the
+ * same output bits on every call. A balanced plan's workspace also holds a small
+ * record that only calls with SQA_FLAG_ADAPTIVE_PAIRS use (see there).
  */
 size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv_heads,
                            int head_dim, int num_splits, int pages_per_split);
@@ -174,7 +174,22 @@ typedef struct sqa_kv_cache {
  *               one byte per element (strides still count elements), widened
  *               exactly to dtype in registers; per-tensor K / V scales go into
  *               scale / out_scale.
+ *   flags       0, or SQA_FLAG_ADAPTIVE_PAIRS. A struct_size that stops
+ *               before this field (callers built against the layout without
+ *               it) means flags = 0.
  */
+
+/*
+ * SQA_FLAG_ADAPTIVE_PAIRS: let the balanced plan's 64-row fp16 kernel (33..64
+ * rows per kv head, head_dim 128, 8 kv heads, every sequence of the expected
+ * max_seq_len) move the boundary between work items 2k and 2k + 1 by a share
+ * that it measures from the previous call's page-loop times, kept in the
+ * workspace (about 1.5% faster at 16 x 32K keys, q_len 16, on boxes whose XCDs
+ * stream at different rates). The output then depends on that share within the
+ * parity tolerance, so identical calls and graph replays may differ in their last
+ * bits; without the flag they never do.
+ */
+#define SQA_FLAG_ADAPTIVE_PAIRS 1
 typedef struct sqa_attention_args {
   size_t struct_size;
   const void* query;
@@ -201,6 +216,7 @@ typedef struct sqa_attention_args {
   void** timing_events;
   int dtype;
   int kv_dtype;
+  int flags;
 } sqa_attention_args;
 
 /*

@@ -56,10 +56,12 @@ class AttentionArgs(ctypes.Structure):
                 ("head_dim", _C.c_int), ("page_size", _C.c_int), ("num_splits", _C.c_int),
                 ("pages_per_split", _C.c_int), ("workspace", _C.c_void_p),
                 ("workspace_bytes", _C.c_size_t), ("stream", _C.c_void_p),
-                ("timing_events", _C.c_void_p), ("dtype", _C.c_int), ("kv_dtype", _C.c_int)]
+                ("timing_events", _C.c_void_p), ("dtype", _C.c_int), ("kv_dtype", _C.c_int),
+                ("flags", _C.c_int)]
 
 
 DTYPE_F16, DTYPE_BF16, DTYPE_FP8_E4M3 = 0, 1, 2
+FLAG_ADAPTIVE_PAIRS = 1  # SQA_FLAG_ADAPTIVE_PAIRS
 
 
 def library_path() -> Path:
@@ -181,10 +183,11 @@ def kv_cache(k_view, v_view) -> KVCache:
 
 def launch_general(query, output, k_view, v_view, block_tables, seq_lens, draft_mask,
                    scale: float, out_scale: float, num_splits: int, pages_per_split: int,
-                   workspace, stream_handle: int, timing_events=None):
+                   workspace, stream_handle: int, timing_events=None, flags: int = 0):
     """Call ``sqa_paged_attention``. ``query``/``output``: contiguous ``[B, Q, Hq, D]``;
     ``k_view``/``v_view``: see :func:`kv_cache`; ``draft_mask``: ``None`` (causal draft
-    chain) or a contiguous 32-bit ``[B, Q, W]`` tensor of packed draft bits."""
+    chain) or a contiguous 32-bit ``[B, Q, W]`` tensor of packed draft bits; ``flags``:
+    0 or :data:`FLAG_ADAPTIVE_PAIRS`."""
     lib = _LIB if _LIB is not None else load()
     b, q_len, hq, d = query.shape
     a = AttentionArgs()
@@ -205,6 +208,7 @@ def launch_general(query, output, k_view, v_view, block_tables, seq_lens, draft_
     a.stream = stream_handle
     a.dtype = DTYPE_BF16 if str(query.dtype) == "torch.bfloat16" else DTYPE_F16
     a.kv_dtype = DTYPE_FP8_E4M3 if str(k_view.dtype) == "torch.float8_e4m3fn" else a.dtype
+    a.flags = int(flags)
     ev = None
     if timing_events is not None:
         ev = (ctypes.c_void_p * 3)(*[ctypes.c_void_p(int(e)) for e in timing_events])

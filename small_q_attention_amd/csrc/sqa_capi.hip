@@ -6,6 +6,7 @@
 
 #include <math.h>
 #include <stdarg.h>
+#include <stddef.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -215,6 +216,8 @@ int run_attention(const sqa_attention_args& a) {
                 a.mask_words);
   if (!(a.scale > 0.f) || !isfinite(a.scale) || !isfinite(a.out_scale))
     return fail(SQA_ERR_INVALID, "scale must be positive and finite, out_scale finite");
+  if (a.flags & ~SQA_FLAG_ADAPTIVE_PAIRS)
+    return fail(SQA_ERR_INVALID, "unknown flags %#x", (unsigned)a.flags);
   if (num_splits <= 0) return fail(SQA_ERR_INVALID, "num_splits must be positive");
   if (pages_per_split > sqa::kMaxSplitPages)
     return fail(SQA_ERR_INVALID, "pages_per_split %d exceeds %d", pages_per_split,
@@ -295,12 +298,13 @@ int run_attention(const sqa_attention_args& a) {
   pa.spec_pps =
       spec_pages > 0 ? sqa::packed_item_pages(batch * spec_pages, num_splits - batch) : 0;
   pa.seam_pages = balanced ? sqa::seam_pages((int)rows, num_kv_heads, head_dim, (int)kv_bytes) : 0;
-  // Paired items: the 64-row kernel (33..64 rows, head dim 128) with fp16 Q, K
-  // and V (bf16 measured 0.2-1.4% slower with them: more math per page, and fp32
+  // Paired items, on request only (they make the output depend on measured
+  // times): the 64-row kernel (33..64 rows, head dim 128) with fp16 Q, K and V
+  // (bf16 measured 0.2-1.4% slower with them: more math per page, and fp32
   // partials), two head groups of four kv heads, an expected page count that
   // pairs of items divide, and an even item count.
   pa.tune = balanced ? (float*)(pa.seq_splits + batch) : nullptr;
-  pa.pair_items = balanced && spec_pages > 0 && pa.spec_pps > 0 &&
+  pa.pair_items = (a.flags & SQA_FLAG_ADAPTIVE_PAIRS) && balanced && spec_pages > 0 && pa.spec_pps > 0 &&
                   spec_pages % (2 * pa.spec_pps) == 0 && (num_splits - batch) % 2 == 0 &&
                   head_dim == 128 && kv_bytes == 2 && a.dtype == SQA_DTYPE_F16 && rows > 32 &&
                   rows <= 64 && num_kv_heads == 8;
@@ -411,9 +415,18 @@ extern "C" {
 
 int sqa_paged_attention(const sqa_attention_args* args) {
   if (!args) return fail(SQA_ERR_INVALID, "null argument struct");
+  // The layout before `flags` (callers built against it) runs with flags = 0.
+  constexpr size_t kLegacySize = offsetof(sqa_attention_args, flags);
+  if (args->struct_size == kLegacySize) {
+    sqa_attention_args a;
+    memset(&a, 0, sizeof(a));
+    memcpy(&a, args, kLegacySize);
+    a.struct_size = sizeof(a);
+    return run_attention(a);
+  }
   if (args->struct_size != sizeof(sqa_attention_args))
-    return fail(SQA_ERR_INVALID, "struct_size %zu does not match this library's %zu",
-                args->struct_size, sizeof(sqa_attention_args));
+    return fail(SQA_ERR_INVALID, "struct_size %zu does not match this library's %zu (or %zu)",
+                args->struct_size, sizeof(sqa_attention_args), kLegacySize);
   return run_attention(*args);
 }
 

@@ -70,9 +70,17 @@ struct SeqSplits {
 // and the access pattern, so delta is measured rather than fixed: each
 // workgroup records its page-loop time and pages, and the merge kernel sets
 // delta for the next call from the per-page times of even and odd items.
-// Any delta gives the same items' keys in some split, so results do not depend
-// on it; every workgroup of a call reads the same value.
+// Every workgroup of a call reads the same value, and any delta covers every
+// key once, so results stay within the parity tolerance; but the split point
+// changes how the fp16-normalised partials round, so the output bits follow
+// delta. Pairing therefore runs only when the caller asks for it
+// (SQA_FLAG_ADAPTIVE_PAIRS); otherwise equal inputs give equal bits.
+// Workgroup 0 of a paired call stamps tune[2] (kTuneStamp), every workgroup of
+// it writes its record, and the merge kernel reads the records only under that
+// stamp, then clears it: records of an earlier call or another shape's data in
+// a reused workspace never feed the delta.
 constexpr unsigned kTuneMagic = 0x51a7u << 16 | 1u;  // tune[0] when tune[1] holds a delta
+constexpr unsigned kTuneStamp = 0x51a7u << 16 | 2u;  // tune[2] after a call that ran paired
 constexpr float kPairDeltaMax = 0.1f;                // |delta| bound
 struct PartialArgs {
   const _Float16* q;          // [B, Q, Hq, head_dim]
@@ -103,7 +111,8 @@ struct PartialArgs {
   int spec_pps;               // the balanced plan's item size when every sequence spans spec_pages
   int seam_pages;             // balanced plan: pages a second piece costs a workgroup (0: no gaps)
   int pair_items;             // paired items on (see above)
-  float* tune;                // paired items: {magic, delta} then per workgroup {loop ticks, pages}
+  float* tune;                // paired items: {magic, delta, stamp, -} then per workgroup
+                              // {loop ticks, pages}
   float scale_log2;           // softmax scale * log2(e)
   float out_scale;            // multiplier applied to the normalised output
   int bf16;                   // element type of Q and out (and of K, V unless kv_fp8): 0 fp16, 1 bf16

@@ -846,9 +846,10 @@ struct WaveRows {
 // loaded lengths. Piece fields are the same in every lane (readfirstlane): the
 // piece, and the buffer-resource addresses built from it, stay in scalar
 // registers. Consecutive pieces are separated by a barrier (they reuse the
-// workgroup's LDS).
+// workgroup's LDS). Returns whether the item ran as a paired item (every
+// workgroup of a call returns the same).
 template <int D, typename Piece>
-__device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, Piece&& piece) {
+__device__ __forceinline__ bool for_each_piece(const PartialArgs& a, int item, Piece&& piece) {
   const int lane = threadIdx.x & 63;
   const bool balanced = is_balanced(a.pages_per_split);
   int first_id[D];
@@ -956,6 +957,7 @@ __device__ __forceinline__ void for_each_piece(const PartialArgs& a, int item, P
     piece(it, first_id);
     g = __builtin_amdgcn_readfirstlane(balanced ? it.g_end : g + 1);
   }
+  return paired;
 }
 
 // Draft bits of a row of sequence b, draft row qi: bit j = the row sees draft
@@ -1476,7 +1478,13 @@ void sqa_partial_lds_kernel(PartialArgs a) {
               16 * L::chunk_of(pos);
   }
 
-  for_each_piece<D>(a, item, [&](const ItemRange& it, const int (&first_id)[D]) {
+  // Paired items: the page loop's time (100 MHz counter) and pages, for the
+  // merge kernel's choice of the next call's item sizes (zero if the item has
+  // no piece).
+  float loop_ticks = 0.f;
+  int loop_pages = 0;
+  const bool paired_call =
+      for_each_piece<D>(a, item, [&](const ItemRange& it, const int (&first_id)[D]) {
   const int tid = piece_tid();
   const int lane = tid & 63;
   const int g16 = lane >> 4;
@@ -1560,8 +1568,6 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   }
   __syncthreads();  // sm_ids written
 
-  // Paired items: the page loop's time (100 MHz counter) for the merge kernel's
-  // choice of the next call's item sizes.
   const unsigned long long t_loop = it.paired ? __builtin_amdgcn_s_memrealtime() : 0;
   int next_pid = sm_ids[D];
   for (int i = 0; i < n_split; i += D) {
@@ -1596,10 +1602,9 @@ void sqa_partial_lds_kernel(PartialArgs a) {
       }
     }
   }
-  if (it.paired && threadIdx.x == 0) {
-    const unsigned long long ticks = __builtin_amdgcn_s_memrealtime() - t_loop;
-    *(int2*)(a.tune + 4 + 2 * blockIdx.x) =
-        int2{__float_as_int((float)ticks), n_split | (item & 1) << 30 | 1 << 31};
+  if (it.paired) {
+    loop_ticks = (float)(__builtin_amdgcn_s_memrealtime() - t_loop);
+    loop_pages = n_split;
   }
   // Loads past the piece still write (zeros) into the ring: drain them before
   // the ring becomes the output staging.
@@ -1609,6 +1614,16 @@ void sqa_partial_lds_kernel(PartialArgs a) {
     write_results<NB, HD, E>(a, st, (float*)sm_ring + wave * 16 * (HD + 4), map, direct,
                              !single && !balanced, b, slot);
   });
+  // A paired call (the same answer in every workgroup) leaves a record from
+  // every workgroup. Whenever pairing was asked for, workgroup 0 stamps the call
+  // (or clears the stamp when the lengths made it fall back): the merge kernel
+  // reads the records only under a stamp of this call.
+  if (a.pair_items && threadIdx.x == 0) {
+    if (paired_call)
+      *(int2*)(a.tune + 4 + 2 * blockIdx.x) =
+          int2{__float_as_int(loop_ticks), loop_pages | (item & 1) << 30 | 1 << 31};
+    if (blockIdx.x == 0) a.tune[2] = paired_call ? __uint_as_float(kTuneStamp) : 0.f;
+  }
 }
 
 // Log-sum-exp merge of split partials (reference: csrc/small_q_attention_ext.cu:339-366):
@@ -1635,10 +1650,14 @@ __device__ __forceinline__ SeqSplits in_range(SeqSplits t, int num_splits) {
 // workgroup of 256 threads). Even items took P + d pages, odd ones P - d; with
 // per-page times t_e and t_o the two end together at delta = (t_o - t_e) /
 // (t_o + t_e), whatever this call's delta was. The new value moves halfway
-// there (one call's times are noisy), within +-kPairDeltaMax.
+// there (one call's times are noisy), within +-kPairDeltaMax. Only after a
+// call that ran paired (its stamp in tune[2]); the stamp is cleared with the
+// records, so a later call that did not pair (a length that differs) changes
+// nothing.
 __device__ __noinline__ void update_pair_delta(float* tune, int records) {
   __shared__ float sums[4][4];
   const int t = threadIdx.x;
+  if (__float_as_uint(tune[2]) != kTuneStamp) return;  // uniform over the workgroup
   float te = 0.f, pe = 0.f, to = 0.f, po = 0.f;
   for (int i = t; i < records; i += 256) {
     const int2 r = *(const int2*)(tune + 4 + 2 * i);
@@ -1681,8 +1700,10 @@ __device__ __noinline__ void update_pair_delta(float* tune, int records) {
       tune[0] = __uint_as_float(kTuneMagic);
     }
   }
-  // Records are marked as read: a later call that writes none changes nothing.
+  // Records and stamp are marked as read: a later call that writes none changes
+  // nothing.
   for (int i = t; i < records; i += 256) tune[4 + 2 * i + 1] = 0.f;
+  if (t == 0) tune[2] = 0.f;
 }
 
 template <int TPR, int HD, typename E, int U>

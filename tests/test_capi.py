@@ -190,10 +190,28 @@ def test_general_entry_rejects_bad_arguments_without_a_gpu(lib, kw, code, msg):
 
 
 def test_general_entry_struct_matches_the_header(lib):
-    # A struct of the wrong size is refused; the right one gets past that check
-    # (and is then refused for a missing workspace, before any device access).
-    assert _general(lib, struct_size=ctypes.sizeof(_lib.AttentionArgs) - 8) == SQA_ERR_INVALID
+    # A struct of the wrong size is refused; the right one, and the layout that
+    # stops before `flags` (read as flags = 0), get past that check (and are then
+    # refused for a missing workspace, before any device access).
+    size = ctypes.sizeof(_lib.AttentionArgs)
+    legacy = _lib.AttentionArgs.flags.offset
+    assert legacy == size - 8
+    for bad in (size - 4, size + 8, legacy - 8):
+        assert _general(lib, struct_size=bad) == SQA_ERR_INVALID
+        assert "struct_size" in lib.sqa_last_error().decode()
     assert _general(lib, num_splits=2) == SQA_ERR_WORKSPACE
+    assert _general(lib, struct_size=legacy, num_splits=2) == SQA_ERR_WORKSPACE
+    # The legacy layout never reads `flags`: a junk value there is not seen.
+    assert _general(lib, struct_size=legacy, num_splits=2, flags=0x7f) == SQA_ERR_WORKSPACE
+
+
+def test_general_entry_flags(lib):
+    header = HEADER.read_text()
+    assert "#define SQA_FLAG_ADAPTIVE_PAIRS 1" in header
+    assert _lib.FLAG_ADAPTIVE_PAIRS == 1
+    assert _general(lib, flags=2) == SQA_ERR_INVALID
+    assert "flags" in lib.sqa_last_error().decode()
+    assert _general(lib, flags=_lib.FLAG_ADAPTIVE_PAIRS, num_splits=2) == SQA_ERR_WORKSPACE
 
 
 def test_noalloc_rejects_plans_beyond_its_scratch_before_any_device_call(lib):

@@ -1,4 +1,5 @@
-"""Paired items on the GPU (the 64-row kernel with the expected-page plan).
+"""Paired items on the GPU (the 64-row kernel with the expected-page plan), which
+run only under ``SQA_FLAG_ADAPTIVE_PAIRS``.
 
 Items 2k and 2k + 1 share 2P pages, the even one taking P + d and the odd one
 P - d, d = round(P * delta), with delta read from a record in the workspace that
@@ -14,7 +15,9 @@ depend on delta:
 * calls in a row (delta moving between them) stay within tolerance and the
   delta stays bounded;
 * items of the largest size (2048 pages) hold the shift to 0 whatever the
-  record says, so neither item of a pair outgrows the page-id table.
+  record says, so neither item of a pair outgrows the page-id table;
+* without the flag the record is neither read nor written: any record gives the
+  same output bits, and the record's bytes are left as they were.
 """
 
 import struct
@@ -33,6 +36,7 @@ pytestmark = pytest.mark.gpu
 
 HKV, HQ, HD = 8, 32, 128
 MAGIC = 0x51A70001  # the record's first word when its second holds a delta
+ADAPTIVE = _lib.FLAG_ADAPTIVE_PAIRS
 
 
 @pytest.fixture(autouse=True)
@@ -86,7 +90,7 @@ def test_paired_items_any_delta(qdt, page, tree):
         _seed(ws, off, magic, delta)
         out = torch.full_like(q, float("nan"))
         _lib.launch_general(q, out, k, v, bt, sl, words, HD ** -0.5, 1.0, ns, pps, ws,
-                            torch.cuda.current_stream().cuda_stream)
+                            torch.cuda.current_stream().cuda_stream, flags=ADAPTIVE)
         torch.cuda.synchronize()
         label = f"{qdt} page{page} tree={tree} delta={delta} magic={magic:#x}"
         assert_parity(out, ref, label=label)
@@ -96,7 +100,7 @@ def test_paired_items_any_delta(qdt, page, tree):
     for i in range(4):  # the delta the kernels choose for themselves
         out = torch.full_like(q, float("nan"))
         _lib.launch_general(q, out, k, v, bt, sl, words, HD ** -0.5, 1.0, ns, pps, ws,
-                            torch.cuda.current_stream().cuda_stream)
+                            torch.cuda.current_stream().cuda_stream, flags=ADAPTIVE)
         torch.cuda.synchronize()
         assert_parity(out, ref, label=f"own delta, call {i}")
         m, d, _ = _record(ws, off, ns, batch)
@@ -119,7 +123,35 @@ def test_paired_items_at_the_item_size_limit():
     _seed(ws, off, MAGIC, 0.1)
     out = torch.full_like(q, float("nan"))
     _lib.launch_general(q, out, k, v, bt, sl, None, HD ** -0.5, 1.0, ns, pps, ws,
-                        torch.cuda.current_stream().cuda_stream)
+                        torch.cuda.current_stream().cuda_stream, flags=ADAPTIVE)
     torch.cuda.synchronize()
     ref = torch_fp32_reference(q, k, v, bt, sl, 16, HKV)
     assert_parity(out, ref, label="P = 2048, delta 0.1")
+
+
+def test_without_the_flag_the_record_is_not_used():
+    """Default calls keep the usual item layout: a record forcing delta to its bound
+    changes no output bit, and neither the record nor the loop-time slots behind it
+    are touched."""
+    q_len, batch, seq_pages, n_items = 16, 2, 256, 16
+    lens = [seq_pages * 16] * batch
+    case = inputs.Case(batch=batch, q_len=q_len, seq_lens=lens, seed=1870)
+    q, k, v, bt, sl = (t.cuda() for t in inputs.make_inputs(case))
+    ns, pps = batch + n_items, -seq_pages
+    nbytes = _lib.workspace_bytes(batch, q_len, HQ, HKV, HD, ns, pps)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    off = _tune_offset(batch, q_len, ns)
+    outs = []
+    for magic, delta in [(0, 0.0), (MAGIC, 0.1), (MAGIC, -0.1)]:
+        _seed(ws, off, magic, delta)
+        ws[off + 16:off + 16 + (ns - batch) * 2 * 8] = 0x5A
+        before = ws[off:off + 16 + (ns - batch) * 2 * 8].clone()
+        out = torch.full_like(q, float("nan"))
+        _lib.launch_general(q, out, k, v, bt, sl, None, HD ** -0.5, 1.0, ns, pps, ws,
+                            torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(ws[off:off + 16 + (ns - batch) * 2 * 8], before), (magic, delta)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    ref = attention_c64(*(t.cpu() for t in (q, k, v, bt, sl)), 16, HKV)
+    assert_parity(outs[0], ref, label="flags 0")
