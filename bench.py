@@ -11,7 +11,10 @@ call (KV bytes / mean call time); ``roofline`` uses the partial kernel's own
 mean duration from HIP events the library records around it on the launch
 stream; ``cpu_baseline`` times the loop-faithful CPU oracle on a bounded
 sample of the same workload. ``per_q_len`` repeats the timing at q_len 2, 4
-and 16 on the same KV pool. ``roofline.read_probe`` is the practical read
+and 16 on the same KV pool. ``metric_grid`` times back-to-back whole calls at
+every point of BASELINE's metric (q_len 2/4/8 x KV 8K/32K x batch 1/4/16);
+``other_configs`` the other single-GPU configs (cfg1, cfg2, cfg5), with the
+committed rocprof figures beside this run's under ``rocprof_*`` keys. ``roofline.read_probe`` is the practical read
 ceiling: the streaming-read probe (``read_probe.hip``) over ~2 GiB of the same
 resident pool (``frac_of_read_probe`` = the partial kernel's rate over it).
 """
@@ -96,6 +99,8 @@ def _parse():
                     help="element types of the timed workload (profiling the other kernels): "
                          "bf16 = bf16 Q/K/V/output, e4m3 = fp16 Q/output over an OCP e4m3 "
                          "cache; fp16 (the bench line) also reports both as extras")
+    ap.add_argument("--grid-only", action="store_true",
+                    help="print only the metric grid (q_len 2/4/8 x KV 8K/32K x batch 1/4/16)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -142,7 +147,7 @@ def input_sets(inputs, case, kv_bytes):
     return sets
 
 
-def time_calls(torch, lib, sets, plan, steps, warmup):
+def time_calls(torch, lib, sets, plan, steps, warmup, kernel_events=True):
     """Time `steps` calls through the C ABI with a preallocated workspace, cycling
     through the input sets (see :func:`input_sets`).
 
@@ -151,7 +156,8 @@ def time_calls(torch, lib, sets, plan, steps, warmup):
     the library's timing events around each kernel (events between the
     kernels add a little time per call, so they stay out of the first pass and
     make the per-kernel figures upper bounds). Returns (ms per call, mean
-    partial-kernel ms, mean merge-kernel ms, output of set 0).
+    partial-kernel ms, mean merge-kernel ms, output of set 0); without
+    `kernel_events` the second pass is skipped and the kernel figures are None.
     """
     q, k = sets[0][0], sets[0][1]
     num_splits, pps = plan
@@ -174,6 +180,8 @@ def time_calls(torch, lib, sets, plan, steps, warmup):
     end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
+    if not kernel_events:
+        return total_ms / steps, None, None, outs[0]
     for i in range(steps):
         calls[i % n](outs[i % n], ws, num_splits, pps, handle,
                      timing_events=[e.cuda_event for e in kev[3 * i:3 * i + 3]])
@@ -181,6 +189,51 @@ def time_calls(torch, lib, sets, plan, steps, warmup):
     part = [kev[3 * i].elapsed_time(kev[3 * i + 1]) for i in range(steps)]
     merge = [kev[3 * i + 1].elapsed_time(kev[3 * i + 2]) for i in range(steps)]
     return total_ms / steps, statistics.mean(part), statistics.mean(merge), outs[0]
+
+
+GRID_Q_LENS = (2, 4, 8)
+GRID_KV_LENS = (8192, 32768)
+GRID_BATCHES = (1, 4, 16)
+
+
+def metric_grid(torch, lib, inputs, steps, warmup):
+    """BASELINE's metric over its whole grid: q_len 2/4/8 x KV 8K/32K x batch 1/4/16
+    (Hq/Hkv 32/8, d 128, page 16, fp16, random page tables over a 2x pool), each
+    point the mean of back-to-back whole calls (partial + merge) through the C ABI
+    with the automatic plan for a known max_seq_len; KV sets under
+    ``ROTATE_BELOW_BYTES`` rotate over several pools (:func:`input_sets`). The
+    pools of one (KV, batch) serve all three q_len (Q drawn per q_len)."""
+    grid = {}
+    for kv in GRID_KV_LENS:
+        for b in GRID_BATCHES:
+            case = inputs.uniform_case(b, max(GRID_Q_LENS), kv, seed=4000 + kv // 1024 + b)
+            kvb = inputs.kv_bytes(case.seq_lens, case.num_kv_heads, case.head_dim)
+            sets = input_sets(inputs, case, kvb)
+            n_steps = steps if kvb >= ROTATE_BELOW_BYTES else max(steps, 100)
+            for ql in GRID_Q_LENS:
+                qsets = []
+                for i, (q, k, v, bt, sl) in enumerate(sets):
+                    g = torch.Generator(device="cuda").manual_seed(4100 + 10 * ql + i)
+                    qx = torch.randn(b, ql, q.shape[2], q.shape[3], generator=g, device="cuda",
+                                     dtype=torch.float16)
+                    qsets.append((qx, k, v, bt, sl))
+                plan = lib.plan_splits(0, b, ql, case.num_query_heads, case.num_kv_heads,
+                                       case.head_dim, kv, sets[0][3].shape[1], 0)
+                _ramp_clocks(torch, lib, qsets[0], plan, seconds=0.03)
+                ms, _, _, out = time_calls(torch, lib, qsets, plan, n_steps, warmup,
+                                           kernel_events=False)
+                if not torch.isfinite(out).all():
+                    raise SystemExit(f"non-finite output at q{ql} KV{kv} B{b}")
+                gbps = kvb / (ms * 1e-3) / 1e9
+                grid[f"q{ql}_kv{kv}_b{b}"] = {
+                    "us_per_call": round(ms * 1e3, 2), "kv_GBps": round(gbps, 1),
+                    "pct_peak": round(100.0 * gbps / PEAK_HBM_GBPS, 2), "kv_bytes": kvb,
+                    "pools": len(sets), "steps": n_steps, "num_splits": plan[0],
+                    "pages_per_split": plan[1]}
+                del qsets
+            del sets
+            torch.cuda.empty_cache()
+    return grid
 
 
 def read_probe(torch, lib, pool, steps):
@@ -321,6 +374,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.grid_only:
+        print(json.dumps({"metric": METRIC, "metric_grid": metric_grid(
+            torch, _lib, inputs, args.steps, args.warmup)}), flush=True)
+        return
     case = inputs.baseline_configs()[args.config]
     if args.q_len:
         case.q_len = args.q_len
@@ -476,19 +533,25 @@ def main():
                    # Upper bounds: the library's events between the kernels add time.
                    "partial_us_events": round(px * 1e3, 2), "merge_us_events": round(mx * 1e3, 2),
                    "num_splits": pl[0], "pages_per_split": pl[1]}
+            # This run's figures: the whole call back to back, and the partial
+            # kernel between the library's events.
+            row["call_frac"] = round(kb / (msx * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)
+            row["kernel_frac_events"] = round(kb / (px * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)
+            # Not measured in this run: the committed rocprof summary of the same
+            # workload (bench.py --config <name>), for comparison.
             prof_times = _profiled_times(profile_path(name, c.q_len, "fp16"))
             if prof_times is not None:
-                row["rocprof"] = prof_times
-                row["kernel_us"] = prof_times["partial_us"]
-                row["kernel_us_source"] = "rocprof (committed profile of bench.py --config " + name + ")"
-            else:
-                row["kernel_us"] = round(px * 1e3, 2)
-                row["kernel_us_source"] = "events"
-            row["kernel_frac"] = round(kb / (row["kernel_us"] * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)
+                row["rocprof_kernel_us"] = prof_times["partial_us"]
+                row["rocprof_kernel_frac"] = round(
+                    kb / (prof_times["partial_us"] * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)
+                if "merge_us" in prof_times:
+                    row["rocprof_merge_us"] = prof_times["merge_us"]
+                row["rocprof_source"] = prof_times["source"]
             others[name] = row
             del ts
             torch.cuda.empty_cache()
         result["other_configs"] = others
+        result["metric_grid"] = metric_grid(torch, _lib, inputs, args.steps, args.warmup)
         tensors = inputs.make_inputs(case, device="cuda", gen_device="cuda")
     if not args.no_cpu_baseline and default_types:
         result["cpu_baseline"] = cpu_baseline(torch, tensors, case, args.cpu_seconds)

@@ -1631,13 +1631,15 @@ void sqa_partial_lds_kernel(PartialArgs a) {
 // with l_s <= 0 are skipped and a row with no visible key is written as 0.
 // fp16 partials hold acc_s / l_s (so acc_s = l_s times the stored row).
 //
-// One pass, every load of a round in flight at once: TPR threads serve one
-// output row; thread t owns 4 dims (chunk t % (HD/4)) and the splits
-// s = g, g + SG, ... of its split group g = t / (HD/4) (SG = TPR / (HD/4)
-// groups), U splits per round. Each group keeps a running max and rescales its
-// sums when the max grows (as the online softmax does), so no pass over the
-// maxima precedes the sums; the SG groups then meet by shuffles (TPR = 64, one
-// wave per row) or in LDS (TPR = 256, a workgroup per row for many splits).
+// One pass, every load of a round in flight at once: WPR waves serve one
+// output row; each thread owns the 16 bytes of a partial row at dims DPT c ..
+// DPT c + DPT - 1 (DPT = 8 fp16 or 4 fp32 values) and the splits g, g + SG, ...
+// of its split group g, U splits per round (one round wherever the row's
+// splits allow: the round trip to the partials, not their bytes, sets the
+// time). Each group keeps a running max and rescales its sums when the max
+// grows (as the online softmax does), so no pass over the maxima precedes the
+// sums; the groups then meet by shuffles within a wave and in LDS across the
+// row's waves.
 // A (first slot, count) entry held to the slots that exist, whatever the table
 // holds (the partial kernel writes it within them).
 __device__ __forceinline__ SeqSplits in_range(SeqSplits t, int num_splits) {
@@ -1706,13 +1708,18 @@ __device__ __noinline__ void update_pair_delta(float* tune, int records) {
   if (t == 0) tune[2] = 0.f;
 }
 
-template <int TPR, int HD, typename E, int U>
+template <int WPR, int HD, typename E, int U>
 __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
-  constexpr int CH = HD / 4;       // 4-dim chunks of a row
-  constexpr int SG = TPR / CH;     // split groups of a row
-  constexpr int RPW = 256 / TPR;   // rows per workgroup
-  // U: splits per thread per round (a round covers U * SG splits of a row)
-  static_assert(SG >= 1 && TPR % CH == 0, "a row's threads must cover its dims");
+  // Each thread owns DPT dims of the row, 16 bytes of every partial row (fp16
+  // partials: 8 dims; fp32: 4), and the splits g, g + SG, ... of its split
+  // group g; a row's WPR waves cover SG = 64 WPR / CH splits per load
+  // instruction and U SG splits per round.
+  constexpr int DPT = E::kHalfPartials ? 8 : 4;
+  constexpr int CH = HD / DPT;      // threads per partial row
+  constexpr int TPR = 64 * WPR;     // threads per output row
+  constexpr int SG = TPR / CH;      // split groups of a row
+  constexpr int RPW = 256 / TPR;    // rows per workgroup
+  static_assert(SG >= 1 && TPR % CH == 0 && 256 % TPR == 0, "a row's threads must cover its dims");
   const int t = threadIdx.x;
   const int tr = t % TPR;
   const int c = tr % CH;
@@ -1758,29 +1765,26 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   if (!live) n_valid = 0;
 
   float mt = -INFINITY, den = 0.f;
-  f4 acc = {0.f, 0.f, 0.f, 0.f};
-  f4 o[U];
+  float acc[DPT];
+  u4 o[U];
   float m[U], l[U];
   // One round: splits sb + u * SG (u < U) of the slots [s0, s0 + nv). Loads are
   // unconditional, from an in-bounds slot (past the last split: split 0 of the
   // row again, weight 0), so rounds need no branch around their loads.
   auto load_round = [&](int s0, int nv, int sb) {
     const float* ml = a.part_ml + ((size_t)s0 * stride + row_item) * 2;
-    const size_t o0 = ((size_t)s0 * stride + row_item) * HD + 4 * c;
+    const size_t o0 = ((size_t)s0 * stride + row_item) * HD + DPT * c;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int sp = sb + u * SG;
       const size_t it = (size_t)(sp < nv ? sp : 0) * stride;
-      if constexpr (E::kHalfPartials) {
-        const h4 x = __builtin_bit_cast(h4, *(const u2*)((const _Float16*)a.part_o + o0 + it * HD));
-        o[u] = f4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
-      } else {
-        o[u] = *(const f4*)(a.part_o + o0 + it * HD);
-      }
+      if constexpr (E::kHalfPartials)
+        o[u] = *(const u4*)((const _Float16*)a.part_o + o0 + it * HD);
+      else
+        o[u] = *(const u4*)(a.part_o + o0 + it * HD);
       const float2 p = *(const float2*)(ml + it * 2);  // (max, sum) in one load
       m[u] = p.x;
-      l[u] = p.y;
-      if (sp >= nv) l[u] = 0.f;
+      l[u] = sp < nv ? p.y : 0.f;
     }
   };
   auto add_round = [&]() {
@@ -1791,7 +1795,8 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
     if (nm != -INFINITY) {
       const float sc = mt == -INFINITY ? 0.f : fast_exp2(mt - nm);
       den *= sc;
-      acc *= sc;
+#pragma unroll
+      for (int i = 0; i < DPT; ++i) acc[i] *= sc;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         // Splits without keys (l <= 0) never touch the sums: their partial sums
@@ -1801,8 +1806,18 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
         den += w * l[u];
         // Normalised partials weigh in with their sum.
         const float wo = E::kHalfPartials ? w * l[u] : w;
+        float x[DPT];
+        if constexpr (E::kHalfPartials) {
+          const h8 v = __builtin_bit_cast(h8, o[u]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = use ? fmaf(wo, o[u][i], acc[i]) : acc[i];
+          for (int i = 0; i < 8; ++i) x[i] = (float)v[i];
+        } else {
+          const f4 v = __builtin_bit_cast(f4, o[u]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = v[i];
+        }
+#pragma unroll
+        for (int i = 0; i < DPT; ++i) acc[i] = use ? fmaf(wo, x[i], acc[i]) : acc[i];
       }
       mt = nm;
     }
@@ -1812,7 +1827,8 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   auto merge_splits = [&](int s0, int nv) {
     mt = -INFINITY;
     den = 0.f;
-    acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) acc[i] = 0.f;
     load_round(s0, nv, g);
     if (expect) table = in_range(a.seq_splits[b], a.num_splits);
     const float first_l = l[0];  // split g (split 0 for group 0)
@@ -1836,43 +1852,59 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   const bool done = balanced ? n_valid == 1 : (g == 0 && first_l < 0.f);
   const bool skip = !live || done;
 
-  // Combine the SG groups of the row.
-  auto combine = [&](float mo, float dn, f4 ao) {
+  // Combine the SG groups of the row: within a wave by shuffles (lanes c,
+  // c + CH, ...), then the row's waves through LDS.
+  auto combine = [&](float mo, float dn, const float (&ao)[DPT]) {
     const float nm = fmaxf(mt, mo);
     if (nm == -INFINITY) return;
     const float sa = mt == -INFINITY ? 0.f : fast_exp2(mt - nm);
     const float so = mo == -INFINITY ? 0.f : fast_exp2(mo - nm);
     den = den * sa + dn * so;
-    acc = acc * sa + ao * so;
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) acc[i] = acc[i] * sa + ao[i] * so;
     mt = nm;
   };
-  if constexpr (SG > 1 && TPR == 64) {
 #pragma unroll
-    for (int off = CH; off < 64; off <<= 1) {
-      const float mo = __shfl_xor(mt, off), dn = __shfl_xor(den, off);
-      const f4 ao = {__shfl_xor(acc[0], off), __shfl_xor(acc[1], off), __shfl_xor(acc[2], off),
-                     __shfl_xor(acc[3], off)};
-      combine(mo, dn, ao);
-    }
-  } else if constexpr (SG > 1) {
-    static_assert(RPW == 1, "LDS combine serves one row per workgroup");
-    __shared__ f4 sm_acc[SG][CH];
-    __shared__ float sm_m[SG], sm_d[SG];
+  for (int off = CH; off < 64; off <<= 1) {
+    const float mo = __shfl_xor(mt, off), dn = __shfl_xor(den, off);
+    float ao[DPT];
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) ao[i] = __shfl_xor(acc[i], off);
+    combine(mo, dn, ao);
+  }
+  if constexpr (WPR > 1) {
+    static_assert(RPW == 1, "the LDS combine serves one row per workgroup");
+    __shared__ float sm_acc[WPR][CH][DPT + 1];
+    __shared__ float sm_m[WPR][CH], sm_d[WPR][CH];
     if (!live || (balanced && n_valid == 1)) return;  // uniform over the workgroup (one row)
-    sm_acc[g][c] = acc;
-    if (c == 0) {
-      sm_m[g] = mt;
-      sm_d[g] = den;
+    const int wave = t >> 6;
+    if ((t & 63) < CH) {
+#pragma unroll
+      for (int i = 0; i < DPT; ++i) sm_acc[wave][c][i] = acc[i];
+      sm_m[wave][c] = mt;
+      sm_d[wave][c] = den;
     }
     __syncthreads();
-    if (g != 0) return;
+    if (t >= CH) return;
 #pragma unroll
-    for (int o = 1; o < SG; ++o) combine(sm_m[o], sm_d[o], sm_acc[o][c]);
+    for (int w = 1; w < WPR; ++w) {
+      float ao[DPT];
+#pragma unroll
+      for (int i = 0; i < DPT; ++i) ao[i] = sm_acc[w][c][i];
+      combine(sm_m[w][c], sm_d[w][c], ao);
+    }
   }
   if (skip || g != 0) return;
   const float inv = den > 0.f ? a.out_scale / den : 0.f;
-  const float out[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
-  *(u2*)(a.out + (size_t)row * HD + 4 * c) = E::pack4(out);
+  if constexpr (DPT == 8) {
+    float out[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = acc[i] * inv;
+    *(u4*)(a.out + (size_t)row * HD + 8 * c) = E::pack8(out);
+  } else {
+    const float out[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+    *(u2*)(a.out + (size_t)row * HD + 4 * c) = E::pack4(out);
+  }
 }
 
 // Ring depth: the pages in flight per wave hold about 32 KiB of 16-bit K and
@@ -1936,32 +1968,32 @@ void launch_partial_as(const PartialArgs& a, const LaunchShape& sh, dim3 grid, d
     launch_partial_hd<128, E, KV<128>>(a, sh, grid, block, stream);
 }
 
+template <int HD, typename E, int WPR>
+void launch_merge_u(const MergeArgs& a, int u, dim3 grid, hipStream_t stream) {
+  if (u <= 2)
+    hipLaunchKernelGGL((sqa_merge_kernel<WPR, HD, E, 2>), grid, dim3(256), 0, stream, a);
+  else if (u <= 4)
+    hipLaunchKernelGGL((sqa_merge_kernel<WPR, HD, E, 4>), grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((sqa_merge_kernel<WPR, HD, E, 8>), grid, dim3(256), 0, stream, a);
+}
+
 template <int HD, typename E>
 void launch_merge_hd(const MergeArgs& a, int per_row, hipStream_t stream) {
-  // A wave per row while its split groups take all of the row's splits in two
-  // rounds of loads; a workgroup per row beyond that. Rows whose splits fit one
-  // round of 4 loads per thread take that round (half the load instructions of
-  // the 8-load round, whose extra slots would reload split 0 for nothing).
-  // Under 1024 rows, where a wave per row needs its second round, it leaves
-  // most CUs idle (256 workgroups of 4 rows at most) while each wave waits out
-  // both: a workgroup per row takes up to 4 * 256 / (HD / 4) splits in one
-  // round of 4 loads (B4 KV 8K, 32 splits per row, whole call: q2 30.7 -> 29.2
-  // us, q4 31.2 -> 30.5 us). Rows that fit one round stay with a wave (B1 KV
-  // 1K, 16 splits per row: merge 3.4 us, 3.7 us a workgroup per row).
-  constexpr int kGroups = 64 / (HD / 4);
-  constexpr int kWgGroups = 256 / (HD / 4);
+  // A row's splits in one round of loads wherever 8 per thread cover them: a
+  // wave per row (4 rows per workgroup) for 1024 rows and more, where the
+  // chip has rows enough; a workgroup of 4 waves per row below that, or where a
+  // wave would need a second round (one sequence, KV 32K, q_len 8: 128 splits
+  // per row). Each thread issues U loads of 16 bytes at once, the smallest U of
+  // 2, 4, 8 that covers the row (more rounds past 8).
+  constexpr int kSplitsPerWave = 64 / (HD / (E::kHalfPartials ? 8 : 4));
   const int total = a.batch * a.q_len * a.hq;
-  const dim3 waves((unsigned)((total + 3) / 4));
-  if (per_row <= 4 * kGroups) {
-    hipLaunchKernelGGL((sqa_merge_kernel<64, HD, E, 4>), waves, dim3(256), 0, stream, a);
-  } else if (per_row <= 2 * 8 * kGroups && (total >= 1024 || per_row <= 8 * kGroups)) {
-    hipLaunchKernelGGL((sqa_merge_kernel<64, HD, E, 8>), waves, dim3(256), 0, stream, a);
-  } else if (per_row <= 4 * kWgGroups) {
-    hipLaunchKernelGGL((sqa_merge_kernel<256, HD, E, 4>), dim3((unsigned)total), dim3(256), 0,
-                       stream, a);
+  if (total >= 1024 && per_row <= 8 * kSplitsPerWave) {
+    const int u = (per_row + kSplitsPerWave - 1) / kSplitsPerWave;
+    launch_merge_u<HD, E, 1>(a, u, dim3((unsigned)((total + 3) / 4)), stream);
   } else {
-    hipLaunchKernelGGL((sqa_merge_kernel<256, HD, E, 8>), dim3((unsigned)total), dim3(256), 0,
-                       stream, a);
+    const int u = (per_row + 4 * kSplitsPerWave - 1) / (4 * kSplitsPerWave);
+    launch_merge_u<HD, E, 4>(a, u, dim3((unsigned)total), stream);
   }
 }
 

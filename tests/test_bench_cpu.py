@@ -80,3 +80,14 @@ def test_small_workloads_rotate_over_enough_pools():
         assert len(set(fake.seeds)) == want  # distinct seeds, distinct pools
         if want > 1:
             assert want >= 3 and want * kv > bench.ROTATE_BELOW_BYTES
+
+
+def test_metric_grid_covers_the_baseline_metric():
+    """The grid is BASELINE's metric: q_len 2/4/8 x KV 8K/32K x batch 1/4/16 (18 points)."""
+    import json
+
+    metric = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+    assert bench.METRIC == metric
+    assert bench.GRID_Q_LENS == (2, 4, 8) and "q_len 2/4/8" in metric
+    assert bench.GRID_KV_LENS == (8192, 32768) and "KV 8K/32K" in metric
+    assert bench.GRID_BATCHES == (1, 4, 16) and "batch 1/4/16" in metric
