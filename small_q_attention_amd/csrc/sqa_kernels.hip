@@ -1897,10 +1897,12 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   if (skip || g != 0) return;
   const float inv = den > 0.f ? a.out_scale / den : 0.f;
   if constexpr (DPT == 8) {
-    float out[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) out[i] = acc[i] * inv;
-    *(u4*)(a.out + (size_t)row * HD + 8 * c) = E::pack8(out);
+    // Two 8-byte stores: the output need only be 8-byte aligned.
+    const float lo[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+    const float hi[4] = {acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
+    u2* op = (u2*)(a.out + (size_t)row * HD + 8 * c);
+    op[0] = E::pack4(lo);
+    op[1] = E::pack4(hi);
   } else {
     const float out[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
     *(u2*)(a.out + (size_t)row * HD + 4 * c) = E::pack4(out);

@@ -337,6 +337,28 @@ def test_c_abi_direct_with_caller_workspace():
         _lib.launch(q, k, v, bt, sl, out, small, ns, pps, 0)
 
 
+@pytest.mark.parametrize("batch,kv,q_len", [(1, 8192, 2), (4, 2048, 8), (16, 600, 4)])
+def test_output_only_8_byte_aligned(batch, kv, q_len):
+    """The C ABI asks for an 8-byte aligned output: the merge (and the partial
+    kernel's direct rows) store 8 bytes at a time, so an output 8 bytes past a
+    16-byte boundary gets the same bits as an aligned one."""
+    case = inputs.uniform_case(batch, q_len, kv, seed=5300 + batch)
+    q, k, v, bt, sl = _to_gpu(inputs.make_inputs(case))
+    ns, pps = _lib.plan_splits(0, batch, q_len, 32, 8, 128, kv, bt.shape[1], 0)
+    ws = torch.empty(max(1, _lib.workspace_bytes(batch, q_len, 32, 8, 128, ns, pps)),
+                     dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    aligned = torch.empty_like(q)
+    _lib.launch(q, k, v, bt, sl, aligned, ws, ns, pps, stream)
+    buf = torch.full((q.numel() + 4,), float("nan"), dtype=q.dtype, device="cuda")
+    shifted = buf[4:].view_as(q)
+    assert shifted.data_ptr() % 16 == 8
+    _lib.launch(q, k, v, bt, sl, shifted, ws, ns, pps, stream)
+    torch.cuda.synchronize()
+    assert torch.equal(shifted, aligned)
+    assert torch.isnan(buf[:4]).all()  # nothing written before the output
+
+
 def test_parity_stats_flags_a_planted_mistake():
     """The checker itself: an oracle off by one visible key fails the bar."""
     case = inputs.Case(batch=1, q_len=4, seq_lens=[40], seed=18)
