@@ -172,6 +172,18 @@ struct ElemBF16 {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Split partials leave as write-through stores (relaxed agent-scope atomics:
+// global_store with sc1, which the XCD's L2 passes on to memory) rather than
+// write-back ones: the merge kernel reads them from other XCDs anyway, and
+// dirty lines left in the L2s would be written back at the end of the partial
+// kernel, before the merge kernel can start (stamped on one box: the merge
+// began 1.6 us after the last partial workgroup at 2 MB of partials, 4.5 us at
+// 8 MB). Whole calls back to back: one sequence of 32K keys, q_len 8, 34.6 ->
+// 31.8 us; 4 x 8K, q_len 4, 30.6 -> 29.7 us; 16 x 32K +-0.7 us.
+__device__ __forceinline__ void store_through(void* p, unsigned long long x) {
+  __hip_atomic_store((unsigned long long*)p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ float xor_max(float x) {
   x = fmaxf(x, __shfl_xor(x, 16));
   return fmaxf(x, __shfl_xor(x, 32));
@@ -1063,16 +1075,18 @@ __device__ __forceinline__ void write_results(const PartialArgs& a, WaveState<NB
           const size_t at = (item_of(nb, rs) + map.row(nb, rs)) * HD + 4 * (e % CPR);
           if constexpr (E::kHalfPartials) {
             const float o[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
-            *(u2*)((_Float16*)a.part_o + at) = E::pack4(o);
+            store_through((_Float16*)a.part_o + at, __builtin_bit_cast(unsigned long long, E::pack4(o)));
           } else {
-            *(f4*)(a.part_o + at) = v[i];
+            const u4 w = __builtin_bit_cast(u4, v[i]);
+            store_through(a.part_o + at, __builtin_bit_cast(unsigned long long, u2{w[0], w[1]}));
+            store_through(a.part_o + at + 2, __builtin_bit_cast(unsigned long long, u2{w[2], w[3]}));
           }
         }
       }
       if (g16 == 0 && map.real(nb, l16)) {
         const size_t pitem = item_of(nb, l16) + map.row(nb, l16);
-        a.part_ml[pitem * 2 + 0] = st.m[nb];
-        a.part_ml[pitem * 2 + 1] = st.l[nb];
+        store_through(a.part_ml + pitem * 2,
+                      __builtin_bit_cast(unsigned long long, float2{st.m[nb], st.l[nb]}));
       }
     }
   }
