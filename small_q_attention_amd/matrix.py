@@ -3,6 +3,9 @@
     python -m small_q_attention_amd.matrix --variants v3 auto --q-lens 2 4 8 16 \\
         --kv-lens 1024 8192 32768 --batch-sizes 1 4 16 --page-mode random
 
+Defaults are the reference runner's (variants v0 v1, shared pages, 512 keys per
+split, q_len 2 4 8, KV 1024 8192, batch 1 4).
+
 Same CLI names and JSONL row schema as ``run_gpu_matrix.py:108-175`` (``variant,
 page_mode, case, status, device, p50_us, p99_us, min_us, max_us``), timed the
 same way (events around the Python call, warmup then repeats,
@@ -192,17 +195,31 @@ def measure_case(torch, variant, case, page_mode, chunk_keys, warmup, repeats, s
     return row
 
 
-def main(argv=None):
-    import torch
+def _chunk_keys(text):
+    """``--chunk-keys``: an integer, as the reference runner takes it, or ``auto``."""
+    if text == "auto":
+        return text
+    try:
+        return int(text)
+    except ValueError:
+        raise argparse.ArgumentTypeError(f"an integer or 'auto', not {text!r}") from None
 
+
+def build_parser():
+    """The runner's CLI. Defaults are the reference runner's
+    (``/root/reference/scripts/run_gpu_matrix.py:111-127``: variants v0 v1, shared
+    pages, 512 keys per split, q_len 2 4 8, KV 1024 8192, batch 1 4), so an
+    invocation that relies on them measures the same workload; ``auto`` (the
+    CU-count plan, as variant or chunk size) and ``random`` page tables are
+    opt-ins."""
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("--variants", nargs="+", default=["v3"],
+    ap.add_argument("--variants", nargs="+", default=["v0", "v1"],
                     choices=("v0", "v1", "v2", "v3", "v4", "v5", "auto"))
-    ap.add_argument("--chunk-keys", default="512",
+    ap.add_argument("--chunk-keys", type=_chunk_keys, default=512,
                     help="KV entries per split for v2-v5, or 'auto' (CU-count plan); "
                          "variant 'auto' always uses the CU-count plan")
     ap.add_argument("--token-group", type=int, choices=(2, 4), default=2)
-    ap.add_argument("--page-mode", choices=("shared", "unique", "random"), default="random")
+    ap.add_argument("--page-mode", choices=("shared", "unique", "random"), default="shared")
     ap.add_argument("--q-lens", nargs="+", type=int, default=[2, 4, 8])
     ap.add_argument("--kv-lens", nargs="+", type=int, default=[1024, 8192])
     ap.add_argument("--batch-sizes", nargs="+", type=int, default=[1, 4])
@@ -214,7 +231,13 @@ def main(argv=None):
     ap.add_argument("--correctness-limit", type=int, default=3,
                     help="cases checked when --check-correctness is given")
     ap.add_argument("--output", type=Path, help="JSONL file rows are appended to")
-    args = ap.parse_args(argv)
+    return ap
+
+
+def main(argv=None):
+    import torch
+
+    args = build_parser().parse_args(argv)
     if not torch.cuda.is_available():
         raise SystemExit("a ROCm GPU is required")
     if args.warmup < 0 or args.repeats < 1:

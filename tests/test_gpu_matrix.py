@@ -22,8 +22,9 @@ OWN_KEYS = {"kernel_p50_us", "merge_p50_us", "b2b_us", "kv_bytes", "kv_GBps", "p
 def test_runner_rows_and_correctness(tmp_path):
     out = tmp_path / "rows.jsonl"
     sys.__stderr__.write("\n[gpu-test] matrix runner: 2 cases x 2 variants\n")
-    rc = matrix.main(["--variants", "auto", "v3", "--q-lens", "2", "--kv-lens", "1024",
-                      "--batch-sizes", "1", "4", "--warmup", "1", "--repeats", "3",
+    rc = matrix.main(["--variants", "auto", "v3", "--page-mode", "random", "--q-lens", "2",
+                      "--kv-lens", "1024", "--batch-sizes", "1", "4", "--warmup", "1",
+                      "--repeats", "3",
                       "--check-correctness", "--correctness-limit", "3", "--output", str(out)])
     assert rc == 0
     rows = [json.loads(line) for line in out.read_text().splitlines()]
@@ -41,3 +42,18 @@ def test_runner_rows_and_correctness(tmp_path):
     for row in checked:
         assert row["within_tolerance"], row
         assert row["max_abs_error"] <= 2e-3 + 1e-2 * 4.0
+
+
+def test_runner_defaults_run(tmp_path):
+    """The reference runner's defaults (variants v0 v1, shared pages, chunk_keys 512)
+    on one small case: rows carry the integer chunk size and the page mode."""
+    out = tmp_path / "rows.jsonl"
+    sys.__stderr__.write("\n[gpu-test] matrix runner: defaults, 1 case x 2 variants\n")
+    rc = matrix.main(["--q-lens", "2", "--kv-lens", "1024", "--batch-sizes", "1",
+                      "--warmup", "1", "--repeats", "3", "--output", str(out)])
+    assert rc == 0
+    rows = [json.loads(line) for line in out.read_text().splitlines()]
+    assert [r["variant"] for r in rows] == ["v0", "v1"]
+    for row in rows:
+        assert row["status"] == "ok", row
+        assert row["page_mode"] == "shared" and row["chunk_keys"] == 512

@@ -92,3 +92,28 @@ def test_ragged_lengths_in_range_and_byte_counts():
     cfg3 = inputs.baseline_configs()["cfg3"]
     assert inputs.kv_bytes(cfg3.seq_lens) == 16 * 32768 * 8 * 128 * 2 * 2
     assert inputs.attention_flops(cfg3) == 4 * 32 * 128 * 16 * sum(32768 - 8 + i + 1 for i in range(8))
+
+
+def test_runner_defaults_are_the_reference_runners():
+    """An invocation relying on the defaults measures the reference runner's workload
+    (``/root/reference/scripts/run_gpu_matrix.py:111-127``): variants v0 v1, shared
+    pages, integer chunk_keys 512, q_len 2 4 8, KV 1024 8192, batch 1 4, warmup 5,
+    repeats 15, 3 cases checked; ``auto`` and ``random`` stay opt-ins."""
+    args = matrix.build_parser().parse_args([])
+    assert args.variants == ["v0", "v1"]
+    assert args.page_mode == "shared"
+    assert args.chunk_keys == 512 and isinstance(args.chunk_keys, int)
+    assert args.token_group == 2
+    assert args.q_lens == [2, 4, 8] and args.kv_lens == [1024, 8192]
+    assert args.batch_sizes == [1, 4]
+    assert (args.warmup, args.repeats, args.limit) == (5, 15, 0)
+    assert not args.check_correctness and args.correctness_limit == 3
+    opt = matrix.build_parser().parse_args(["--variants", "auto", "v3", "--chunk-keys", "auto",
+                                            "--page-mode", "random"])
+    assert opt.variants == ["auto", "v3"] and opt.chunk_keys == "auto"
+    assert opt.page_mode == "random"
+    assert matrix.build_parser().parse_args(["--chunk-keys", "128"]).chunk_keys == 128
+    import pytest
+
+    with pytest.raises(SystemExit):
+        matrix.build_parser().parse_args(["--chunk-keys", "lots"])
