@@ -41,9 +41,12 @@ ROTATE_BELOW_BYTES = 512 << 20
 # rocprofv3 FETCH_SIZE + WRITE_SIZE summary of the partial kernel on this workload
 # (calibrated against a plain 1 GiB copy); regenerated with the kernel. The bench
 # line's is profiles/sqa_partial_kernel_cfg3_b16_q8_kv32768.txt.
-def profile_path(config: str, q_len: int, kv_dtype: str) -> Path:
-    shape = {"cfg1": f"cfg1_b1_q{q_len}_kv1024", "cfg2": f"cfg2_b4_q{q_len}_kv8192",
-             "cfg3": f"cfg3_b16_q{q_len}_kv32768", "cfg5": f"cfg5_b16_q{q_len}_ragged"}[config]
+def profile_path(config: str, q_len: int, kv_dtype: str, batch: int = 0, kv_len: int = 0) -> Path:
+    if batch and kv_len:  # a uniform grid point (--batch / --kv-len)
+        shape = f"b{batch}_q{q_len}_kv{kv_len}"
+    else:
+        shape = {"cfg1": f"cfg1_b1_q{q_len}_kv1024", "cfg2": f"cfg2_b4_q{q_len}_kv8192",
+                 "cfg3": f"cfg3_b16_q{q_len}_kv32768", "cfg5": f"cfg5_b16_q{q_len}_ragged"}[config]
     suffix = "" if kv_dtype == "fp16" else f"_{kv_dtype}"
     return ROOT / "profiles" / f"sqa_partial_kernel_{shape}{suffix}.txt"
 
@@ -95,6 +98,10 @@ def _parse():
                     help="override the workload's q_len (profiling other rows per kv head)")
     ap.add_argument("--config", default="cfg3", choices=("cfg1", "cfg2", "cfg3", "cfg5"),
                     help="workload (cfg3 is the bench line; others for profiling)")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="with --kv-len: time a uniform batch of this many sequences instead "
+                         "of the config (profiling a metric-grid point)")
+    ap.add_argument("--kv-len", type=int, default=0, help="keys per sequence (with --batch)")
     ap.add_argument("--kv-dtype", default="fp16", choices=("fp16", "bf16", "e4m3"),
                     help="element types of the timed workload (profiling the other kernels): "
                          "bf16 = bf16 Q/K/V/output, e4m3 = fp16 Q/output over an OCP e4m3 "
@@ -379,6 +386,10 @@ def main():
             torch, _lib, inputs, args.steps, args.warmup)}), flush=True)
         return
     case = inputs.baseline_configs()[args.config]
+    if args.batch and args.kv_len:
+        case = inputs.uniform_case(args.batch, args.q_len or 8, args.kv_len,
+                                   seed=4000 + args.kv_len // 1024 + args.batch)
+        args.config = f"b{args.batch}_kv{args.kv_len}"
     if args.q_len:
         case.q_len = args.q_len
     kvb16 = inputs.kv_bytes(case.seq_lens, case.num_kv_heads, case.head_dim)
@@ -398,7 +409,7 @@ def main():
     ms, part_ms, merge_ms, out = time_calls(torch, _lib, sets, plan, args.steps, args.warmup)
     if not torch.isfinite(out).all():
         raise SystemExit("non-finite output")
-    prof = profile_path(args.config, case.q_len, args.kv_dtype)
+    prof = profile_path(args.config, case.q_len, args.kv_dtype, args.batch, args.kv_len)
     kvb = kvb16 * k.element_size() // 2
     value = kvb / (ms * 1e-3) / 1e9
     achieved = kvb / (part_ms * 1e-3) / 1e9
