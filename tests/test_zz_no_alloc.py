@@ -106,3 +106,70 @@ def test_noalloc_refuses_a_plan_beyond_the_scratch():
     assert "no-allocation" in _lib.last_error(lib)
     torch.cuda.synchronize()
     assert not out.any()  # nothing ran
+
+
+# Run in a fresh process: the no-allocation call captured into a HIP graph, either
+# as the process's first call of the entry point (the scratch address is looked up
+# inside the capture) or after an eager warm-up call; replays must equal an eager
+# call of the same entry point bit for bit.
+_CAPTURE_SCRIPT = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import torch
+from small_q_attention_amd import _lib, inputs
+warm = sys.argv[2] == "warm"
+lib = _lib.load(build_if_missing=False)
+case = inputs.Case(batch=3, q_len=8, seq_lens=[3000, 700, 1900], seed=47)
+q, k, v, bt, sl = (t.cuda() for t in inputs.make_inputs(case))
+ns, pps = _lib.plan_splits(0, 3, 8, 32, 8, 128, 3000, bt.shape[1], 0)
+assert ns > 1
+
+def call(out, stream):
+    return lib.sqa_paged_mtp_attention_noalloc(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr(), out.data_ptr(),
+        3, 8, 32, 8, 128, k.shape[0], 16, bt.shape[1], ns, pps, stream)
+
+eager = torch.empty_like(q)
+if warm:
+    assert call(eager, torch.cuda.current_stream().cuda_stream) == 0, _lib.last_error(lib)
+    torch.cuda.synchronize()
+static_out = torch.empty_like(q)
+graph = torch.cuda.CUDAGraph()
+s = torch.cuda.Stream()
+s.wait_stream(torch.cuda.current_stream())
+with torch.cuda.stream(s):
+    with torch.cuda.graph(graph, stream=s):
+        rc = call(static_out, s.cuda_stream)
+torch.cuda.current_stream().wait_stream(s)
+torch.cuda.synchronize()
+if rc != 0:
+    print("capture rc", rc, _lib.last_error(lib), flush=True)
+    sys.exit(3)
+if not warm:
+    assert call(eager, torch.cuda.current_stream().cuda_stream) == 0, _lib.last_error(lib)
+    torch.cuda.synchronize()
+for i in range(3):
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(static_out, eager), f"replay {i}"
+    junk = torch.randn(1 << 20, device="cuda").sum()
+    torch.cuda.synchronize()
+print("capture ok", flush=True)
+"""
+
+
+@pytest.mark.parametrize("order", ["cold", "warm"])
+def test_noalloc_under_graph_capture(order):
+    """The no-allocation entry point captured in a HIP graph in a fresh process: as
+    the first call of the entry point (its scratch address is looked up during the
+    capture) and after an eager warm-up call. Replays equal an eager call."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    print(f"[noalloc] graph capture, {order}", flush=True)
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, str(root), order],
+                       capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
+    assert "capture ok" in r.stdout
