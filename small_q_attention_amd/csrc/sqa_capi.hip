@@ -258,6 +258,13 @@ int run_attention(const sqa_attention_args& a) {
   if (need > 0 && (uintptr_t)a.workspace % 16)
     return fail(SQA_ERR_WORKSPACE, "workspace must be 16-byte aligned");
 
+  // fp16 outputs keep fp16 partial rows (half of the region), bf16 fp32 ones.
+  const unsigned long long part_o_bytes =
+      (unsigned long long)sqa::plan_slots(batch, num_splits, pages_per_split) * num_kv_heads *
+      rows * head_dim * (a.dtype == SQA_DTYPE_F16 ? 2 : 4);
+  if ((balanced || num_splits > 1) && part_o_bytes > sqa::kMaxPartialBytes)
+    return fail(SQA_ERR_INVALID, "the plan's partials (%llu bytes) exceed %llu bytes",
+                part_o_bytes, sqa::kMaxPartialBytes);
   hipStream_t s = (hipStream_t)a.stream;
   hipEvent_t* ev = (hipEvent_t*)a.timing_events;
   void* workspace = a.workspace;
@@ -277,6 +284,7 @@ int run_attention(const sqa_attention_args& a) {
   pa.part_o = merged ? (float*)workspace : nullptr;
   pa.part_ml = merged ? (float*)workspace + items * head_dim : nullptr;
   pa.seq_splits = balanced ? (sqa::SeqSplits*)(pa.part_ml + items * 2) : nullptr;
+  pa.part_o_bytes = merged ? (unsigned)part_o_bytes : 0u;
   pa.num_pages = num_pages;
   pa.page_stride = kv_bytes * ps;
   pa.token_stride = (unsigned)(kv_bytes * ts);

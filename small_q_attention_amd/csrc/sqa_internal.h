@@ -17,6 +17,9 @@ constexpr int kMaxRows = 64;    // q_len * (Hq / Hkv) rows one work item holds
 constexpr int kMaxSplitPages = 2048;  // pages one split may own (LDS page-id table)
 constexpr int kMinSplitPages = 4;     // fewest pages the automatic plans give a split
 constexpr int kMaxBalancedBatch = 256;  // balanced plan: four sequences per lane of one wave
+// Partial sums are stored through a buffer resource with 32-bit offsets; a plan
+// whose partials need more is refused.
+constexpr unsigned long long kMaxPartialBytes = 0xFFFF0000ull;
 
 // Per-sequence split layout of the balanced plan, written by the partial
 // kernel for the merge kernel: first slot and number of splits.
@@ -94,6 +97,7 @@ struct PartialArgs {
                               // fp16 outputs fp16 rows divided by their sum (the first half
                               // of the same region)
   float* part_ml;             // [slots, Hkv, rows, 2] (max in log2 units, sum)
+  unsigned part_o_bytes;      // bytes of part_o the partials use (< kMaxPartialBytes)
   SeqSplits* seq_splits;      // [B] (balanced plan only)
   long long num_pages;        // pages in the cache pool; ids outside are clamped to 0
   long long page_stride;      // bytes between consecutive cache pages (K and V alike)
