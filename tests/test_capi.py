@@ -146,6 +146,11 @@ def _call(lib, **kw):
     (dict(out=20), SQA_ERR_INVALID, "output 8-byte aligned"),
     (dict(bt=18), SQA_ERR_INVALID, "4-byte aligned"),
     (dict(sl=17), SQA_ERR_INVALID, "4-byte aligned"),
+    # Partial sums travel through 32-bit buffer offsets: a plan whose partials
+    # pass 4 GiB (16 x 2048 one-page splits x 8 kv heads x 64 rows x 256 bytes)
+    # is refused before anything is launched.
+    (dict(batch=16, q_len=16, max_pages=2048, splits=2048, pps=1, ws=16, ws_bytes=1 << 40),
+     SQA_ERR_INVALID, "partials"),
 ])
 def test_launch_rejects_bad_arguments_without_a_gpu(lib, kw, code, msg):
     # Validation runs before any HIP call, so these pointers are never touched.
