@@ -94,8 +94,9 @@ size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv
  * 256 needs q_len * num_query_heads / num_kv_heads <= 32. `workspace` must hold
  * sqa_workspace_bytes(...) bytes, 16-byte aligned (may be NULL when that is 0). query
  * and the caches must be 16-byte aligned, output 8-byte, block_tables and seq_lens
- * 4-byte (SQA_ERR_INVALID otherwise). Allocates
- * nothing and never synchronises.
+ * 4-byte (SQA_ERR_INVALID otherwise), and a plan's partial sums must stay within
+ * 0xFFFF0000 bytes (SQA_ERR_INVALID; the automatic plans need a few MB to ~40 MB).
+ * Allocates nothing and never synchronises.
  * `timing_events`: NULL, or an array of 3 hipEvent_t recorded on `stream`
  * before the partial kernel, between the two kernels and after the merge
  * kernel (used by the benchmark to time the partial kernel alone).
