@@ -316,6 +316,12 @@ int run_attention(const sqa_attention_args& a) {
                   spec_pages % (2 * pa.spec_pps) == 0 && (num_splits - batch) % 2 == 0 &&
                   head_dim == 128 && kv_bytes == 2 && a.dtype == SQA_DTYPE_F16 && rows > 32 &&
                   rows <= 64 && num_kv_heads == 8;
+  // Pieces that fit the register ring take it in one softmax step: fixed plans
+  // of at most kRingPages pages per split, balanced plans whose expected items
+  // are that short (pieces can only be shorter than their item).
+  pa.ring_batch = head_dim == 128 && kv_bytes == 2 && rows <= 32 &&
+                  (balanced ? (spec_pages > 0 && pa.spec_pps <= sqa::kRingPages)
+                            : pages_per_split <= sqa::kRingPages);
   pa.scale_log2 = (float)(1.4426950408889634 * (double)a.scale);
   pa.out_scale = a.out_scale;
   pa.bf16 = a.dtype == SQA_DTYPE_BF16;

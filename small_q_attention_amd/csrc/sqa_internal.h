@@ -115,6 +115,7 @@ struct PartialArgs {
   int spec_pps;               // the balanced plan's item size when every sequence spans spec_pages
   int seam_pages;             // balanced plan: pages a second piece costs a workgroup (0: no gaps)
   int pair_items;             // paired items on (see above)
+  int ring_batch;             // every piece expected within the register ring (kRingPages)
   float* tune;                // paired items: {magic, delta, stamp, -} then per workgroup
                               // {loop ticks, pages}
   float scale_log2;           // softmax scale * log2(e)
@@ -200,6 +201,11 @@ inline LaunchShape launch_shape(int rows, int hkv, int head_dim) {
   if (rows <= 32) return {2, 4, 1, 1};
   return {4, 4, 1, 1};
 }
+
+// Pages the register ring of the one-wave-per-head kernel holds at head dim 128
+// with 16-bit K/V and up to 32 rows: pieces of at most this many pages take the
+// whole-ring softmax step (PartialArgs::ring_batch).
+constexpr int kRingPages = 4;
 
 // What a second piece costs a workgroup of the balanced plan, in pages of its
 // own: ~5.6 us measured at 16 ragged sequences of 2K-32K tokens (q_len 8, head

@@ -450,37 +450,35 @@ __device__ __forceinline__ void mask_scores(f4 (&s)[NB], const unsigned long lon
   }
 }
 
-template <int NB, int HD, typename E, typename KV, int HPW>
-__device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
-                                            PageV<HD, HPW>& pv, bool upper,
-                                            const unsigned long long (&dbits)[NB],
-                                            int draft_base, int tok0, int len, bool masked,
-                                            float c) {
-  constexpr int MB = Dims<HD>::MB, VW = Dims<HD>::VW;
-  if (masked) {
-    mask_scores<NB>(s, dbits, draft_base, tok0, len);
-    // V rows past the sequence end may hold anything (even NaN); 0 * NaN would
-    // poison the product, so zero them.
+// Masked pages: scores of tokens a row does not see become -inf, and V rows
+// past the sequence end may hold anything (even NaN; 0 * NaN would poison the
+// product), so they are zeroed.
+template <int NB, int HD, int HPW>
+__device__ __forceinline__ void mask_page(f4 (&s)[NB], PageV<HD, HPW>& pv,
+                                          const unsigned long long (&dbits)[NB], int draft_base,
+                                          int tok0, int len) {
+  constexpr int VW = Dims<HD>::VW;
+  mask_scores<NB>(s, dbits, draft_base, tok0, len);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (tok0 + e >= len) {
+  for (int e = 0; e < 4; ++e) {
+    if (tok0 + e >= len) {
 #pragma unroll
-        for (int h = 0; h < HPW; ++h)
+      for (int h = 0; h < HPW; ++h)
 #pragma unroll
-          for (int i = 0; i < VW; ++i) pv.v[h][e][i] = 0u;
-      }
+        for (int i = 0; i < VW; ++i) pv.v[h][e][i] = 0u;
     }
   }
+}
 
-  // Lane-local max (4 tokens of one row); the row max is only reduced across
-  // the four 16-lane groups when some lane runs ahead of its running max.
-  float lm[NB];
+// The running max: lm[nb] holds this lane's max of its new scores (times c); the
+// row max is only reduced across the four 16-lane groups when some lane runs
+// ahead of its running max.
+template <int NB, int HD>
+__device__ __forceinline__ void raise_max(WaveState<NB, HD>& st, const float (&lm)[NB]) {
+  constexpr int MB = Dims<HD>::MB;
   bool grow = false;
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    lm[nb] = max4(s[nb]) * c;
-    grow |= lm[nb] > st.m[nb] + kMaxLag;
-  }
+  for (int nb = 0; nb < NB; ++nb) grow |= lm[nb] > st.m[nb] + kMaxLag;
   if (__any(grow)) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
@@ -492,7 +490,13 @@ __device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
       for (int mb = 0; mb < MB; ++mb) st.acc[mb][nb] *= alpha;
     }
   }
+}
 
+// One page's probabilities against the running max and its PV products.
+template <int NB, int HD, typename E, typename KV, int HPW>
+__device__ __forceinline__ void page_pv(WaveState<NB, HD>& st, const f4 (&s)[NB],
+                                        const PageV<HD, HPW>& pv, bool upper, float c) {
+  constexpr int MB = Dims<HD>::MB;
   // P = 2^(c*s - m), rounded once to the element type; with fp16 the row sum
   // is taken over the rounded values so O is an exact convex combination (with
   // bf16, P is hi + lo and the sum is within 2^-17 of it).
@@ -530,6 +534,20 @@ __device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
       }
     }
   }
+}
+
+template <int NB, int HD, typename E, typename KV, int HPW>
+__device__ __forceinline__ void page_finish(WaveState<NB, HD>& st, f4 (&s)[NB],
+                                            PageV<HD, HPW>& pv, bool upper,
+                                            const unsigned long long (&dbits)[NB],
+                                            int draft_base, int tok0, int len, bool masked,
+                                            float c) {
+  if (masked) mask_page<NB, HD, HPW>(s, pv, dbits, draft_base, tok0, len);
+  float lm[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) lm[nb] = max4(s[nb]) * c;
+  raise_max<NB, HD>(st, lm);
+  page_pv<NB, HD, E, KV, HPW>(st, s, pv, upper, c);
 }
 
 // Two pages in one softmax step: fp16 queries over an e4m3 cache at head dim
@@ -1150,7 +1168,8 @@ __device__ __forceinline__ void write_empty_split(const PartialArgs& a, const Ma
 // softmax state and writes its own partials (or, with a single split, the
 // output). Every K/V byte is read by one wave only, so the loads are
 // non-temporal.
-template <int NB, int D, int WW, int WPE, int HD, typename E, typename KV, int HPW>
+template <int NB, int D, int WW, int WPE, int HD, typename E, typename KV, int HPW,
+          bool RB = false>
 __global__ __launch_bounds__(WW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void sqa_partial_kernel(PartialArgs a) {
   constexpr int KK = Dims<HD>::KK, MB = Dims<HD>::MB;
@@ -1319,6 +1338,11 @@ void sqa_partial_kernel(PartialArgs a) {
   // pages two at a time (pair_finish).
   constexpr bool kPairSteps = __is_same(E, ElemF16) && KV::kBytes == 1 && HD == 128 &&
                               NB == 4 && HPW == 1 && D % 2 == 0;
+  // A piece that fits the ring in one softmax step (below), in the RB
+  // instantiations only (the host picks them for plans whose pieces fit the
+  // ring: with the step in it, the kernel's page loop for long pieces ran 1-2%
+  // slower): 16-bit K/V, whose ring registers the MFMAs read as they are.
+  constexpr bool kRingBatch = RB && KV::kBytes == 2 && HD <= 128;
   const bool upper = l16 >= 8;
   int next_pid = page_id(D);
   if constexpr (kPairSteps) {
@@ -1343,6 +1367,40 @@ void sqa_partial_kernel(PartialArgs a) {
         load_page(pid1, p_begin + ii + D + 1, ring[j + 1]);
       }
     }
+  } else if (kRingBatch && n_pages <= D) {  // uniform: the whole piece is in the ring
+    // Short pieces (one sequence of 8K keys in 4-page splits, every piece of a
+    // 1K-key sequence): the ring's pages arrive together, so they are taken in
+    // one softmax step, all scores first, one running-max update, then the PV
+    // products, instead of D dependent page steps (the MFMAs of all pages
+    // issue back to back; one sequence of 8K keys, whole calls: q_len 2 14.1
+    // -> 13.7 us, q_len 4 14.8 -> 14.2 us). Zero pages past the piece take no
+    // part.
+    f4 sb[D][NB];
+    PageV<HD, HPW> pvb[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      page_scores<NB, HD, E, KV, HPW>(sb[j], widen_k<E, KV, HD, HPW>(ring[j]), my_q, lane, upper);
+      pvb[j] = widen_v<E, KV, HD, HPW>(ring[j]);
+    }
+    float lm[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) lm[nb] = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int p = p_begin + j;
+      if (j >= n_pages) {  // uniform
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) sb[j][nb] = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      } else if ((p + 1) * kPageSize > mask_from) {  // uniform
+        mask_page<NB, HD, HPW>(sb[j], pvb[j], dbits, mask_from, p * kPageSize + 4 * g16, len);
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) lm[nb] = fmaxf(lm[nb], max4(sb[j][nb]) * a.scale_log2);
+    }
+    raise_max<NB, HD>(st, lm);
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+      if (j < n_pages) page_pv<NB, HD, E, KV, HPW>(st, sb[j], pvb[j], upper, a.scale_log2);
   } else {
   f4 s_cur[NB];
   if constexpr (kPipelined)
@@ -1966,6 +2024,7 @@ template <int HD, typename E, typename KV>
 void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, dim3 block,
                        hipStream_t stream) {
   constexpr int D4 = 4 * 128 / HD, D2 = 2 * 128 / HD;
+  static_assert(HD != 128 || D4 == kRingPages, "the host's ring-batch test assumes this ring");
   // e4m3 at head dim 128: 2 pages, or 4 under fp16 queries, whose pair steps
   // (pair_finish) need a second pair in flight while one is computed.
   constexpr int D3 = KV::kBytes == 1 ? (HD == 128 ? (__is_same(E, ElemF16) ? 4 : 2) : 3)
@@ -1984,9 +2043,23 @@ void launch_partial_hd(const PartialArgs& a, const LaunchShape& sh, dim3 grid, d
                            stream, a);
     }
   } else if (sh.row_blocks == 1) {
+    if constexpr (HD == 128 && KV::kBytes == 2) {
+      if (a.ring_batch) {
+        hipLaunchKernelGGL((sqa_partial_kernel<1, D4, 4, 1, HD, E, KV, 1, true>), grid, block, 0,
+                           stream, a);
+        return;
+      }
+    }
     hipLaunchKernelGGL((sqa_partial_kernel<1, D4, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
                        a);
   } else if (sh.row_blocks == 2) {
+    if constexpr (HD == 128 && KV::kBytes == 2) {
+      if (a.ring_batch) {
+        hipLaunchKernelGGL((sqa_partial_kernel<2, D4, 4, 1, HD, E, KV, 1, true>), grid, block, 0,
+                           stream, a);
+        return;
+      }
+    }
     hipLaunchKernelGGL((sqa_partial_kernel<2, D4, 4, 1, HD, E, KV, 1>), grid, block, 0, stream,
                        a);
   } else if constexpr (HD == 128 && KV::kBytes == 2) {

@@ -256,3 +256,24 @@ def test_balanced_plan_with_no_pages_at_all():
         out, ws = _run((q, k, v, bt, sl), ns, pps)
         assert torch.all(out == 0), pps
         assert [c for _, c in _plan_table(ws, (q, k, v, bt, sl), ns)] == [0] * len(lens)
+
+
+@pytest.mark.parametrize("q_len", [2, 4, 8])
+def test_pieces_that_fit_the_register_ring(q_len):
+    """Fixed plans of 1..4 pages per split and a balanced plan of 4-page items take
+    the whole ring in one softmax step (pieces of at most 4 pages at head dim 128):
+    pieces of 1..4 pages, partial last pages, the draft block inside the last
+    page or spanning two, against the float64 oracle."""
+    lens = [q_len, 17, 31, 64, 65, 100, 2 * q_len + 1, 260]
+    case = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=1900 + q_len)
+    tensors = _gpu(case)
+    ref = _oracle(tensors)
+    for pps in (1, 2, 3, 4):
+        ns = -(-max(-(-n // 16) for n in lens) // pps)
+        out, _ = _run(tensors, ns, pps)
+        assert_parity(out, ref, label=f"q{q_len} fixed {pps} pages")
+    uni = _gpu(inputs.Case(batch=4, q_len=q_len, seq_lens=[1000] * 4, seed=1950 + q_len))
+    pages = (1000 + 15) // 16
+    ns = 4 + pages  # items of 4 pages (63 pages x 4 sequences over 63 items)
+    out, _ = _run(uni, ns, -pages)
+    assert_parity(out, _oracle(uni), label=f"q{q_len} balanced 4-page items")
