@@ -108,14 +108,15 @@ int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int n
     }
     const long long splits = ceil_div(slots_target, batch);
     pps = ceil_div(pages, splits);
-    // Each split leaves a partial row per query row for the merge. Past 16
-    // rows, sequences of more than 64 four-page splits start at 8 pages: there
-    // the merge of the extra splits costs more than the shorter splits save
-    // (one sequence, KV 8K, per call: q8 21.4 us at 64 x 8 pages, 22.4 at 128
-    // x 4; q16 25.7 / 28.3), while shorter ones gain from 4 (KV 1K-4K, q8 and
-    // q16: 0.6-2.5 us per call).
-    const bool past16 = (long long)q_len * (num_query_heads / num_kv_heads) > 16;
-    const long long min_pps = past16 && pages > 64 * sqa::kMinSplitPages
+    // Each split leaves a partial row per query row for the merge. Past 32
+    // rows (the 64-row kernel), sequences of more than 64 four-page splits
+    // start at 8 pages: there the merge of the extra splits costs more than the
+    // shorter splits save (one sequence, KV 8K, q16, per call: 23.9 us at 64 x
+    // 8 pages, 26.7 at 128 x 4), while shorter ones gain from 4. Up to 32 rows
+    // 4-page pieces take the register ring in one softmax step, and 4 pages win
+    // (KV 8K, q8: 18.0 us at 128 x 4, 19.0 at 64 x 8).
+    const bool past32 = (long long)q_len * (num_query_heads / num_kv_heads) > 32;
+    const long long min_pps = past32 && pages > 64 * sqa::kMinSplitPages
                                   ? 2 * sqa::kMinSplitPages
                                   : sqa::kMinSplitPages;
     if (pps < min_pps) pps = min_pps;

@@ -133,7 +133,7 @@ def test_balanced_plan_on_a_skewed_batch(q_len):
 
 def test_single_sequence_automatic_plans():
     """One sequence (the fixed automatic plan; 128 slots per kv-head group on 256
-    CUs): splits of at least 4 pages, and past 16 rows per kv head at least 8 once
+    CUs): splits of at least 4 pages, and past 32 rows per kv head at least 8 once
     the sequence spans more than 256 pages; then parity on one short case of each."""
     def plan(q_len, kv):
         return _lib.plan_splits(0, 1, q_len, 32, 8, 128, kv, kv // 16, 0)
@@ -142,7 +142,7 @@ def test_single_sequence_automatic_plans():
         pytest.skip(f"plan figures below are for 256 CUs (this device: {cus})")
     assert plan(2, 1024) == (16, 4) and plan(2, 8192) == (128, 4)
     assert plan(8, 1024) == (16, 4) and plan(8, 4096) == (64, 4)
-    assert plan(8, 8192) == (64, 8) and plan(16, 8192) == (64, 8)
+    assert plan(8, 8192) == (128, 4) and plan(16, 8192) == (64, 8)
     assert plan(8, 32768) == (128, 16)
     for q_len, kv in ((8, 1000), (16, 4000)):
         case = inputs.Case(batch=1, q_len=q_len, seq_lens=[kv], seed=470 + q_len)
