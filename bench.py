@@ -216,7 +216,10 @@ def metric_grid(torch, lib, inputs, steps, warmup):
             case = inputs.uniform_case(b, max(GRID_Q_LENS), kv, seed=4000 + kv // 1024 + b)
             kvb = inputs.kv_bytes(case.seq_lens, case.num_kv_heads, case.head_dim)
             sets = input_sets(inputs, case, kvb)
-            n_steps = steps if kvb >= ROTATE_BELOW_BYTES else max(steps, 100)
+            # At least 100 calls below 512 MB of KV, 50 up to 2 GB: ~4-5 ms of calls
+            # per point, long enough that clocks settled by the ramp stay settled.
+            n_steps = max(steps, 100 if kvb < ROTATE_BELOW_BYTES else
+                          (50 if kvb < (2 << 30) else steps))
             for ql in GRID_Q_LENS:
                 qsets = []
                 for i, (q, k, v, bt, sl) in enumerate(sets):
@@ -226,7 +229,7 @@ def metric_grid(torch, lib, inputs, steps, warmup):
                     qsets.append((qx, k, v, bt, sl))
                 plan = lib.plan_splits(0, b, ql, case.num_query_heads, case.num_kv_heads,
                                        case.head_dim, kv, sets[0][3].shape[1], 0)
-                _ramp_clocks(torch, lib, qsets[0], plan, seconds=0.03)
+                _ramp_clocks(torch, lib, qsets[0], plan, seconds=0.1)
                 ms, _, _, out = time_calls(torch, lib, qsets, plan, n_steps, warmup,
                                            kernel_events=False)
                 if not torch.isfinite(out).all():
