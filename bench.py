@@ -216,9 +216,10 @@ def metric_grid(torch, lib, inputs, steps, warmup):
             case = inputs.uniform_case(b, max(GRID_Q_LENS), kv, seed=4000 + kv // 1024 + b)
             kvb = inputs.kv_bytes(case.seq_lens, case.num_kv_heads, case.head_dim)
             sets = input_sets(inputs, case, kvb)
-            # At least 100 calls below 512 MB of KV, 50 up to 2 GB: ~4-5 ms of calls
-            # per point, long enough that clocks settled by the ramp stay settled.
-            n_steps = max(steps, 100 if kvb < ROTATE_BELOW_BYTES else
+            # At least 400 calls below 512 MB of KV (6-12 ms: a run of 100 such
+            # calls varied by up to 10% from run to run on one box), 50 up to
+            # 2 GB (~4-5 ms).
+            n_steps = max(steps, 400 if kvb < ROTATE_BELOW_BYTES else
                           (50 if kvb < (2 << 30) else steps))
             for ql in GRID_Q_LENS:
                 qsets = []
