@@ -150,7 +150,16 @@ def raw_stream(device_index: int) -> int:
 
 def launch(query, key_cache, value_cache, block_tables, seq_lens, output, workspace,
            num_splits: int, pages_per_split: int, stream_handle: int, timing_events=None):
-    """Call ``sqa_paged_mtp_attention`` on raw device pointers of torch tensors."""
+    """Call ``sqa_paged_mtp_attention`` on raw device pointers of torch tensors.
+
+    The entry point reads fp16 elements through bare pointers, so any other
+    element type (a bf16 or e4m3 cache: :func:`launch_general`) is refused here
+    before the call; a 1-byte cache read as fp16 would run past its end."""
+    for name, t in (("query", query), ("key_cache", key_cache), ("value_cache", value_cache),
+                    ("output", output)):
+        if str(t.dtype) != "torch.float16":
+            raise TypeError(f"sqa_paged_mtp_attention takes fp16 tensors; {name} is {t.dtype} "
+                            "(bf16 or e4m3 caches go through launch_general)")
     lib = _LIB if _LIB is not None else load()
     b, q_len, hq, d = query.shape
     ev = None

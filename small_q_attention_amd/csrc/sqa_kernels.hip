@@ -334,6 +334,10 @@ struct WaveState {
   f4 acc[Dims<HD>::MB][NB];  // O^T blocks: lane l holds dims (HD/4)*(l/16)+(HD/16)*r+mb of row 16*nb+l%16
   float m[NB];     // reference max (log2 units, within kMaxLag of the true row max), same in all 4 lane groups
   float l[NB];     // partial row sum over this lane's tokens
+  // Kept with m by the page-pair steps (pair_finish): m + kMaxLag, and the
+  // exponent offset -(m, or 0 while m is -inf).
+  float thr[NB];
+  float nmu[NB];
 };
 
 // Padding of the LDS page-id table beyond the split's last page: covers the
@@ -351,7 +355,17 @@ __device__ __forceinline__ int clamp_page(int pid, long long num_pages) {
 // more than this, which after the first page is rare.
 constexpr float kMaxLag = 8.0f;
 
-__device__ __forceinline__ float max4(f4 v) { return fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])); }
+// max(a, b, c) as one v_max3_f32. fmaxf's IEEE-mode lowering quiets every
+// operand it cannot prove canonical (MFMA results among them) with an extra
+// v_max_f32 x, x, x first, doubling the instructions of the per-page score
+// maxima; scores are never signalling NaNs (products, sums and -inf selects),
+// so the plain instruction returns fmaxf's value.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max4(f4 v) { return max3_raw(max3_raw(v[0], v[1], v[2]), v[3], v[3]); }
 
 // Bytes {a.lo16, b.lo16} and {a.hi16, b.hi16} of two dwords (v_perm_b32).
 __device__ __forceinline__ unsigned pack_lo(unsigned a, unsigned b) {
@@ -570,26 +584,37 @@ __device__ __forceinline__ void pair_finish(WaveState<NB, 128>& st, f4 (&s0)[NB]
                                             float c) {
   using E = ElemF16;
   constexpr int MB = Dims<128>::MB;
-  if (masked) {
-    mask_scores<NB>(s0, dbits, draft_base, tok0, len);
-    mask_scores<NB>(s1, dbits, draft_base, tok0 + kPageSize, len);
+  // Both conditions are uniform over the wave and rare (pages at the draft
+  // block or the sequence end; the last pair of a piece of odd length): one
+  // branch keeps their selects out of the common step.
+  if (masked || !have1) {
+    if (masked) {
+      mask_scores<NB>(s0, dbits, draft_base, tok0, len);
+      mask_scores<NB>(s1, dbits, draft_base, tok0 + kPageSize, len);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (tok0 + e >= len) r0.v[e][0] = r0.v[e][1] = 0u;
-      if (tok0 + kPageSize + e >= len) r1.v[e][0] = r1.v[e][1] = 0u;
+      for (int e = 0; e < 4; ++e) {
+        if (tok0 + e >= len) r0.v[e][0] = r0.v[e][1] = 0u;
+        if (tok0 + kPageSize + e >= len) r1.v[e][0] = r1.v[e][1] = 0u;
+      }
+    }
+    if (!have1) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) s1[nb] = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     }
   }
-  if (!have1) {  // uniform over the wave
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) s1[nb] = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  }
 
+  // The step is VALU-bound (fp8 widening, 32 exponentials per lane): the
+  // pair's maxima as four v_max3 (no operand quieting), and the threshold and
+  // exponent offset kept with the running max instead of recomputed per step
+  // (cfg3 shape q16: 214.0 -> 205.0 us, bit-identical).
   float lm[NB];
   bool grow = false;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    lm[nb] = fmaxf(max4(s0[nb]), max4(s1[nb])) * c;
-    grow |= lm[nb] > st.m[nb] + kMaxLag;
+    lm[nb] = max3_raw(max3_raw(s0[nb][0], s0[nb][1], s0[nb][2]),
+                      max3_raw(s0[nb][3], s1[nb][0], s1[nb][1]),
+                      max3_raw(s1[nb][2], s1[nb][3], s1[nb][3])) * c;
+    grow |= lm[nb] > st.thr[nb];
   }
   if (__any(grow)) {
 #pragma unroll
@@ -597,6 +622,8 @@ __device__ __forceinline__ void pair_finish(WaveState<NB, 128>& st, f4 (&s0)[NB]
       const float mn = fmaxf(st.m[nb], xor_max(lm[nb]));
       const float alpha = fast_exp2(st.m[nb] - (mn == -INFINITY ? 0.f : mn));
       st.m[nb] = mn;
+      st.thr[nb] = mn + kMaxLag;
+      st.nmu[nb] = -(mn == -INFINITY ? 0.f : mn);
       st.l[nb] *= alpha;
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) st.acc[mb][nb] *= alpha;
@@ -606,13 +633,13 @@ __device__ __forceinline__ void pair_finish(WaveState<NB, 128>& st, f4 (&s0)[NB]
   u4 pp[NB];  // P^T of both pages: this lane's 4 tokens of page p, then of p + 1
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const float mu = st.m[nb] == -INFINITY ? 0.f : st.m[nb];
+    const float nmu = st.nmu[nb];
     u2 unused;
-    const u2 a0 = E::round_p(fast_exp2(fmaf(s0[nb][0], c, -mu)), fast_exp2(fmaf(s0[nb][1], c, -mu)),
-                             fast_exp2(fmaf(s0[nb][2], c, -mu)), fast_exp2(fmaf(s0[nb][3], c, -mu)),
+    const u2 a0 = E::round_p(fast_exp2(fmaf(s0[nb][0], c, nmu)), fast_exp2(fmaf(s0[nb][1], c, nmu)),
+                             fast_exp2(fmaf(s0[nb][2], c, nmu)), fast_exp2(fmaf(s0[nb][3], c, nmu)),
                              st.l[nb], unused);
-    const u2 a1 = E::round_p(fast_exp2(fmaf(s1[nb][0], c, -mu)), fast_exp2(fmaf(s1[nb][1], c, -mu)),
-                             fast_exp2(fmaf(s1[nb][2], c, -mu)), fast_exp2(fmaf(s1[nb][3], c, -mu)),
+    const u2 a1 = E::round_p(fast_exp2(fmaf(s1[nb][0], c, nmu)), fast_exp2(fmaf(s1[nb][1], c, nmu)),
+                             fast_exp2(fmaf(s1[nb][2], c, nmu)), fast_exp2(fmaf(s1[nb][3], c, nmu)),
                              st.l[nb], unused);
     pp[nb] = u4{a0[0], a0[1], a1[0], a1[1]};
   }
@@ -1316,6 +1343,8 @@ void sqa_partial_kernel(PartialArgs a) {
   for (int nb = 0; nb < NB; ++nb) {
     st.m[nb] = -INFINITY;
     st.l[nb] = 0.f;
+    st.thr[nb] = -INFINITY;
+    st.nmu[nb] = -0.f;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) st.acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
   }
@@ -1346,6 +1375,18 @@ void sqa_partial_kernel(PartialArgs a) {
   const bool upper = l16 >= 8;
   int next_pid = page_id(D);
   if constexpr (kPairSteps) {
+    // The Q fragments stay in registers for the whole loop (16 x 4 dwords; the
+    // ring, scores and accumulators take the 256 arch VGPRs, so they live in
+    // AGPRs, which the MFMAs read directly). Left to itself the compiler
+    // copied every fragment to a second set of AGPRs before each pair (104
+    // v_accvgpr_mov per 4 pages); the empty asm below states that the values
+    // sit in AGPRs at that point, and the copies are gone (cfg3 shape q16:
+    // 217.8 -> 209.6 us).
+    u4 qf[NB][KK];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) qf[nb][kk] = my_q[(nb * KK + kk) * 64 + lane];
     for (int i = 0; i < n_pages; i += D) {
 #pragma unroll
       for (int j = 0; j < D; j += 2) {
@@ -1353,10 +1394,24 @@ void sqa_partial_kernel(PartialArgs a) {
         if (ii < n_pages) {
           const int p = p_begin + ii;
           const bool masked = (p + 2) * kPageSize > mask_from;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+a"(qf[nb][kk]));
+          // Both pages' scores, their MFMA chains interleaved.
+          const PageK<HD, 1> k0 = widen_k<E, KV, HD, 1>(ring[j]);
+          const PageK<HD, 1> k1 = widen_k<E, KV, HD, 1>(ring[j + 1]);
           f4 s0[NB], s1[NB];
-          page_scores<NB, HD, E, KV, 1>(s0, widen_k<E, KV, HD, 1>(ring[j]), my_q, lane, upper);
-          page_scores<NB, HD, E, KV, 1>(s1, widen_k<E, KV, HD, 1>(ring[j + 1]), my_q, lane,
-                                        upper);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            s0[nb] = f4{0.f, 0.f, 0.f, 0.f};
+            s1[nb] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+              s0[nb] = E::mma_qk(k0.k[0][kk], qf[nb][kk], s0[nb]);
+              s1[nb] = E::mma_qk(k1.k[0][kk], qf[nb][kk], s1[nb]);
+            }
+          }
           pair_finish<NB>(st, s0, s1, ring[j][0], ring[j + 1][0], ii + 1 < n_pages, dbits,
                           mask_from, p * kPageSize + 4 * g16, len, masked, a.scale_log2);
         }
@@ -1663,6 +1718,8 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   for (int nb = 0; nb < NB; ++nb) {
     st.m[nb] = -INFINITY;
     st.l[nb] = 0.f;
+    st.thr[nb] = -INFINITY;
+    st.nmu[nb] = -0.f;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) st.acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
   }

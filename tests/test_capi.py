@@ -230,3 +230,18 @@ def test_noalloc_rejects_plans_beyond_its_scratch_before_any_device_call(lib):
     assert b"no-allocation" in lib.sqa_last_error()
     header = HEADER.read_text()
     assert "#define SQA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)" in header
+
+
+@pytest.mark.parametrize("dtype", ["float8_e4m3fn", "bfloat16", "float32"])
+def test_fp16_launcher_refuses_other_element_types(dtype):
+    """``sqa_paged_mtp_attention`` reads fp16 through bare pointers: the Python
+    launcher refuses any other cache type before the call (an e4m3 pool read as
+    fp16 would be read past its end)."""
+    import torch
+
+    q = torch.zeros(1, 2, 32, 128, dtype=torch.float16)
+    k = torch.zeros(4, 16, 8, 128, dtype=getattr(torch, dtype))
+    bt = torch.zeros(1, 4, dtype=torch.int32)
+    sl = torch.full((1,), 64, dtype=torch.int32)
+    with pytest.raises(TypeError, match="launch_general"):
+        _lib.launch(q, k, k, bt, sl, torch.empty_like(q), None, 1, 4, 0)
