@@ -355,15 +355,15 @@ __device__ __forceinline__ int clamp_page(int pid, long long num_pages) {
 // more than this, which after the first page is rare.
 constexpr float kMaxLag = 8.0f;
 
-// max(a, b, c) as one v_max3_f32. fmaxf's IEEE-mode lowering quiets every
-// operand it cannot prove canonical (MFMA results among them) with an extra
-// v_max_f32 x, x, x first, doubling the instructions of the per-page score
-// maxima; scores are never signalling NaNs (products, sums and -inf selects),
-// so the plain instruction returns fmaxf's value.
+// max(a, b, c) as one v_maximum3_f32 (IEEE maximum: a NaN operand gives NaN).
+// fmaxf (maxnum) makes the compiler quiet every operand it cannot prove
+// canonical, MFMA results among them, with an extra v_max_f32 x, x, x first,
+// which doubled the instructions of the per-page score maxima. The two agree
+// except where a score is NaN, and such a score's row is NaN either way (its
+// probability enters the row's sums). Invisible tokens are masked to -inf
+// before any maximum is taken.
 __device__ __forceinline__ float max3_raw(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 __device__ __forceinline__ float max4(f4 v) { return max3_raw(max3_raw(v[0], v[1], v[2]), v[3], v[3]); }
 
