@@ -503,31 +503,50 @@ def main():
         result["bf16"] = {"kernel_us": round(pb * 1e3, 2),
                           "kernel_frac": round(kvb / (pb * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
         del qb, kb, vb, outb, wsb
-        # fp16 queries over an OCP e4m3 cache of the same shape (half the KV bytes).
+        # fp16 queries over an OCP e4m3 cache of the same shape (half the KV bytes):
+        # the workload's q_len, and q_len 16 (64 rows per kv head, the
+        # compute-heaviest e4m3 kernel).
         k8, v8 = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
-        out8 = torch.empty_like(q)
-        ws8 = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
 
-        def fp8_call(ev=None):
-            _lib.launch_general(q, out8, k8, v8, bt, sl, None, case.head_dim ** -0.5, 1.0,
-                                plan[0], plan[1], ws8, handle, timing_events=ev)
+        def fp8_kernel_ms(qx):
+            plan8 = _lib.plan_splits(0, case.batch, qx.shape[1], case.num_query_heads,
+                                     case.num_kv_heads, case.head_dim, case.max_seq_len,
+                                     bt.shape[1], 0)
+            n8 = _lib.workspace_bytes(case.batch, qx.shape[1], case.num_query_heads,
+                                      case.num_kv_heads, case.head_dim, plan8[0], plan8[1])
+            out8 = torch.empty_like(qx)
+            ws8 = torch.empty(max(n8, 1), dtype=torch.uint8, device="cuda")
 
-        t0 = time.perf_counter()
-        while time.perf_counter() - t0 < 0.1:
-            fp8_call()
+            def fp8_call(ev=None):
+                _lib.launch_general(qx, out8, k8, v8, bt, sl, None, case.head_dim ** -0.5, 1.0,
+                                    plan8[0], plan8[1], ws8, handle, timing_events=ev)
+
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < 0.1:
+                fp8_call()
+                torch.cuda.synchronize()
+            for _ in range(args.warmup):
+                fp8_call()
+            kev = _events(torch, 3 * args.steps)
             torch.cuda.synchronize()
-        for _ in range(args.warmup):
-            fp8_call()
-        kev = _events(torch, 3 * args.steps)
-        torch.cuda.synchronize()
-        for i in range(args.steps):
-            fp8_call([e.cuda_event for e in kev[3 * i:3 * i + 3]])
-        torch.cuda.synchronize()
-        p8 = statistics.mean(kev[3 * i].elapsed_time(kev[3 * i + 1]) for i in range(args.steps))
+            for i in range(args.steps):
+                fp8_call([e.cuda_event for e in kev[3 * i:3 * i + 3]])
+            torch.cuda.synchronize()
+            return statistics.mean(kev[3 * i].elapsed_time(kev[3 * i + 1])
+                                   for i in range(args.steps))
+
+        p8 = fp8_kernel_ms(q)
+        g16 = torch.Generator(device="cuda").manual_seed(case.seed + 16)
+        q16 = torch.randn(case.batch, 16, case.num_query_heads, case.head_dim, generator=g16,
+                          device="cuda", dtype=torch.float16)
+        p16 = fp8_kernel_ms(q16)
         result["fp8_kv"] = {"kernel_us": round(p8 * 1e3, 2), "kv_bytes": kvb // 2,
                             "kernel_frac": round(kvb / 2 / (p8 * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
-                            "speedup_vs_fp16_kv": round(part_ms / p8, 3)}
-        del k8, v8, out8, ws8
+                            "speedup_vs_fp16_kv": round(part_ms / p8, 3),
+                            "q16": {"kernel_us": round(p16 * 1e3, 2),
+                                    "kernel_frac": round(kvb / 2 / (p16 * 1e-3) / 1e9 /
+                                                         PEAK_HBM_GBPS, 4)}}
+        del k8, v8, q16
     if not args.no_per_q and default_types:
         # The other single-GPU benchmark configs, same timing (extra fields only).
         others = {}
