@@ -1071,7 +1071,9 @@ __device__ __forceinline__ void write_results(const PartialArgs& a, WaveState<NB
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     if (map.row(nb, 0) >= a.rows) break;  // uniform
-    const float inv_l = st.l[nb] > 0.f ? 1.f / st.l[nb] : 0.f;
+    // l = 0: the row saw no key (written as 0). A NaN l (a NaN score or
+    // probability the row saw) passes, so the NaN reaches the row's output.
+    const float inv_l = !(st.l[nb] <= 0.f) ? 1.f / st.l[nb] : 0.f;
     const float sc = direct ? a.out_scale * inv_l : (E::kHalfPartials ? inv_l : 1.f);
     if (map.real(nb, l16)) {
       float* dst = stage + l16 * kStageRow + (HD / 4) * g16;
@@ -1158,8 +1160,10 @@ __device__ __forceinline__ void write_results(const PartialArgs& a, WaveState<NB
       }
       if (g16 == 0 && map.real(nb, l16)) {
         const size_t pitem = item_of(nb, l16) + map.row(nb, l16);
+        // A NaN sum travels with a finite max, so the merge counts the split.
+        const float m_out = st.l[nb] == st.l[nb] ? st.m[nb] : 0.f;
         store_through(a.part_ml + pitem * 2,
-                      __builtin_bit_cast(unsigned long long, float2{st.m[nb], st.l[nb]}));
+                      __builtin_bit_cast(unsigned long long, float2{m_out, st.l[nb]}));
       }
     }
   }
@@ -1947,7 +1951,7 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   auto add_round = [&]() {
     float cm = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < U; ++u) cm = l[u] > 0.f ? fmaxf(cm, m[u]) : cm;
+    for (int u = 0; u < U; ++u) cm = !(l[u] <= 0.f) ? fmaxf(cm, m[u]) : cm;
     const float nm = fmaxf(mt, cm);
     if (nm != -INFINITY) {
       const float sc = mt == -INFINITY ? 0.f : fast_exp2(mt - nm);
@@ -1957,8 +1961,9 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         // Splits without keys (l <= 0) never touch the sums: their partial sums
-        // were never written and may hold anything.
-        const bool use = l[u] > 0.f;
+        // were never written and may hold anything. A NaN sum (the split saw a
+        // NaN) is used, so the row comes out NaN.
+        const bool use = !(l[u] <= 0.f);
         const float w = use ? fast_exp2(m[u] - nm) : 0.f;
         den += w * l[u];
         // Normalised partials weigh in with their sum.
@@ -2052,7 +2057,7 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
     }
   }
   if (skip || g != 0) return;
-  const float inv = den > 0.f ? a.out_scale / den : 0.f;
+  const float inv = !(den <= 0.f) ? a.out_scale / den : 0.f;  // 0: no key; NaN stays NaN
   if constexpr (DPT == 8) {
     // Two 8-byte stores: the output need only be 8-byte aligned.
     const float lo[4] = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
@@ -2069,9 +2074,11 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
 // Ring depth: the pages in flight per wave hold about 32 KiB of 16-bit K and
 // V: 4 pages at head dim 128 (3 at 64 rows, where the registers run out), 8 at
 // head dim 64 (4 at 64 rows: bf16 q16 201.5 -> 194.5 us, fp16 174.5 -> 173.9)
-// and 2 at 256, which holds at most 32 rows (its accumulators double). e4m3 caches keep the same page counts although their pages hold
-// half the bytes, and fewer at 64 rows (2 pages at head dim 128, 3 at 64): the
-// widened K and V fragments take the registers a deeper ring would need.
+// and 2 at 256, which holds at most 32 rows (its accumulators double). e4m3
+// caches keep the same page counts although their pages hold half the bytes,
+// and at 64 rows 3 at head dim 64 and, at head dim 128, 2 under bf16 queries
+// or 4 under fp16 ones (two page pairs): the widened K and V fragments take
+// the registers a deeper ring would need.
 // Measured at 16 sequences of 32K keys, partial kernel, e4m3 ring at twice
 // these depths -> these: head dim 128 q2 / q8 170.7 / 181.4 -> 169.7 / 174.2
 // us, q16 278 (6 pages) -> 261 (3) -> 251 us (2); head dim 256 q8 342.7 ->
