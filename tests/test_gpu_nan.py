@@ -43,8 +43,8 @@ def _announce(request):
     sys.__stderr__.flush()
 
 
-def _inputs(q_len, kv, seed):
-    c = inputs.Case(batch=len(LENS), q_len=q_len, seq_lens=LENS, seed=seed)
+def _inputs(q_len, kv, seed, lens=LENS):
+    c = inputs.Case(batch=len(lens), q_len=q_len, seq_lens=lens, seed=seed)
     q, k, v, bt, sl = (t.cuda() for t in inputs.make_inputs(c))
     if kv == "e4m3":
         k, v = k.to(F8), v.to(F8)
@@ -62,7 +62,7 @@ def _poison(cache, bt, b, t, head, dim):
 
 def _run(q, k, v, bt, sl, chunk):
     b, q_len, hq, d = q.shape
-    ns, pps = _lib.plan_splits(0, b, q_len, hq, k.shape[2], d, max(LENS), bt.shape[1], chunk)
+    ns, pps = _lib.plan_splits(0, b, q_len, hq, k.shape[2], d, int(sl.max()), bt.shape[1], chunk)
     nbytes = _lib.workspace_bytes(b, q_len, hq, k.shape[2], d, ns, pps)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
     out = torch.empty_like(q)
@@ -124,3 +124,23 @@ def test_nan_value_in_a_draft_token(kv):
     r16 = ref.astype(np.float16).astype(np.float64)
     assert np.isfinite(out[keep]).all()
     assert np.all(np.abs(out[keep] - r16[keep]) <= TOL_ABS + TOL_REL * np.abs(r16[keep]))
+
+
+@pytest.mark.parametrize("q_len", [2, 8])
+@pytest.mark.parametrize("kv", ["fp16", "e4m3"])
+def test_nan_single_sequence_whole_ring_pieces(kv, q_len):
+    """One sequence of 4096 keys: the automatic plan cuts it into 4-page splits,
+    which the 16-bit kernels take in one softmax step over the whole register
+    ring (scores of all pages, then one running-max update)."""
+    lens = [4096]
+    q, k, v, bt, sl = _inputs(q_len, kv, seed=1780 + q_len, lens=lens)
+    ns, pps = _lib.plan_splits(0, 1, q_len, 32, 8, 128, 4096, bt.shape[1], 0)
+    assert pps == 4, (ns, pps)
+    _poison(k, bt, 0, 1000, 3, 17)                   # prefix key: heads 12-15
+    _poison(v, bt, 0, 2000, 6, 5)                    # prefix value: dim 5 of heads 24-27
+    _poison(k, bt, 0, lens[0] - q_len + 1, 5, 64)    # draft key 1: rows qi >= 1, heads 20-23
+    q[0, q_len - 1, 30, 7] = float("nan")
+    ref = attention_c64(*(t.cpu() for t in (q, k, v, bt, sl)), 16, 8)
+    out = _run(q, k, v, bt, sl, 0)
+    _compare(out, ref, f"{kv} q{q_len} one sequence")
+    assert torch.isfinite(out[0, 0, 20:24].float()).all()
