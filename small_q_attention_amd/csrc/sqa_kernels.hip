@@ -1464,11 +1464,13 @@ void sqa_partial_kernel(PartialArgs a) {
   f4 s_cur[NB];
   if constexpr (kPipelined)
     page_scores<NB, HD, E, KV, HPW>(s_cur, widen_k<E, KV, HD, HPW>(ring[0]), my_q, lane, upper);
-  // 64 rows over e4m3 outside the page pairs (bf16 queries): the Q fragments
-  // held in AGPRs for the loop, pinned there as in the pair loop (the compiler
-  // had copied them between AGPR sets every page; cfg3 shape q16 283.7 ->
-  // 271.0 us).
-  constexpr bool kQRegs = NB == 4 && KV::kBytes == 1 && HPW == 1 && !kPipelined;
+  // 64 rows over e4m3 outside the page pairs (bf16 queries), and head dim 256:
+  // the Q fragments held in AGPRs for the loop, pinned there as in the pair
+  // loop (the compiler had copied them between AGPR sets every page; cfg3
+  // shape: bf16 / e4m3 q16 283.7 -> 271.0 us, head dim 256 q8 680.5 -> 668.7
+  // us, e4m3 324.2 -> 322.2 us).
+  constexpr bool kQRegs =
+      ((NB == 4 && KV::kBytes == 1) || HD == 256) && HPW == 1 && !kPipelined;
   u4 qf[kQRegs ? NB : 1][KK];
   if constexpr (kQRegs) {
 #pragma unroll
