@@ -604,7 +604,7 @@ __device__ __forceinline__ void pair_finish(WaveState<NB, 128>& st, f4 (&s0)[NB]
   }
 
   // The step is VALU-bound (fp8 widening, 32 exponentials per lane): the
-  // pair's maxima as four v_max3 (no operand quieting), and the threshold and
+  // pair's maxima as four v_maximum3 (no operand quieting), and the threshold and
   // exponent offset kept with the running max instead of recomputed per step
   // (cfg3 shape q16: 214.0 -> 205.0 us, bit-identical).
   float lm[NB];
