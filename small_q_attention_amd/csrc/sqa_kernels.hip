@@ -1618,11 +1618,14 @@ struct LdsSlice<KvNative<128>> {
 // (load_to_lds: 1 KiB of a head's page slice per wave and load, in the layout of
 // LdsSlice), so the bytes in flight take no registers. Per page: wait for this
 // thread's loads of the page (manual vmcnt: nothing else in the loop touches
-// vector memory), a barrier (the page is in LDS), read the wave's K and V into
-// registers, a second barrier (every wave has read the slot), refill the slot
-// with the page D ahead, then the math: a slot is refilled before its page's
-// math, so D pages stay in flight. Pages past the split load through a
-// zero-length resource (zeros, no memory traffic), as in sqa_partial_kernel.
+// vector memory), one barrier (the page is in LDS, and every wave has read the
+// previous page's slot, which it did before that page's math), read the wave's K
+// and V into registers, refill the previous page's slot with the page D - 1
+// ahead, then the math: D - 1 pages stay in flight. One barrier a page rather
+// than two (read, barrier, refill this page's slot with D in flight) measured
+// 0.3% faster for fp16 and 3.8% for bf16 at KV 32K x 16 sequences. Pages past the
+// split load through a zero-length resource (zeros, no memory traffic), as in
+// sqa_partial_kernel.
 template <int D, typename E, typename KV>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void sqa_partial_lds_kernel(PartialArgs a) {
@@ -1743,7 +1746,7 @@ void sqa_partial_lds_kernel(PartialArgs a) {
                   (unsigned)(size_t)(sm_ring + j * kSlot + (8 * i + wave) * 1024));
   };
 #pragma unroll
-  for (int j = 0; j < D; ++j)
+  for (int j = 0; j < D - 1; ++j)
     issue_page(j < n_split ? clamp_page(first_id[j], a.num_pages) : -1, p_begin + j, j);
 #pragma unroll
   for (int k = 0; k < kIdSlots; ++k) {
@@ -1765,21 +1768,20 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   __syncthreads();  // sm_ids written
 
   const unsigned long long t_loop = it.paired ? __builtin_amdgcn_s_memrealtime() : 0;
-  int next_pid = sm_ids[D];
+  int next_pid = sm_ids[D - 1];
   for (int i = 0; i < n_split; i += D) {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
       const int ii = i + j;
       if (ii < n_split) {  // uniform over the workgroup
-        wait_vmcnt<kLoads * (D - 1)>();  // this thread's loads of page ii
-        __syncthreads();                  // everyone's: page ii is in slot j
+        wait_vmcnt<kLoads * (D - 2)>();  // this thread's loads of page ii
+        __syncthreads();  // page ii is in slot j; every wave is done with page ii - 1
         const char* ks = sm_ring + j * kSlot + hs * kHeadSlice;
         typename KV::Regs raw[1];
         L::read(raw[0], ks, ks + 4 * kHeadSlice, g16, l16);
-        __syncthreads();  // every wave has read slot j
         const int pid = next_pid;
-        next_pid = sm_ids[ii + D + 1];
-        issue_page(pid, p_begin + ii + D, j);
+        next_pid = sm_ids[ii + D];
+        issue_page(pid, p_begin + ii + D - 1, (j + D - 1) % D);
         if (active) {
           const int p = p_begin + ii;
           const bool masked = (p + 1) * kPageSize > mask_from;
