@@ -212,9 +212,10 @@ constexpr int kRingPages = 4;
 // dim 128, fp16), where one page of the workgroup's (16 tokens of K and V for 4
 // kv heads, 32 KiB) takes ~1.15 us; scaled by the bytes of a workgroup's page
 // for other shapes and element types. The 8-wave LDS kernel (33..64 rows, head
-// dim 128, 16-bit K/V) restarts a ring behind two barriers per page and writes
+// dim 128, 16-bit K/V) restarts a ring behind a barrier per page and writes
 // 64 rows per head: 8 pages measured best there (ragged q16 fp16 190.2 -> 187.8
-// us, bf16 194.4 -> 190.2; 12 pages 187.8 / 190.8).
+// us, bf16 194.4 -> 190.2; 12 pages 187.8 / 190.8; with one barrier per page
+// partial 183.0 / 180.7 / 181.3 us at 5 / 8 / 11 pages).
 inline int seam_pages(int rows, int hkv, int head_dim, int kv_bytes) {
   const LaunchShape sh = launch_shape(rows, hkv, head_dim);
   const int wg_page = 16 * sh.heads * head_dim * 2 * kv_bytes;
