@@ -181,14 +181,18 @@ typedef struct sqa_kv_cache {
  */
 
 /*
- * SQA_FLAG_ADAPTIVE_PAIRS: let the balanced plan's 64-row fp16 kernel (33..64
- * rows per kv head, head_dim 128, 8 kv heads, every sequence of the expected
- * max_seq_len) move the boundary between work items 2k and 2k + 1 by a share
- * that it measures from the previous call's page-loop times, kept in the
- * workspace (about 1.5% faster at 16 x 32K keys, q_len 16, on boxes whose XCDs
- * stream at different rates). The output then depends on that share within the
- * parity tolerance, so identical calls and graph replays may differ in their last
- * bits; without the flag they never do.
+ * Paired work items: the balanced plan's 64-row kernel (33..64 rows per kv
+ * head, head_dim 128, 16-bit K/V, 8 kv heads, every sequence of the expected
+ * max_seq_len, pairs of items dividing a sequence) gives work items 2k and
+ * 2k + 1 unequal shares of their pages, the even one 3% more, because the XCDs
+ * that run the odd ones stream that kernel's pages more slowly (measured on
+ * every box; 2% faster at 16 x 32K keys, q_len 16). The shares follow from the
+ * plan alone: equal inputs give equal bits.
+ *
+ * SQA_FLAG_ADAPTIVE_PAIRS: instead of the fixed 3%, a share measured from the
+ * previous call's page-loop times, kept in the workspace. The output then
+ * depends on that share within the parity tolerance, so identical calls and
+ * graph replays may differ in their last bits; without the flag they never do.
  */
 #define SQA_FLAG_ADAPTIVE_PAIRS 1
 typedef struct sqa_attention_args {

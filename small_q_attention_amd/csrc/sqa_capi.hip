@@ -307,16 +307,19 @@ int run_attention(const sqa_attention_args& a) {
   pa.spec_pps =
       spec_pages > 0 ? sqa::packed_item_pages(batch * spec_pages, num_splits - batch) : 0;
   pa.seam_pages = balanced ? sqa::seam_pages((int)rows, num_kv_heads, head_dim, (int)kv_bytes) : 0;
-  // Paired items, on request only (they make the output depend on measured
-  // times): the 64-row kernel (33..64 rows, head dim 128) with fp16 Q, K and V
-  // (bf16 measured 0.2-1.4% slower with them: more math per page, and fp32
-  // partials), two head groups of four kv heads, an expected page count that
-  // pairs of items divide, and an even item count.
+  // Paired items: the 64-row kernel (33..64 rows, head dim 128) with 16-bit K
+  // and V, two head groups of four kv heads, an expected page count that pairs
+  // of items divide, and an even item count. By default with the fixed delta
+  // (the bits depend on the inputs alone); with SQA_FLAG_ADAPTIVE_PAIRS with the
+  // measured one (the bits follow the previous call's times).
   pa.tune = balanced ? (float*)(pa.seq_splits + batch) : nullptr;
-  pa.pair_items = (a.flags & SQA_FLAG_ADAPTIVE_PAIRS) && balanced && spec_pages > 0 && pa.spec_pps > 0 &&
-                  spec_pages % (2 * pa.spec_pps) == 0 && (num_splits - batch) % 2 == 0 &&
-                  head_dim == 128 && kv_bytes == 2 && a.dtype == SQA_DTYPE_F16 && rows > 32 &&
-                  rows <= 64 && num_kv_heads == 8;
+  const bool pair_ok = balanced && spec_pages > 0 && pa.spec_pps > 0 &&
+                       spec_pages % (2 * pa.spec_pps) == 0 && (num_splits - batch) % 2 == 0 &&
+                       head_dim == 128 && kv_bytes == 2 && rows > 32 && rows <= 64 &&
+                       num_kv_heads == 8;
+  pa.pair_items = !pair_ok                              ? sqa::kPairsOff
+                  : (a.flags & SQA_FLAG_ADAPTIVE_PAIRS) ? sqa::kPairsAdaptive
+                                                        : sqa::kPairsFixed;
   // Pieces that fit the register ring take it in one softmax step: fixed plans
   // of at most kRingPages pages per split, balanced plans whose expected items
   // are that short (pieces can only be shorter than their item).
@@ -353,7 +356,7 @@ int run_attention(const sqa_attention_args& a) {
     ma.spec_pps = pa.spec_pps;
     ma.out_scale = a.out_scale;
     ma.bf16 = pa.bf16;
-    ma.tune = pa.pair_items ? pa.tune : nullptr;
+    ma.tune = pa.pair_items == sqa::kPairsAdaptive ? pa.tune : nullptr;
     ma.tune_records = (num_splits - batch) * 2;
     if ((e = sqa::launch_merge(ma, s)) != hipSuccess) return hip_fail(e, "merge kernel launch");
   }

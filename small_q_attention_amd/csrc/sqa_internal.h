@@ -68,20 +68,25 @@ struct SeqSplits {
 // 2k and 2k + 1 share 2P pages, the even one taking P + d and the odd one
 // P - d, d = round(P * delta), and both workgroups of item i (one per head
 // group) run on XCDs of i's parity (blockIdx.x = 4k + 2 head_group + (i & 1);
-// workgroups are dealt to the XCDs in turn). The XCDs of one parity stream
-// faster than the others on these boxes, by a margin that depends on the box
-// and the access pattern, so delta is measured rather than fixed: each
-// workgroup records its page-loop time and pages, and the merge kernel sets
-// delta for the next call from the per-page times of even and odd items.
-// Every workgroup of a call reads the same value, and any delta covers every
-// key once, so results stay within the parity tolerance; but the split point
-// changes how the fp16-normalised partials round, so the output bits follow
-// delta. Pairing therefore runs only when the caller asks for it
-// (SQA_FLAG_ADAPTIVE_PAIRS); otherwise equal inputs give equal bits.
-// Workgroup 0 of a paired call stamps tune[2] (kTuneStamp), every workgroup of
-// it writes its record, and the merge kernel reads the records only under that
-// stamp, then clears it: records of an earlier call or another shape's data in
-// a reused workspace never feed the delta.
+// workgroups are dealt to the XCDs in turn). The 64-row kernel streams its
+// pages more slowly on the odd XCDs: per-workgroup stamps at 16 sequences of
+// 32K keys put the odd XCDs' workgroups 6-8% behind the even ones' on every box
+// measured (the head group adds 1-2%), so by default (kPairsFixed) the even
+// items take kPairDeltaFixed more pages: the split depends on the plan alone
+// and equal inputs give equal bits. On request (kPairsAdaptive,
+// SQA_FLAG_ADAPTIVE_PAIRS) delta is measured instead: each workgroup records
+// its page-loop time and pages, and the merge kernel sets delta for the next
+// call from the per-page times of even and odd items. Every workgroup of a call
+// reads the same value, and any delta covers every key once, so results stay
+// within the parity tolerance; but the split point changes how the
+// fp16-normalised partials round, so with adaptive pairs the output bits follow
+// the previous call's times.
+// Workgroup 0 of an adaptive paired call stamps tune[2] (kTuneStamp), every
+// workgroup of it writes its record, and the merge kernel reads the records only
+// under that stamp, then clears it: records of an earlier call or another
+// shape's data in a reused workspace never feed the delta.
+constexpr int kPairsOff = 0, kPairsAdaptive = 1, kPairsFixed = 2;  // PartialArgs::pair_items
+constexpr float kPairDeltaFixed = 0.03f;  // even items' extra share with fixed pairs
 constexpr unsigned kTuneMagic = 0x51a7u << 16 | 1u;  // tune[0] when tune[1] holds a delta
 constexpr unsigned kTuneStamp = 0x51a7u << 16 | 2u;  // tune[2] after a call that ran paired
 constexpr float kPairDeltaMax = 0.1f;                // |delta| bound
@@ -114,10 +119,10 @@ struct PartialArgs {
   int spec_pages;             // balanced plan: expected pages of every sequence (0: none)
   int spec_pps;               // the balanced plan's item size when every sequence spans spec_pages
   int seam_pages;             // balanced plan: pages a second piece costs a workgroup (0: no gaps)
-  int pair_items;             // paired items on (see above)
+  int pair_items;             // kPairsOff, kPairsAdaptive or kPairsFixed (see above)
   int ring_batch;             // every piece expected within the register ring (kRingPages)
-  float* tune;                // paired items: {magic, delta, stamp, -} then per workgroup
-                              // {loop ticks, pages}
+  float* tune;                // adaptive paired items: {magic, delta, stamp, -} then per
+                              // workgroup {loop ticks, pages}
   float scale_log2;           // softmax scale * log2(e)
   float out_scale;            // multiplier applied to the normalised output
   int bf16;                   // element type of Q and out (and of K, V unless kv_fp8): 0 fp16, 1 bf16
@@ -150,7 +155,7 @@ struct MergeArgs {
   int spec_pps;     // the balanced plan's item size when that holds
   float out_scale;
   int bf16;
-  float* tune;      // paired items: the delta record to update (null: none)
+  float* tune;      // adaptive paired items: the delta record to update (null: none)
   int tune_records; // workgroup records after it
 };
 

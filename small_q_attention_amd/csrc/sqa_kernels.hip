@@ -954,14 +954,18 @@ __device__ __forceinline__ bool for_each_piece(const PartialArgs& a, int item, P
         }
       }
       // Paired items: the shared boundary of items 2k and 2k + 1 moves by d
-      // pages; the delta record is read with the lengths, the first ids after.
+      // pages; delta is the fixed one, or (adaptive pairs) the record's, read
+      // with the lengths, the first ids after.
       paired = a.pair_items != 0;
       int g0 = item * pb.P;
       item_end = g0 + pb.P;
       if (paired) {
-        const float2 rec = *(const float2*)a.tune;
+        float dl = kPairDeltaFixed;
+        if (a.pair_items == kPairsAdaptive) {
+          const float2 rec = *(const float2*)a.tune;
+          dl = __float_as_uint(rec.x) == kTuneMagic ? rec.y : 0.f;
+        }
         load_lengths(a, pb.len);
-        float dl = __float_as_uint(rec.x) == kTuneMagic ? rec.y : 0.f;
         dl = dl == dl ? fminf(fmaxf(dl, -kPairDeltaMax), kPairDeltaMax) : 0.f;
         // Both items of a pair stay within kMaxSplitPages (the page-id table).
         const int dmax = kMaxSplitPages - pb.P;
@@ -1812,11 +1816,11 @@ void sqa_partial_lds_kernel(PartialArgs a) {
     write_results<NB, HD, E>(a, st, (float*)sm_ring + wave * 16 * (HD + 4), map, direct,
                              !single && !balanced, b, slot);
   });
-  // A paired call (the same answer in every workgroup) leaves a record from
-  // every workgroup. Whenever pairing was asked for, workgroup 0 stamps the call
-  // (or clears the stamp when the lengths made it fall back): the merge kernel
-  // reads the records only under a stamp of this call.
-  if (a.pair_items && threadIdx.x == 0) {
+  // An adaptive paired call (the same answer in every workgroup) leaves a record
+  // from every workgroup. Whenever adaptive pairing was asked for, workgroup 0
+  // stamps the call (or clears the stamp when the lengths made it fall back):
+  // the merge kernel reads the records only under a stamp of this call.
+  if (a.pair_items == kPairsAdaptive && threadIdx.x == 0) {
     if (paired_call)
       *(int2*)(a.tune + 4 + 2 * blockIdx.x) =
           int2{__float_as_int(loop_ticks), loop_pages | (item & 1) << 30 | 1 << 31};

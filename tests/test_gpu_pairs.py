@@ -1,15 +1,16 @@
-"""Paired items on the GPU (the 64-row kernel with the expected-page plan), which
-run only under ``SQA_FLAG_ADAPTIVE_PAIRS``.
+"""Paired items on the GPU (the 64-row kernel with the expected-page plan).
 
 Items 2k and 2k + 1 share 2P pages, the even one taking P + d and the odd one
-P - d, d = round(P * delta), with delta read from a record in the workspace that
-the merge kernel updates from the workgroups' page-loop times. Results must not
+P - d, d = round(P * delta): by default delta is fixed (0.03), under
+``SQA_FLAG_ADAPTIVE_PAIRS`` it is read from a record in the workspace that the
+merge kernel updates from the workgroups' page-loop times. Results must not
 depend on delta:
 
 * parity with the float64 oracle for delta forced to -0.1, -0.05, 0, 0.03 and
   0.1 (the bound), to NaN and to a record without its magic word (both: delta
-  0), at q_len 16 (fp16: bf16 keeps the usual layout), cache pages of 16 and
-  64 tokens, and a tree mask;
+  0), at q_len 16 (fp16 and bf16), cache pages of 16 and 64 tokens, and a tree
+  mask;
+* a default call gives the bits of an adaptive one whose record holds 0.03;
 * after each call the record holds the magic word and a delta within the
   bound, and every loop-time record has been consumed (marked read);
 * calls in a row (delta moving between them) stay within tolerance and the
@@ -64,8 +65,9 @@ def _seed(ws, off, magic, delta):
         np.frombuffer(struct.pack("<If", magic, delta), dtype=np.uint8), device=ws.device)
 
 
-@pytest.mark.parametrize("qdt,page,tree", [(torch.float16, 16, False), (torch.float16, 64, True)],
-                         ids=["page16", "page64-tree"])
+@pytest.mark.parametrize("qdt,page,tree", [(torch.float16, 16, False), (torch.float16, 64, True),
+                                            (torch.bfloat16, 16, False)],
+                         ids=["page16", "page64-tree", "bf16"])
 def test_paired_items_any_delta(qdt, page, tree):
     q_len, batch, seq_pages, n_items = 16, 2, 256, 16  # items of 32 pages, pairs of 64
     lens = [seq_pages * 16] * batch
@@ -127,12 +129,17 @@ def test_paired_items_at_the_item_size_limit():
     torch.cuda.synchronize()
     ref = torch_fp32_reference(q, k, v, bt, sl, 16, HKV)
     assert_parity(out, ref, label="P = 2048, delta 0.1")
+    fixed = torch.full_like(q, float("nan"))  # the default's fixed delta, held to 0 too
+    _lib.launch_general(q, fixed, k, v, bt, sl, None, HD ** -0.5, 1.0, ns, pps, ws,
+                        torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(fixed, out)
 
 
 def test_without_the_flag_the_record_is_not_used():
-    """Default calls keep the usual item layout: a record forcing delta to its bound
-    changes no output bit, and neither the record nor the loop-time slots behind it
-    are touched."""
+    """Default calls pair items with the fixed delta: a record forcing delta to its
+    bound changes no output bit, and neither the record nor the loop-time slots
+    behind it are touched."""
     q_len, batch, seq_pages, n_items = 16, 2, 256, 16
     lens = [seq_pages * 16] * batch
     case = inputs.Case(batch=batch, q_len=q_len, seq_lens=lens, seed=1870)
@@ -155,3 +162,38 @@ def test_without_the_flag_the_record_is_not_used():
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     ref = attention_c64(*(t.cpu() for t in (q, k, v, bt, sl)), 16, HKV)
     assert_parity(outs[0], ref, label="flags 0")
+
+
+@pytest.mark.parametrize("qdt", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_default_pairs_use_the_fixed_delta(qdt):
+    """A default call (no flag) splits each pair at delta 0.03: the same bits as an
+    adaptive call whose record holds 0.03, and within the parity bar of the
+    float64 oracle. A record of 0 gives another split (other bits, same parity)."""
+    q_len, batch, seq_pages, n_items = 16, 2, 256, 16  # P = 32: d = round(0.96) = 1
+    lens = [seq_pages * 16] * batch
+    case = inputs.Case(batch=batch, q_len=q_len, seq_lens=lens, seed=1890)
+    q, k, v, bt, sl = inputs.make_inputs(case)
+    q, k, v = q.to(qdt), k.to(qdt), v.to(qdt)
+    ref = attention_c64(q, k, v, bt, sl, 16, HKV)
+    q, k, v, bt, sl = (t.cuda() for t in (q, k, v, bt, sl))
+    ns, pps = batch + n_items, -seq_pages
+    ws = torch.zeros(_lib.workspace_bytes(batch, q_len, HQ, HKV, HD, ns, pps), dtype=torch.uint8,
+                     device="cuda")
+    off = _tune_offset(batch, q_len, ns)
+
+    def call(flags, delta=None):
+        if delta is not None:
+            _seed(ws, off, MAGIC, delta)
+        out = torch.full_like(q, float("nan"))
+        _lib.launch_general(q, out, k, v, bt, sl, None, HD ** -0.5, 1.0, ns, pps, ws,
+                            torch.cuda.current_stream().cuda_stream, flags=flags)
+        torch.cuda.synchronize()
+        return out
+
+    default = call(0)
+    assert_parity(default, ref, label=f"{qdt} default pairs")
+    assert torch.equal(call(ADAPTIVE, 0.03), default)
+    at_zero = call(ADAPTIVE, 0.0)
+    assert_parity(at_zero, ref, label=f"{qdt} delta 0")
+    assert not torch.equal(at_zero, default)
+    assert torch.equal(call(0), default)
