@@ -143,8 +143,9 @@ size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv
   const size_t rows = (size_t)q_len * (num_query_heads / num_kv_heads);
   const size_t items = (size_t)sqa::plan_slots(batch, num_splits, pages_per_split) * num_kv_heads * rows;
   size_t bytes = items * ((size_t)head_dim + 2) * sizeof(float);
-  // Balanced plans: the merge table, then the paired items' delta record (16
-  // bytes) and one 8-byte loop-time record per workgroup (two per slot).
+  // Balanced plans: the merge table, then the adaptive paired items' delta
+  // record (16 bytes) and one 8-byte loop-time record per workgroup (two per
+  // slot).
   if (balanced)
     bytes += (size_t)batch * sizeof(sqa::SeqSplits) + 16 + (size_t)num_splits * 2 * 8;
   return bytes;

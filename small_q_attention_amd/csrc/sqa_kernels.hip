@@ -679,7 +679,7 @@ struct ItemRange {
   int n_valid;  // splits of this sequence that own pages
   int slot0;    // partial slot of split 0 of this sequence
   int g_end;    // balanced plan: where the piece ends along the item's pages
-  int paired;   // a paired item of the expected-page plan (its loop time is recorded)
+  int paired;   // a paired item of the expected-page plan (its loop time is timed)
 };
 
 // Fixed plan: sequence b owns slots b * num_splits + s.
@@ -1680,8 +1680,8 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   }
 
   // Paired items: the page loop's time (100 MHz counter) and pages, for the
-  // merge kernel's choice of the next call's item sizes (zero if the item has
-  // no piece).
+  // merge kernel's choice of the next call's item sizes under adaptive pairs
+  // (zero if the item has no piece).
   float loop_ticks = 0.f;
   int loop_pages = 0;
   const bool paired_call =
