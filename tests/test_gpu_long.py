@@ -2,7 +2,8 @@
 (16384 pages: the fixed plan's 128 splits of 128 pages), and ragged batches up to
 512K keys (32768 pages in one block-table row) where the balanced plan's items
 lie inside one sequence for hundreds of pages and pieces cross few, far-apart
-sequence starts. Each against the float32 torch checker (pinned to the C oracle
+sequence starts, and a uniform batch at q_len 16 whose items are paired. Each
+against the float32 torch checker (pinned to the C oracle
 by ``tests/test_checker_pinned.py``) on the device, a short sequence of the batch
 against the float64 C oracle, and the reference's default fixed plan (512-key
 chunks) against the automatic one.
@@ -30,6 +31,9 @@ CASES = [
     ("one_256k_q8", [262144], 8),
     ("ragged_200k_70k_5k_q16", [200000, 70000, 5000], 16),
     ("ragged_512k_1k_q4", [524288, 1000], 4),
+    # uniform and as promised: the 64-row kernel's paired items (items of 64
+    # pages, the even ones 2 pages longer) over 4096-page sequences
+    ("uniform_2x64k_q16_pairs", [65536, 65536], 16),
 ]
 
 
