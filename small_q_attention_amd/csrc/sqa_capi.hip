@@ -321,6 +321,35 @@ int run_attention(const sqa_attention_args& a) {
   pa.pair_items = !pair_ok                              ? sqa::kPairsOff
                   : (a.flags & SQA_FLAG_ADAPTIVE_PAIRS) ? sqa::kPairsAdaptive
                                                         : sqa::kPairsFixed;
+  // Items per head group (sqa_internal.h): e4m3 caches with token rows of 1 KiB
+  // (8 kv heads of 128 dims), read as two 512-byte halves by the two head groups
+  // of the one-wave kernel (up to 32 rows), under fp16 queries. The half whose
+  // address bit 9 is 0 streams more slowly: per-workgroup stamps at 16 x 32K
+  // keys, pools at 2 MiB boundaries, 165 against 146 us per workgroup; K's bit
+  // sets which half (V's adds or takes away about a third), so the K pool's bit
+  // 9 picks the slower group and whether V's agrees sets its extra items (6.5%
+  // of the items, best of 4 / 6.5 / 9%, or 2%). Under bf16 queries (more math
+  // per page) the same split ran 2.6% slower at q_len 8, so they keep one count.
+  pa.hg_items[0] = pa.hg_items[1] = 0;
+  pa.hg_spec_pps1 = 0;
+  const long long kv_page_bytes = kv_bytes * ps;
+  if (balanced && spec_pages > 0 && kv_fp8 && a.dtype == SQA_DTYPE_F16 && head_dim == 128 &&
+      num_kv_heads == 8 && rows <= 32 && kv_bytes * hs == 128 && kv_bytes * ts == 1024 &&
+      kv_page_bytes % 1024 == 0) {
+    const int n = num_splits - batch;
+    const bool k_high = ((uintptr_t)a.kv.k >> 9) & 1, v_high = ((uintptr_t)a.kv.v >> 9) & 1;
+    const int slow = k_high ? 1 : 0;
+    const int extra = (int)lround(n * (k_high == v_high ? 0.065 : 0.02));
+    const long long total = (long long)batch * spec_pages;
+    const int fewest = (int)ceil_div(total, sqa::kMaxSplitPages);
+    if (extra > 0 && n - extra >= (fewest > 1 ? fewest : 1)) {
+      pa.hg_items[slow] = n + extra;
+      pa.hg_items[1 - slow] = n - extra;
+      const int pps0 = sqa::packed_item_pages((int)total, pa.hg_items[0]);
+      pa.hg_spec_pps1 = sqa::packed_item_pages((int)total, pa.hg_items[1]);
+      pa.spec_pps = pps0;
+    }
+  }
   // Pieces that fit the register ring take it in one softmax step: fixed plans
   // of at most kRingPages pages per split, balanced plans whose expected items
   // are that short (pieces can only be shorter than their item).
@@ -355,6 +384,9 @@ int run_attention(const sqa_attention_args& a) {
     ma.num_splits = num_splits;
     ma.spec_pages = spec_pages;
     ma.spec_pps = pa.spec_pps;
+    ma.hg_items[0] = pa.hg_items[0];
+    ma.hg_items[1] = pa.hg_items[1];
+    ma.hg_spec_pps1 = pa.hg_spec_pps1;
     ma.out_scale = a.out_scale;
     ma.bf16 = pa.bf16;
     ma.tune = pa.pair_items == sqa::kPairsAdaptive ? pa.tune : nullptr;

@@ -90,6 +90,41 @@ constexpr float kPairDeltaFixed = 0.03f;  // even items' extra share with fixed 
 constexpr unsigned kTuneMagic = 0x51a7u << 16 | 1u;  // tune[0] when tune[1] holds a delta
 constexpr unsigned kTuneStamp = 0x51a7u << 16 | 2u;  // tune[2] after a call that ran paired
 constexpr float kPairDeltaMax = 0.1f;                // |delta| bound
+
+// Items per head group (hg_items[0] > 0; the balanced plan with an expected
+// page count, 8 kv heads in two head groups of four, one wave per head): the
+// two head groups cut the same pages into different numbers of items, N0 and
+// N1 with N0 + N1 = 2 (num_splits - batch), so the head group that streams its
+// half of the token rows more slowly gets the shorter items. Each head group
+// then has its own slots, table and item size: group g's slots are g's region
+// of the partials, Sg = Ng + batch slots of 4 kv heads each (region 1 after
+// region 0's S0: the regions fill the same num_splits x 8 heads), its (first
+// slot, count) table is at seq_splits + g * batch, its item size spec_pps
+// (group 0) or hg_spec_pps1. Workgroups 2i and 2i + 1 are item i of groups 0
+// and 1 up to the smaller count, the rest the larger group's remaining items.
+struct HeadGroupItems {
+  int group, item;   // this workgroup's head group and item
+  int slots;         // Sg
+  int slot_base;     // slots of the regions before this group's (0 or S0)
+  int spec_pps;      // this group's item size
+};
+__host__ __device__ inline HeadGroupItems head_group_items(const int (&n)[2], int batch,
+                                                           int spec_pps0, int spec_pps1,
+                                                           int block) {
+  const int nf = n[0] < n[1] ? n[0] : n[1];
+  HeadGroupItems h;
+  if (block < 2 * nf) {
+    h.group = block & 1;
+    h.item = block >> 1;
+  } else {
+    h.group = n[0] > n[1] ? 0 : 1;
+    h.item = nf + (block - 2 * nf);
+  }
+  h.slots = n[h.group] + batch;
+  h.slot_base = h.group ? n[0] + batch : 0;
+  h.spec_pps = h.group ? spec_pps1 : spec_pps0;
+  return h;
+}
 struct PartialArgs {
   const _Float16* q;          // [B, Q, Hq, head_dim]
   const _Float16* k;          // K of page 0, slot 0, kv head 0
@@ -121,6 +156,9 @@ struct PartialArgs {
   int seam_pages;             // balanced plan: pages a second piece costs a workgroup (0: no gaps)
   int pair_items;             // kPairsOff, kPairsAdaptive or kPairsFixed (see above)
   int ring_batch;             // every piece expected within the register ring (kRingPages)
+  int hg_items[2];            // items per head group (HeadGroupItems below); 0: both
+                              // num_splits - batch, the usual layout
+  int hg_spec_pps1;           // with hg_items: head group 1's item size (spec_pps: group 0's)
   float* tune;                // adaptive paired items: {magic, delta, stamp, -} then per
                               // workgroup {loop ticks, pages}
   float scale_log2;           // softmax scale * log2(e)
@@ -153,6 +191,8 @@ struct MergeArgs {
   int pages_per_split, num_splits;
   int spec_pages;   // balanced plan: expected pages of every sequence (0: none)
   int spec_pps;     // the balanced plan's item size when that holds
+  int hg_items[2];  // as PartialArgs::hg_items
+  int hg_spec_pps1; // as PartialArgs::hg_spec_pps1
   float out_scale;
   int bf16;
   float* tune;      // adaptive paired items: the delta record to update (null: none)

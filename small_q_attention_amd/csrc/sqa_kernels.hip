@@ -752,6 +752,22 @@ struct PackedBatch {
   int total;               // pages of the batch
 };
 
+// A workgroup's view of the balanced plan: its head group's slot count, merge
+// table and item size, and whether it writes that table (the first workgroup of
+// the call, or with items per head group the first of its group).
+struct PlanView {
+  int num_splits;
+  SeqSplits* table;
+  int spec_pps;
+  bool writer;
+};
+__device__ __forceinline__ PlanView plan_view(const PartialArgs& a) {
+  return PlanView{a.num_splits, a.seq_splits, a.spec_pps, blockIdx.x == 0};
+}
+__device__ __forceinline__ PlanView plan_view(const PartialArgs& a, const HeadGroupItems& h) {
+  return PlanView{h.slots, a.seq_splits + h.group * a.batch, h.spec_pps, h.item == 0};
+}
+
 // Kernel pages of a sequence of `len` tokens within a block-table row.
 __device__ __forceinline__ int pages_of(const PartialArgs& a, int len) {
   return min((len + kPageSize - 1) / kPageSize, a.max_pages);
@@ -759,8 +775,8 @@ __device__ __forceinline__ int pages_of(const PartialArgs& a, int len) {
 
 // Prefix sums of the page counts and the item size; with write_table, the
 // merge kernel's table.
-__device__ __forceinline__ void packed_plan(const PartialArgs& a, PackedBatch& pb,
-                                            bool write_table) {
+__device__ __forceinline__ void packed_plan(const PartialArgs& a, const PlanView& v,
+                                            PackedBatch& pb, bool write_table) {
   const int lane = threadIdx.x & 63;
   // Groups of 64 sequences past the batch hold no pages: their scans are skipped
   // (a uniform branch), and a group's sum is the last lane of its scan.
@@ -781,7 +797,7 @@ __device__ __forceinline__ void packed_plan(const PartialArgs& a, PackedBatch& p
   // compiler, which keeps the loop over pieces (and the page ids loaded in it)
   // uniform rather than wrapping each buffer load in a waterfall loop.
   pb.total = __builtin_amdgcn_readfirstlane(base);
-  const int target = a.num_splits - a.batch;
+  const int target = v.num_splits - a.batch;
   pb.P = packed_item_pages(pb.total, target);
   // Seams (ragged batches): seam_pages of nothing before every sequence start
   // that is not on an item boundary of the layout without them, so an item that
@@ -820,7 +836,7 @@ __device__ __forceinline__ void packed_plan(const PartialArgs& a, PackedBatch& p
       if (sq < a.batch) {
         const int i0 = pb.start[k] / pb.P;
         const int count = pages[k] > 0 ? (pb.start[k] + pages[k] - 1) / pb.P - i0 + 1 : 0;
-        a.seq_splits[sq] = SeqSplits{min(i0 + sq, a.num_splits - 1), count};
+        v.table[sq] = SeqSplits{min(i0 + sq, v.num_splits - 1), count};
       }
     }
   }
@@ -912,7 +928,8 @@ struct WaveRows {
 // workgroup's LDS). Returns whether the item ran as a paired item (every
 // workgroup of a call returns the same).
 template <int D, typename Piece>
-__device__ __forceinline__ bool for_each_piece(const PartialArgs& a, int item, Piece&& piece) {
+__device__ __forceinline__ bool for_each_piece(const PartialArgs& a, const PlanView& v, int item,
+                                               Piece&& piece) {
   const int lane = threadIdx.x & 63;
   const bool balanced = is_balanced(a.pages_per_split);
   int first_id[D];
@@ -942,14 +959,14 @@ __device__ __forceinline__ bool for_each_piece(const PartialArgs& a, int item, P
 #pragma unroll
       for (int k = 0; k < kSeqPerLane; ++k) pb.start[k] = min(64 * k + lane, a.batch) * P;
       pb.total = a.batch * P;
-      pb.P = a.spec_pps;
-      if (blockIdx.x == 0 && threadIdx.x < 64) {
+      pb.P = v.spec_pps;
+      if (v.writer && threadIdx.x < 64) {
 #pragma unroll
         for (int k = 0; k < kSeqPerLane; ++k) {
           const int sq = 64 * k + lane;
           if (sq < a.batch) {
             const int i0 = pb.start[k] / pb.P;
-            a.seq_splits[sq] = SeqSplits{i0 + sq, (pb.start[k] + P - 1) / pb.P - i0 + 1};
+            v.table[sq] = SeqSplits{i0 + sq, (pb.start[k] + P - 1) / pb.P - i0 + 1};
           }
         }
       }
@@ -982,7 +999,7 @@ __device__ __forceinline__ bool for_each_piece(const PartialArgs& a, int item, P
       for (int k = 0; k < kSeqPerLane; ++k)
         differs |= 64 * k + lane < a.batch && pages_of(a, pb.len[k]) != P;
       if (__any(differs)) {
-        packed_plan(a, pb, blockIdx.x == 0);  // rewrites the table
+        packed_plan(a, v, pb, v.writer);  // rewrites the table
         paired = false;
       } else {
         ids_loaded = true;
@@ -990,7 +1007,7 @@ __device__ __forceinline__ bool for_each_piece(const PartialArgs& a, int item, P
       if (paired) g = g0;
     } else {
       load_lengths(a, pb.len);
-      packed_plan(a, pb, blockIdx.x == 0);
+      packed_plan(a, v, pb, v.writer);
     }
     if (!paired) {
       g = item * pb.P;
@@ -1062,13 +1079,19 @@ __device__ __forceinline__ unsigned long long draft_bits(const PartialArgs& a, i
 template <int NB, int HD, typename E, typename Map>
 __device__ __forceinline__ void write_results(const PartialArgs& a, WaveState<NB, HD>& st,
                                               float* stage, const Map& map, bool direct,
-                                              bool mark_done, int b, size_t slot) {
+                                              bool mark_done, int b, size_t slot,
+                                              int slot_heads, int head0) {
   constexpr int MB = Dims<HD>::MB;
   constexpr int kStageRow = HD + 4;  // floats per staged row
   constexpr int CPR = HD / 4;        // 4-value chunks per row
   const int lane = piece_tid() & 63;
   const int g16 = lane >> 4, l16 = lane & 15;
-  auto item_of = [&](int nb, int r) { return (slot * a.hkv + map.head(nb, r)) * a.rows; };
+  // Partial slots of slot_heads kv heads from head0 on: all of them (hkv, 0), or
+  // with items per head group the group's four (4, 4 group; slot counts from
+  // the start of the group's region).
+  auto item_of = [&](int nb, int r) {
+    return (slot * slot_heads + map.head(nb, r) - head0) * a.rows;
+  };
   // Row sums over the four lane groups.
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) st.l[nb] = xor_sum(st.l[nb]);
@@ -1210,10 +1233,18 @@ void sqa_partial_kernel(PartialArgs a) {
   constexpr int KK = Dims<HD>::KK, MB = Dims<HD>::MB;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-  // blockIdx.x = item * head_groups + head_group.
+  // blockIdx.x = item * head_groups + head_group, or with items per head group
+  // (hg_items) as head_group_items() deals them.
   const int head_groups = (a.hkv + WW * HPW - 1) / (WW * HPW);
-  const int hgrp = blockIdx.x % head_groups;
-  const int item = blockIdx.x / head_groups;
+  const bool hg_split = a.hg_items[0] > 0;
+  const HeadGroupItems hgi =
+      head_group_items(a.hg_items, a.batch, a.spec_pps, a.hg_spec_pps1, blockIdx.x);
+  const int hgrp = hg_split ? hgi.group : (int)blockIdx.x % head_groups;
+  const int item = hg_split ? hgi.item : (int)blockIdx.x / head_groups;
+  const PlanView view = hg_split ? plan_view(a, hgi) : plan_view(a);
+  const int slot_heads = hg_split ? WW : a.hkv;  // partial slot layout (write_results)
+  const int head0 = hg_split ? hgrp * WW : 0;
+  const int slot_base = hg_split ? hgi.slot_base : 0;
   const int kvh = (hgrp * WW + wave) * HPW;  // the wave's first kv head
   // Waves past the last kv head (hkv not a multiple of WW * HPW) idle but stay
   // for the barrier.
@@ -1237,7 +1268,7 @@ void sqa_partial_kernel(PartialArgs a) {
   // Each piece of the work item (one, except where a balanced item spans the
   // end of a sequence): its page range of one sequence, with the ids of its
   // first D pages already requested.
-  for_each_piece<D>(a, item, [&](const ItemRange& it, const int (&first_id)[D]) {
+  for_each_piece<D>(a, view, item, [&](const ItemRange& it, const int (&first_id)[D]) {
   const int tid = piece_tid();
   const int lane = tid & 63;
   const int g16 = lane >> 4;
@@ -1538,7 +1569,7 @@ void sqa_partial_kernel(PartialArgs a) {
   }
   if (active)
     write_results<NB, HD, E>(a, st, sm_stage + wave * 16 * (HD + 4), map, direct,
-                             !single && !balanced, b, slot);
+                             !single && !balanced, b, slot + slot_base, slot_heads, head0);
   });
 }
 
@@ -1685,7 +1716,7 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   float loop_ticks = 0.f;
   int loop_pages = 0;
   const bool paired_call =
-      for_each_piece<D>(a, item, [&](const ItemRange& it, const int (&first_id)[D]) {
+      for_each_piece<D>(a, plan_view(a), item, [&](const ItemRange& it, const int (&first_id)[D]) {
   const int tid = piece_tid();
   const int lane = tid & 63;
   const int g16 = lane >> 4;
@@ -1814,7 +1845,7 @@ void sqa_partial_lds_kernel(PartialArgs a) {
   __syncthreads();
   if (active)
     write_results<NB, HD, E>(a, st, (float*)sm_ring + wave * 16 * (HD + 4), map, direct,
-                             !single && !balanced, b, slot);
+                             !single && !balanced, b, slot, a.hkv, 0);
   });
   // An adaptive paired call (the same answer in every workgroup) leaves a record
   // from every workgroup. Whenever adaptive pairing was asked for, workgroup 0
@@ -1947,17 +1978,27 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
   // table if the two differ.
   const bool balanced = is_balanced(a.pages_per_split);
   const bool expect = balanced && a.spec_pages > 0;
-  const size_t stride = (size_t)a.hkv * a.rows;  // items between consecutive splits of this row
-  const size_t row_item = (size_t)kvh * a.rows + r;
+  // With items per head group (hg_items) the row's head group has its own
+  // region of slots (four kv heads each), table, slot count and item size.
+  const bool hg_split = a.hg_items[0] > 0;
+  const int grp = kvh >> 2;
+  const int num_splits = hg_split ? a.hg_items[grp] + a.batch : a.num_splits;
+  const SeqSplits* seq_splits = a.seq_splits + (hg_split ? grp * a.batch : 0);
+  const int spec_pps = hg_split && grp ? a.hg_spec_pps1 : a.spec_pps;
+  // items between consecutive splits of this row, and the row's item in split 0
+  const size_t stride = (size_t)(hg_split ? 4 : a.hkv) * a.rows;
+  const size_t row_item =
+      hg_split ? ((size_t)(grp ? a.hg_items[0] + a.batch : 0) * 4 + (kvh & 3)) * a.rows + r
+               : (size_t)kvh * a.rows + r;
   int n_valid, slot0;
   SeqSplits table = {0, 0};
   if (expect) {
     const int start = b * a.spec_pages;
-    const int i0 = start / a.spec_pps;
-    n_valid = (start + a.spec_pages - 1) / a.spec_pps - i0 + 1;
+    const int i0 = start / spec_pps;
+    n_valid = (start + a.spec_pages - 1) / spec_pps - i0 + 1;
     slot0 = i0 + b;
   } else if (balanced) {
-    table = in_range(a.seq_splits[b], a.num_splits);
+    table = in_range(seq_splits[b], num_splits);
     n_valid = table.count;
     slot0 = table.first;
   } else {
@@ -2033,7 +2074,7 @@ __global__ __launch_bounds__(256) void sqa_merge_kernel(MergeArgs a) {
 #pragma unroll
     for (int i = 0; i < DPT; ++i) acc[i] = 0.f;
     load_round(s0, nv, g);
-    if (expect) table = in_range(a.seq_splits[b], a.num_splits);
+    if (expect) table = in_range(seq_splits[b], num_splits);
     const float first_l = l[0];  // split g (split 0 for group 0)
     add_round();
     for (int sb = g + U * SG; sb < nv; sb += U * SG) {
