@@ -2302,9 +2302,12 @@ hipError_t launch_merge(const MergeArgs& a, hipStream_t stream) {
   // device: the batch average, items / batch. It depends on the slot count
   // alone, so the plain balanced plan and the one with an expected page count
   // merge with the same variant (and give the same bits).
-  const int per_row = is_balanced(a.pages_per_split)
-                          ? (a.num_splits - a.batch + a.batch - 1) / a.batch
-                          : a.num_splits;
+  // With items per head group, the larger group's count (a row of the other
+  // group then loads a few more splits than it has, as splits past a row's
+  // last do).
+  const int items = a.hg_items[0] > 0 ? max(a.hg_items[0], a.hg_items[1]) : a.num_splits - a.batch;
+  const int per_row = is_balanced(a.pages_per_split) ? (items + a.batch - 1) / a.batch
+                                                     : a.num_splits;
   if (a.bf16)
     launch_merge_as<ElemBF16>(a, per_row, stream);
   else
