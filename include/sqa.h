@@ -116,8 +116,11 @@ int sqa_paged_mtp_attention(const void* query, const void* key_cache, const void
  * reference: it serves callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * The plan's split partials go to a device array of SQA_NOALLOC_SCRATCH_BYTES
- * that the library holds on every GPU it runs on until the process ends; its
- * device address is looked up once per device (hipGetSymbolAddress). Same
+ * in a code object of its own (no kernels), which HIP's deferred loading (its
+ * default) places on a GPU when the array's address is first looked up there
+ * (hipGetSymbolAddress, at this entry point's first call on the device): from
+ * then until the process ends that GPU holds it; a process that never calls
+ * this entry point holds none. Same
  * arguments, plans, kernels, results and status codes as
  * sqa_paged_mtp_attention, on the current device's array; a plan whose
  * sqa_workspace_bytes exceeds SQA_NOALLOC_SCRATCH_BYTES is rejected with

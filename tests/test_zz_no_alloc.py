@@ -173,3 +173,72 @@ def test_noalloc_under_graph_capture(order):
                        capture_output=True, text=True, timeout=110)
     assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
     assert "capture ok" in r.stdout
+
+
+# Run in a fresh process: device free memory (hipMemGetInfo) around the first call
+# of the workspace entry point, then around the first and second calls of the
+# no-allocation entry point. The scratch lives in a code object of its own, with
+# no kernels, which HIP loads (deferred loading, its default) when the scratch
+# address is first looked up: a process that never calls the no-allocation entry
+# point does not hold the scratch.
+_MEMORY_SCRIPT = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import torch
+from small_q_attention_amd import _lib, inputs
+
+def free():
+    torch.cuda.synchronize()
+    return torch.cuda.mem_get_info()[0]
+
+torch.zeros(1, device="cuda")
+case = inputs.uniform_case(2, 4, 2048, seed=48)
+q, k, v, bt, sl = (t.cuda() for t in inputs.make_inputs(case))
+lib = _lib.load(build_if_missing=False)
+ns, pps = _lib.plan_splits(0, 2, 4, 32, 8, 128, 2048, bt.shape[1], 0)
+nbytes = _lib.workspace_bytes(2, 4, 32, 8, 128, ns, pps)
+ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+want, got, again = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+stream = torch.cuda.current_stream().cuda_stream
+
+def noalloc(out):
+    rc = lib.sqa_paged_mtp_attention_noalloc(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr(), out.data_ptr(),
+        2, 4, 32, 8, 128, k.shape[0], 16, bt.shape[1], ns, pps, stream)
+    assert rc == 0, _lib.last_error(lib)
+
+f0 = free()
+_lib.launch(q, k, v, bt, sl, want, ws, ns, pps, stream)
+f1 = free()
+noalloc(got)
+f2 = free()
+noalloc(again)
+f3 = free()
+assert torch.equal(got, want) and torch.equal(again, want)
+print("held", f0 - f1, f1 - f2, f2 - f3, flush=True)
+"""
+
+
+def test_scratch_is_held_from_the_first_noalloc_call_on():
+    """A process holds the 64 MiB scratch only once it calls the no-allocation entry
+    point: the first workspace call takes well under it (the kernels' code object),
+    the first no-allocation call at least the scratch, the second nothing more."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    env = {k: v for k, v in os.environ.items() if k != "HIP_ENABLE_DEFERRED_LOADING"}
+    print("[noalloc] device memory held, fresh process", flush=True)
+    r = subprocess.run([sys.executable, "-c", _MEMORY_SCRIPT, str(root)], capture_output=True,
+                       text=True, timeout=110, env=env)
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
+    line = [s for s in r.stdout.splitlines() if s.startswith("held ")][-1]
+    workspace_call, first_noalloc, second_noalloc = (int(x) for x in line.split()[1:])
+    print(f"[noalloc] held by the first workspace call {workspace_call >> 20} MiB, first "
+          f"no-allocation call {first_noalloc >> 20} MiB, second {second_noalloc >> 20} MiB",
+          flush=True)
+    assert workspace_call < 32 << 20
+    assert first_noalloc >= SCRATCH_BYTES
+    assert abs(second_noalloc) < 8 << 20
