@@ -145,7 +145,10 @@ size_t sqa_workspace_bytes(int batch, int q_len, int num_query_heads, int num_kv
   size_t bytes = items * ((size_t)head_dim + 2) * sizeof(float);
   // Balanced plans: the merge table, then the adaptive paired items' delta
   // record (16 bytes) and one 8-byte loop-time record per workgroup (two per
-  // slot).
+  // slot). With items per head group the second group's table takes the first
+  // batch x 8 bytes of that record region (num_splits > batch keeps it inside):
+  // those calls (e4m3, at most 32 rows) never pair, and a later paired call
+  // reads no magic or stamp there.
   if (balanced)
     bytes += (size_t)batch * sizeof(sqa::SeqSplits) + 16 + (size_t)num_splits * 2 * 8;
   return bytes;
