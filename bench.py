@@ -12,7 +12,8 @@ mean duration from HIP events the library records around it on the launch
 stream; ``cpu_baseline`` times the loop-faithful CPU oracle on a bounded
 sample of the same workload. ``per_q_len`` repeats the timing at q_len 2, 4
 and 16 on the same KV pool. ``metric_grid`` times back-to-back whole calls at
-every point of BASELINE's metric (q_len 2/4/8 x KV 8K/32K x batch 1/4/16);
+every point of BASELINE's metric (q_len 2/4/8 x KV 8K/32K x batch 1/4/16), and
+each point's p50 per synchronised Python call (the reference runner's method);
 ``other_configs`` the other single-GPU configs (cfg1, cfg2, cfg5), with the
 committed rocprof figures beside this run's under ``rocprof_*`` keys. ``roofline.read_probe`` is the practical read
 ceiling: the streaming-read probe (``read_probe.hip``) over ~2 GiB of the same
@@ -198,6 +199,30 @@ def time_calls(torch, lib, sets, plan, steps, warmup, kernel_events=True):
     return total_ms / steps, statistics.mean(part), statistics.mean(merge), outs[0]
 
 
+def p50_call_us(torch, sets, max_seq_len, warmup=5, repeats=15):
+    """The reference runner's per-call latency (``run_gpu_matrix.py:63-81``): HIP events
+    around each call of the Python entry, synchronised after each, warmup 5, repeats
+    15, p50 in us. The call is ``paged_mtp_attention`` (the native entry: automatic
+    plan, known ``max_seq_len``), so it includes the host-side checks, the output
+    allocation and both launches, with the GPU idle before each call; it cycles
+    through the same pools as the back-to-back timing."""
+    from small_q_attention_amd import cuda as sqa
+
+    n = len(sets)
+    for i in range(warmup):
+        sqa.paged_mtp_attention(*sets[i % n], 16, max_seq_len)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    samples = []
+    for i in range(repeats):
+        start.record()
+        sqa.paged_mtp_attention(*sets[i % n], 16, max_seq_len)
+        end.record()
+        end.synchronize()
+        samples.append(start.elapsed_time(end) * 1e3)
+    return statistics.median(samples)
+
+
 GRID_Q_LENS = (2, 4, 8)
 GRID_KV_LENS = (8192, 32768)
 GRID_BATCHES = (1, 4, 16)
@@ -207,7 +232,9 @@ def metric_grid(torch, lib, inputs, steps, warmup):
     """BASELINE's metric over its whole grid: q_len 2/4/8 x KV 8K/32K x batch 1/4/16
     (Hq/Hkv 32/8, d 128, page 16, fp16, random page tables over a 2x pool), each
     point the mean of back-to-back whole calls (partial + merge) through the C ABI
-    with the automatic plan for a known max_seq_len; KV sets under
+    with the automatic plan for a known max_seq_len (``us_per_call``), and the p50 of
+    single synchronised calls through the Python entry, as the reference runner
+    times them (``p50_call_us``, :func:`p50_call_us`); KV sets under
     ``ROTATE_BELOW_BYTES`` rotate over several pools (:func:`input_sets`). The
     pools of one (KV, batch) serve all three q_len (Q drawn per q_len)."""
     grid = {}
@@ -240,7 +267,8 @@ def metric_grid(torch, lib, inputs, steps, warmup):
                     "us_per_call": round(ms * 1e3, 2), "kv_GBps": round(gbps, 1),
                     "pct_peak": round(100.0 * gbps / PEAK_HBM_GBPS, 2), "kv_bytes": kvb,
                     "pools": len(sets), "steps": n_steps, "num_splits": plan[0],
-                    "pages_per_split": plan[1]}
+                    "pages_per_split": plan[1],
+                    "p50_call_us": round(p50_call_us(torch, qsets, kv), 2)}
                 del qsets
             del sets
             torch.cuda.empty_cache()
