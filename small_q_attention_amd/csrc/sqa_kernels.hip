@@ -644,23 +644,31 @@ __device__ __forceinline__ void pair_finish(WaveState<NB, 128>& st, f4 (&s0)[NB]
     pp[nb] = u4{a0[0], a0[1], a1[0], a1[1]};
   }
 
-  // Dim block mb takes half mb%2 of widened dword mb/2 of the lane's four token
-  // rows of each page (dword j of a token row is e4m3 dword j/2, half j%2).
+  // Dim block mb = 2 j + h takes byte 2 (j % 2) + h of the lane's e4m3 dword
+  // j / 2 from each of its four token rows of each page. The
+  // bytes of token rows 2i and 2i + 1 are interleaved first (one v_perm_b32:
+  // {t0 b, t1 b, t0 b+1, t1 b+1}), so each fp8 -> fp16 conversion of a 16-bit
+  // word yields the MFMA operand dword itself (tokens 2i, 2i + 1 at one dim):
+  // 8 conversions and 4 permutes per j instead of 8 conversions and 8 permutes
+  // (widen each token row, then pair the rows' halves). Same values, same bits.
+  const unsigned sel = 0x05010400u;  // bytes {t0.b0, t1.b0, t0.b1, t1.b1}; + 0x02020202: b2, b3
 #pragma unroll
   for (int j = 0; j < MB / 2; ++j) {
-    unsigned w0[4], w1[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      w0[e] = E::widen_fp8x4(r0.v[e][j >> 1])[j & 1];
-      w1[e] = E::widen_fp8x4(r1.v[e][j >> 1])[j & 1];
-    }
+    const unsigned sj = (j & 1) ? sel + 0x02020202u : sel;
+    const int d = j >> 1;
+    const unsigned x[4] = {__builtin_amdgcn_perm(r0.v[1][d], r0.v[0][d], sj),
+                           __builtin_amdgcn_perm(r0.v[3][d], r0.v[2][d], sj),
+                           __builtin_amdgcn_perm(r1.v[1][d], r1.v[0][d], sj),
+                           __builtin_amdgcn_perm(r1.v[3][d], r1.v[2][d], sj)};
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int mb = 2 * j + h;
-      const u4 av = h == 0 ? u4{pack_lo(w0[0], w0[1]), pack_lo(w0[2], w0[3]),
-                                pack_lo(w1[0], w1[1]), pack_lo(w1[2], w1[3])}
-                           : u4{pack_hi(w0[0], w0[1]), pack_hi(w0[2], w0[3]),
-                                pack_hi(w1[0], w1[1]), pack_hi(w1[2], w1[3])};
+      u4 av;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        av[i] = __builtin_bit_cast(
+            unsigned, h == 0 ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x[i], 1.f, false)
+                             : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x[i], 1.f, true));
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
         st.acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
