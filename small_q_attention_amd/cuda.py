@@ -2,8 +2,10 @@
 
 Mirrors ``/root/reference/src/small_q_attention/cuda.py`` (same names,
 parameter order, defaults and exception classes) over one gfx950 library,
-``libsqa.so``. Eager calls go straight to the library; under ``torch.compile`` /
-``torch.export`` the ``sqa::paged_mtp_attention`` torch custom op is used.
+``libsqa.so``. Eager calls go straight to the library; under ``torch.compile``
+(``fullgraph=True`` included) and ``torch.export`` the checks trace as guards, the
+split plan becomes a constant of the graph and the graph calls the
+``sqa::paged_mtp_attention`` torch custom op (:func:`_traced_op`).
 All six ``forward_vN`` run the same HIP kernels (split-KV partial kernel with
 GQA and draft-row reuse, plus the log-sum-exp merge kernel); the version
 number only selects which of the reference's argument checks apply.
@@ -44,6 +46,8 @@ MAX_ROWS = 64
 
 
 def _load(verbose: bool = False):
+    if _tracing():  # the traced call loads it through the plan (see _traced_op)
+        return None
     return _lib.load(verbose=bool(verbose))
 
 
@@ -82,6 +86,8 @@ _MODULE = None
 
 def _module(verbose):
     global _MODULE
+    if _tracing():  # no module state is touched while torch.compile traces
+        return _Module(None)
     if _MODULE is None or verbose:
         _MODULE = _Module(_load(verbose))
     return _MODULE
@@ -119,7 +125,8 @@ def _check_python_contract(tag, query, key_cache, value_cache, block_tables, seq
     bfloat16 and the other head dims of this build."""
     import torch
 
-    if not _gpu_present(torch):
+    # (While torch.compile traces, the inputs are device tensors already.)
+    if not _tracing() and not _gpu_present(torch):
         raise RuntimeError(f"a ROCm GPU is required for the {tag} kernel")
     tensors = (query, key_cache, value_cache, block_tables, seq_lens)
     for t in tensors:
@@ -196,6 +203,9 @@ def _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
     whole block-table row (no sync).
     """
     _check_launcher_contract(query, key_cache, value_cache, block_tables, seq_lens, page_size)
+    if _tracing():
+        return _traced_op(query, key_cache, value_cache, block_tables, seq_lens, chunk_keys,
+                          max_seq_len)
     if max_seq_len == -1:
         max_seq_len = int(seq_lens.max().item())
         if max_seq_len <= 0:
@@ -207,12 +217,32 @@ def _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
     kernel_pages = block_tables.shape[1] * (key_cache.shape[1] // PAGE_SIZE)
     num_splits, pps = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv,
                                        query.shape[-1], int(max_seq_len), kernel_pages, ck)
-    if _tracing():
-        # Under torch.compile / export the registered custom op is the traceable unit.
-        return _lib.custom_op()(query, key_cache, value_cache, block_tables, seq_lens,
-                                num_splits, pps)
-    # Eager: the same allocation and launch without the dispatcher round trip.
+    # Eager: the custom op's allocation and launch without the dispatcher round trip.
     return _lib.run(query, key_cache, value_cache, block_tables, seq_lens, num_splits, pps)
+
+
+def _traced_op(query, key_cache, value_cache, block_tables, seq_lens,
+               chunk_keys: Optional[int], max_seq_len: int):
+    """A call that torch.compile (also with ``fullgraph=True``) or torch.export is
+    tracing, after the same checks, which trace as guards on dtypes and shapes: the
+    split plan is computed while tracing (``_op.traced_plan``, a constant of the
+    graph) and the graph calls the ``sqa::paged_mtp_attention`` custom op. A measured
+    ``max_seq_len`` (-1: ``seq_lens.max().item()``, a host sync) plans over the whole
+    block-table row instead, so the graph never synchronises; its splits differ from
+    the measured plan's only past the sequences' ends (empty), which changes the
+    merge's summation order, not which keys count."""
+    import torch
+
+    from . import _op
+
+    batch, q_len, hq, dim = query.shape
+    num_splits, pps = _op.traced_plan(
+        query.device.index or 0, int(batch), int(q_len), int(hq), int(key_cache.shape[2]),
+        int(dim), max(int(max_seq_len), 0),
+        int(block_tables.shape[1]) * (int(key_cache.shape[1]) // PAGE_SIZE),
+        0 if chunk_keys is None else int(chunk_keys))
+    return torch.ops.sqa.paged_mtp_attention(query, key_cache, value_cache, block_tables,
+                                             seq_lens, num_splits, pps)
 
 
 def _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, chunk_keys,
@@ -221,6 +251,8 @@ def _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, chun
     shapes, eager, library loaded) checked in one pass, then planned and launched;
     ``None`` when anything differs, and the full checks then run (and raise as the
     reference does). Accepts exactly what those checks accept."""
+    if _tracing():
+        return None
     torch = _TORCH
     if torch is None or _GPU_SEEN_BY is not torch.cuda.is_available or _lib._LIB is None:
         return None
@@ -256,8 +288,6 @@ def _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, chun
     if (gqa4 and group != 4) or q_len * group > MAX_ROWS:
         return None
     if chunk_keys is not None and chunk_keys <= 0:
-        return None
-    if _tracing():
         return None
     if max_seq_len == -1:
         max_seq_len = int(seq_lens.max().item())

@@ -1,0 +1,105 @@
+"""The op boundary under ``torch.compile`` with ``fullgraph=True`` (no graph break
+allowed) and under ``torch.export``: the checks trace as guards, the split plan is
+computed while tracing and the graph calls the ``sqa::paged_mtp_attention`` custom
+op, whose output must equal the eager call's bit for bit wherever the plan is the
+same (a known ``max_seq_len``, or the whole block-table row), and pass the parity
+bar where the eager call measures ``max_seq_len`` with a host sync (the traced call
+plans over the row instead). Backends ``eager`` and ``aot_eager`` (no code
+generation: the graph is the op between torch's own tensor ops).
+"""
+
+import sys
+
+import pytest
+import torch
+
+from small_q_attention_amd import cuda as sqa, inputs
+from tests._helpers import torch_fp32_reference, assert_parity
+
+pytestmark = pytest.mark.gpu
+
+CASE = inputs.Case(batch=3, q_len=8, seq_lens=[900, 40, 2100], seed=19)
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    sys.__stderr__.write(f"\n[gpu-test] {request.node.nodeid}\n")
+    sys.__stderr__.flush()
+    torch._dynamo.reset()
+    yield
+    torch._dynamo.reset()
+
+
+def _tensors(seed=19):
+    c = inputs.Case(batch=CASE.batch, q_len=CASE.q_len, seq_lens=CASE.seq_lens, seed=seed)
+    return tuple(t.cuda() for t in inputs.make_inputs(c))
+
+
+# (name, call): each call's eager plan is the one its traced call computes, except
+# forward_v2, whose eager call measures max_seq_len.
+CALLS = [
+    ("native", lambda q, k, v, bt, sl: sqa.paged_mtp_attention(q, k, v, bt, sl, 16, 2100)),
+    ("native_row", lambda q, k, v, bt, sl: sqa.paged_mtp_attention(q, k, v, bt, sl, 16)),
+    ("v0", lambda q, k, v, bt, sl: sqa.forward_v0(q, k, v, bt, sl, 16)),
+    ("v1", lambda q, k, v, bt, sl: sqa.forward_v1(q, k, v, bt, sl, 16)),
+    ("v3", lambda q, k, v, bt, sl: sqa.forward_v3(q, k, v, bt, sl, 16, 512, 2100)),
+    ("v4_auto", lambda q, k, v, bt, sl: sqa.forward_v4(q, k, v, bt, sl, 16, None, 2100)),
+    ("v5", lambda q, k, v, bt, sl: sqa.forward_v5(q, k, v, bt, sl, 16, 512, 2, 2100)),
+]
+
+
+@pytest.mark.parametrize("backend", ["eager", "aot_eager"])
+@pytest.mark.parametrize("name,call", CALLS, ids=[c[0] for c in CALLS])
+def test_compile_fullgraph_equals_eager(name, call, backend):
+    t = _tensors()
+    eager = call(*t)
+    compiled = torch.compile(call, backend=backend, fullgraph=True)
+    got = compiled(*t)
+    torch.cuda.synchronize()
+    assert torch.equal(got, eager), name
+    # Other inputs of the same shapes reuse the graph and follow their own data.
+    t2 = _tensors(seed=23)
+    got2 = compiled(*t2)
+    torch.cuda.synchronize()
+    assert torch.equal(got2, call(*t2)), name
+
+
+def test_compile_fullgraph_measured_max_seq_len_plans_over_the_row():
+    """forward_v2 measures max_seq_len eagerly (a host sync); traced, it plans over
+    the block-table row: same keys, the merge's order differs, within the bar."""
+    t = _tensors()
+    call = lambda q, k, v, bt, sl: sqa.forward_v2(q, k, v, bt, sl, 16, 512)  # noqa: E731
+    eager = call(*t)
+    got = torch.compile(call, backend="aot_eager", fullgraph=True)(*t)
+    torch.cuda.synchronize()
+    ref = torch_fp32_reference(*t, 16, 8)
+    assert_parity(got, ref, label="traced v2")
+    assert (got.float() - eager.float()).abs().max().item() <= 2e-3
+
+
+def test_compile_with_torch_ops_around_the_call():
+    """The op inside a larger compiled function (a scaled query in, a reduction out)."""
+    t = _tensors()
+
+    def step(q, k, v, bt, sl):
+        out = sqa.paged_mtp_attention(q * 0.5, k, v, bt, sl, 16, 2100)
+        return out.float().square().sum(dim=-1)
+
+    got = torch.compile(step, backend="aot_eager", fullgraph=True)(*t)
+    torch.cuda.synchronize()
+    assert torch.equal(got, step(*t))
+
+
+def test_export_holds_the_custom_op():
+    t = _tensors()
+
+    class Attention(torch.nn.Module):
+        def forward(self, q, k, v, bt, sl):
+            return sqa.paged_mtp_attention(q, k, v, bt, sl, 16, 2100)
+
+    ep = torch.export.export(Attention(), t)
+    targets = [str(n.target) for n in ep.graph.nodes if n.op == "call_function"]
+    assert any("sqa.paged_mtp_attention" in x for x in targets), targets
+    got = ep.module()(*t)
+    torch.cuda.synchronize()
+    assert torch.equal(got, sqa.paged_mtp_attention(*t, 16, 2100))
