@@ -3,13 +3,15 @@
 Allocates the output and the split-KV workspace with torch's caching allocator
 and launches on the current stream of the query's device. The fake (meta)
 implementation only shapes the output, so the op traces under
-``torch.compile`` / ``torch.export``; :func:`traced_plan` gives a traced call its split
-plan.
+``torch.compile`` / ``torch.export``; traced calls run
+:func:`paged_mtp_attention_planned`, which makes the split plan at run time.
 """
 
 import torch
 
 from . import _lib
+
+_KERNEL_PAGE = 16  # tokens per kernel page: the plan counts these (a cache page is 1-16 of them)
 
 
 @torch.library.custom_op("sqa::paged_mtp_attention", mutates_args=())
@@ -21,16 +23,27 @@ def paged_mtp_attention(query: torch.Tensor, key_cache: torch.Tensor,
                     pages_per_split)
 
 
-@torch.compiler.assume_constant_result
-def traced_plan(device_index: int, batch: int, q_len: int, num_query_heads: int,
-                num_kv_heads: int, head_dim: int, max_seq_len: int, max_pages: int,
-                chunk_keys: int):
-    """``(num_splits, pages_per_split)`` of ``_lib.plan_splits`` for a call being traced:
-    run while tracing (it loads the library and reads the device's CU count through
-    the C ABI, which Dynamo does not trace), its result a constant of the graph; the
-    plan is a pure function of these integers and the device."""
-    return _lib.plan_splits(device_index, batch, q_len, num_query_heads, num_kv_heads, head_dim,
-                            max_seq_len, max_pages, chunk_keys)
+@torch.library.custom_op("sqa::paged_mtp_attention_planned", mutates_args=())
+def paged_mtp_attention_planned(query: torch.Tensor, key_cache: torch.Tensor,
+                                value_cache: torch.Tensor, block_tables: torch.Tensor,
+                                seq_lens: torch.Tensor, max_seq_len: int,
+                                chunk_keys: int) -> torch.Tensor:
+    """:func:`paged_mtp_attention` with its split plan made at run time from the
+    tensors' shapes (``_lib.plan_splits``: ``max_seq_len`` 0 plans over the whole
+    block-table row, ``chunk_keys`` 0 is the automatic plan). What a traced call
+    (torch.compile, torch.export) runs: the graph holds no plan, so shapes it
+    leaves dynamic (the batch size of a serving loop) need no recompilation."""
+    batch, q_len, hq, dim = query.shape
+    num_splits, pps = _lib.plan_splits(
+        query.device.index or 0, batch, q_len, hq, key_cache.shape[2], dim, max_seq_len,
+        block_tables.shape[1] * (key_cache.shape[1] // _KERNEL_PAGE), chunk_keys)
+    return _lib.run(query, key_cache, value_cache, block_tables, seq_lens, num_splits, pps)
+
+
+@paged_mtp_attention_planned.register_fake
+def _paged_mtp_attention_planned_fake(query, key_cache, value_cache, block_tables, seq_lens,
+                                      max_seq_len, chunk_keys):
+    return torch.empty_like(query)
 
 
 @paged_mtp_attention.register_fake

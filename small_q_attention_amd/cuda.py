@@ -3,9 +3,9 @@
 Mirrors ``/root/reference/src/small_q_attention/cuda.py`` (same names,
 parameter order, defaults and exception classes) over one gfx950 library,
 ``libsqa.so``. Eager calls go straight to the library; under ``torch.compile``
-(``fullgraph=True`` included) and ``torch.export`` the checks trace as guards, the
-split plan becomes a constant of the graph and the graph calls the
-``sqa::paged_mtp_attention`` torch custom op (:func:`_traced_op`).
+(``fullgraph=True`` included) and ``torch.export`` the checks trace as guards and
+the graph calls the ``sqa::paged_mtp_attention_planned`` torch custom op, which
+plans the splits at run time (:func:`_traced_op`).
 All six ``forward_vN`` run the same HIP kernels (split-KV partial kernel with
 GQA and draft-row reuse, plus the log-sum-exp merge kernel); the version
 number only selects which of the reference's argument checks apply.
@@ -225,24 +225,20 @@ def _traced_op(query, key_cache, value_cache, block_tables, seq_lens,
                chunk_keys: Optional[int], max_seq_len: int):
     """A call that torch.compile (also with ``fullgraph=True``) or torch.export is
     tracing, after the same checks, which trace as guards on dtypes and shapes: the
-    split plan is computed while tracing (``_op.traced_plan``, a constant of the
-    graph) and the graph calls the ``sqa::paged_mtp_attention`` custom op. A measured
-    ``max_seq_len`` (-1: ``seq_lens.max().item()``, a host sync) plans over the whole
-    block-table row instead, so the graph never synchronises; its splits differ from
-    the measured plan's only past the sequences' ends (empty), which changes the
-    merge's summation order, not which keys count."""
+    graph calls the ``sqa::paged_mtp_attention_planned`` custom op, which makes the
+    split plan at run time from the tensors' shapes, so a dynamic batch size needs
+    no recompilation. A measured ``max_seq_len`` (-1: ``seq_lens.max().item()``, a
+    host sync) plans over the whole block-table row instead, so the graph never
+    synchronises; its splits differ from the measured plan's only past the
+    sequences' ends (empty), which changes the merge's summation order, not which
+    keys count."""
     import torch
 
-    from . import _op
+    from . import _op  # noqa: F401  (registers the ops)
 
-    batch, q_len, hq, dim = query.shape
-    num_splits, pps = _op.traced_plan(
-        query.device.index or 0, int(batch), int(q_len), int(hq), int(key_cache.shape[2]),
-        int(dim), max(int(max_seq_len), 0),
-        int(block_tables.shape[1]) * (int(key_cache.shape[1]) // PAGE_SIZE),
+    return torch.ops.sqa.paged_mtp_attention_planned(
+        query, key_cache, value_cache, block_tables, seq_lens, max(int(max_seq_len), 0),
         0 if chunk_keys is None else int(chunk_keys))
-    return torch.ops.sqa.paged_mtp_attention(query, key_cache, value_cache, block_tables,
-                                             seq_lens, num_splits, pps)
 
 
 def _fast(query, key_cache, value_cache, block_tables, seq_lens, page_size, chunk_keys,

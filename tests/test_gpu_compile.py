@@ -1,11 +1,12 @@
 """The op boundary under ``torch.compile`` with ``fullgraph=True`` (no graph break
-allowed) and under ``torch.export``: the checks trace as guards, the split plan is
-computed while tracing and the graph calls the ``sqa::paged_mtp_attention`` custom
-op, whose output must equal the eager call's bit for bit wherever the plan is the
+allowed) and under ``torch.export``: the checks trace as guards and the graph calls
+the ``sqa::paged_mtp_attention_planned`` custom op, which plans the splits at run
+time; its output must equal the eager call's bit for bit wherever the plan is the
 same (a known ``max_seq_len``, or the whole block-table row), and pass the parity
 bar where the eager call measures ``max_seq_len`` with a host sync (the traced call
-plans over the row instead). Backends ``eager`` and ``aot_eager`` (no code
-generation: the graph is the op between torch's own tensor ops).
+plans over the row instead). With ``dynamic=True`` one graph serves every batch
+size. Backends ``eager`` and ``aot_eager`` (no code generation: the graph is the op
+between torch's own tensor ops).
 """
 
 import sys
@@ -30,8 +31,9 @@ def _announce(request):
     torch._dynamo.reset()
 
 
-def _tensors(seed=19):
-    c = inputs.Case(batch=CASE.batch, q_len=CASE.q_len, seq_lens=CASE.seq_lens, seed=seed)
+def _tensors(seed=19, seq_lens=None):
+    lens = CASE.seq_lens if seq_lens is None else seq_lens
+    c = inputs.Case(batch=len(lens), q_len=CASE.q_len, seq_lens=lens, seed=seed)
     return tuple(t.cuda() for t in inputs.make_inputs(c))
 
 
@@ -75,6 +77,23 @@ def test_compile_fullgraph_measured_max_seq_len_plans_over_the_row():
     ref = torch_fp32_reference(*t, 16, 8)
     assert_parity(got, ref, label="traced v2")
     assert (got.float() - eager.float()).abs().max().item() <= 2e-3
+
+
+def test_compile_dynamic_batch_with_one_graph():
+    """dynamic=True: batches of 2, 3 and 5 sequences (other lengths, block-table
+    widths and pools) through one compiled frame, each equal to its eager call."""
+    from torch._dynamo.testing import CompileCounter
+
+    counter = CompileCounter()
+    call = lambda q, k, v, bt, sl: sqa.paged_mtp_attention(q, k, v, bt, sl, 16, 3000)  # noqa: E731
+    compiled = torch.compile(call, backend=counter, fullgraph=True, dynamic=True)
+    for seed, lens in ((31, [3000, 700]), (32, [1200, 16, 2999]),
+                       (33, [50, 3000, 800, 2048, 9])):
+        t = _tensors(seed, lens)
+        got = compiled(*t)
+        torch.cuda.synchronize()
+        assert torch.equal(got, call(*t)), lens
+    assert counter.frame_count == 1, counter.frame_count
 
 
 def test_compile_with_torch_ops_around_the_call():
