@@ -25,7 +25,10 @@ The caller's workspace buffer holds the split-KV partials, so a run allocates
 only its output (none when ``out`` is given) and is graph-capturable after
 ``plan()``. Arguments outside the contract raise ``ValueError`` (positional
 encodings, soft caps, sliding windows, sinks, custom prefill masks); behaviour
-is pinned against this build's oracle, not against FlashInfer itself.
+is pinned against this build's oracle, not against FlashInfer itself. Traced by
+``torch.compile`` (also ``fullgraph=True``) or ``torch.export``, a call runs the
+``sqa::paged_attention_planned`` custom op, which plans the splits and takes its
+workspace from torch's allocator at run time.
 """
 
 from __future__ import annotations
@@ -33,6 +36,7 @@ from __future__ import annotations
 from typing import Optional
 
 from . import _lib
+from .cuda import _tracing
 from .masks import as_words
 
 PAGE_SIZE = 16  # tokens per kernel page; cache pages hold 16 << k of them
@@ -128,12 +132,26 @@ def _run(query, k, v, block_tables, seq_lens, max_seq_len: int, q_len: int, scal
     if words is not None:
         _on_device(words, device, "mask")
     q4 = query.view(batch, q_len, hq, d)
-    if out is None:
-        out = torch.empty_like(query)
-    else:
+    if out is not None:
         _on_device(out, device, "out")
         if out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous():
             raise ValueError("out must be a contiguous tensor shaped and typed like query")
+    if _tracing():
+        # torch.compile / torch.export: the checks above trace as guards; the graph
+        # calls a custom op that plans the splits and takes its workspace from torch's
+        # allocator at run time (the caller's buffer is not used).
+        from . import _op  # noqa: F401  (registers the ops)
+
+        res = torch.ops.sqa.paged_attention_planned(q4, k, v, block_tables, seq_lens, words,
+                                                     float(scale), float(out_scale),
+                                                     max(int(max_seq_len), 0))
+        res = res.view(query.shape)
+        if out is None:
+            return res
+        out.copy_(res)
+        return out
+    if out is None:
+        out = torch.empty_like(query)
     if plan is None:
         plan = _lib.plan_splits(query.device.index or 0, batch, q_len, hq, hkv, d,
                                 int(max_seq_len), block_tables.shape[1] * (k.shape[1] // PAGE_SIZE),

@@ -122,3 +122,81 @@ def test_export_holds_the_custom_op():
     got = ep.module()(*t)
     torch.cuda.synchronize()
     assert torch.equal(got, sqa.paged_mtp_attention(*t, 16, 2100))
+
+
+def _cache(k, v, layout):
+    """Interleaved ``[P, 2, 16, Hkv, D]`` (NHD) or ``[P, 2, Hkv, 16, D]`` (HND) from
+    ``[P, 16, Hkv, D]`` K and V (e4m3 stacked through their bytes)."""
+    f8 = torch.float8_e4m3fn
+    if layout == "HND":
+        k, v = k.transpose(1, 2), v.transpose(1, 2)
+    if k.dtype == f8:
+        return torch.stack([k.view(torch.uint8), v.view(torch.uint8)], 1).contiguous().view(f8)
+    return torch.stack([k, v], 1).contiguous()
+
+
+@pytest.mark.parametrize("layout,kv_dtype,qdt,tree,with_out", [
+    ("NHD", "fp16", torch.float16, False, False),
+    ("HND", "e4m3", torch.float16, True, False),
+    ("NHD", "bf16", torch.bfloat16, False, True),
+], ids=["nhd_fp16", "hnd_e4m3_tree", "nhd_bf16_out"])
+def test_compile_fullgraph_xqa_decode(layout, kv_dtype, qdt, tree, with_out):
+    """The FlashInfer-shaped call traced into ``sqa::paged_attention_planned``: equal
+    to the eager call (the workspace's contents never matter)."""
+    from small_q_attention_amd import decode_api as fi
+    from small_q_attention_amd.masks import pack_draft_mask
+
+    q, k, v, bt, sl = _tensors()
+    q = q.to(qdt)
+    if kv_dtype == "e4m3":
+        k, v = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
+    elif kv_dtype == "bf16":
+        k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+    kv = _cache(k, v, layout)
+    b, q_len = q.shape[0], q.shape[1]
+    mask = None
+    if tree:
+        g = torch.Generator().manual_seed(5)
+        vis = torch.rand(b, q_len, q_len, generator=g) < 0.5
+        vis[:, torch.arange(q_len), torch.arange(q_len)] = True
+        mask = pack_draft_mask(vis).cuda()
+    qf = q.reshape(b * q_len, 32, 128)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+
+    def decode(qf, kv, bt, sl, out):
+        return fi.xqa_batch_decode_with_kv_cache(qf, kv, ws, bt, sl, 2100, 128 ** -0.5, 0.75,
+                                                 kv_layout=layout, q_len_per_req=q_len,
+                                                 mask=mask, out=out)
+
+    out_e = torch.empty_like(qf) if with_out else None
+    eager = decode(qf, kv, bt, sl, out_e)
+    out_c = torch.full_like(qf, float("nan")) if with_out else None
+    got = torch.compile(decode, backend="aot_eager", fullgraph=True)(qf, kv, bt, sl, out_c)
+    torch.cuda.synchronize()
+    assert torch.equal(got, eager)
+    if with_out:
+        assert torch.equal(out_c, eager)
+
+
+def test_compile_fullgraph_wrapper_run():
+    """A planned decode wrapper's run() traced: equal to its eager run()."""
+    from small_q_attention_amd import decode_api as fi
+
+    lens = [3000, 1200, 64]
+    q_len, hq, hkv = 8, 32, 8
+    counts = [-(-n // 16) for n in lens]
+    g = torch.Generator().manual_seed(9)
+    pool = 2 * sum(counts) + 3
+    ids = torch.randperm(pool, generator=g)[:sum(counts)].to(torch.int32).cuda()
+    indptr = torch.tensor([0] + [sum(counts[:i + 1]) for i in range(len(counts))],
+                          dtype=torch.int32).cuda()
+    last = torch.tensor([(n - 1) % 16 + 1 for n in lens], dtype=torch.int32).cuda()
+    kv = torch.randn(pool, 2, 16, hkv, 128, generator=g).half().cuda()
+    q = torch.randn(len(lens) * q_len, hq, 128, generator=g).half().cuda()
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    dec = fi.BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
+    dec.plan(indptr, ids, last, hq, hkv, 128, 16, q_len_per_req=q_len)
+    eager = dec.run(q, kv)
+    got = torch.compile(lambda q, kv: dec.run(q, kv), backend="aot_eager", fullgraph=True)(q, kv)
+    torch.cuda.synchronize()
+    assert torch.equal(got, eager)
