@@ -25,7 +25,10 @@ int fail(int code, const char* fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(buf, sizeof(buf), fmt, ap);
   va_end(ap);
-  g_last_error = buf;
+  try {  // a message that cannot be stored is lost; the status still returns
+    g_last_error = buf;
+  } catch (...) {
+  }
   return code;
 }
 
@@ -52,19 +55,24 @@ const char* sqa_last_error(void) { return g_last_error.c_str(); }
 const char* sqa_version(void) { return "sqa 0.2.0 gfx950 sqa-src-hash:" SQA_SOURCE_HASH; }
 
 int sqa_device_cu_count(int device) {
-  std::lock_guard<std::mutex> lock(g_cu_mutex);
   if (device < 0) return -1;
-  if ((int)g_cu_count.size() <= device) g_cu_count.resize(device + 1, 0);
-  if (g_cu_count[device] == 0) {
-    int n = 0;
-    hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
-    if (e != hipSuccess || n <= 0) {
-      hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
-      return -1;
+  try {  // the lock and the cache's growth may throw; nothing crosses the C boundary
+    std::lock_guard<std::mutex> lock(g_cu_mutex);
+    if ((int)g_cu_count.size() <= device) g_cu_count.resize(device + 1, 0);
+    if (g_cu_count[device] == 0) {
+      int n = 0;
+      hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+      if (e != hipSuccess || n <= 0) {
+        hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
+        return -1;
+      }
+      g_cu_count[device] = n;
     }
-    g_cu_count[device] = n;
+    return g_cu_count[device];
+  } catch (...) {
+    fail(SQA_ERR_HIP, "sqa_device_cu_count: out of host memory or lock failure");
+    return -1;
   }
-  return g_cu_count[device];
 }
 
 int sqa_plan_splits(int device, int batch, int q_len, int num_query_heads, int num_kv_heads,
@@ -451,16 +459,20 @@ int scratch_address(void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0) return hip_fail(e, "hipGetDevice");
-  std::lock_guard<std::mutex> lock(g_scratch_mutex);
-  if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
-  if (!g_scratch_ptr[dev]) {
-    void* p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress(scratch)");
-    g_scratch_ptr[dev] = p;
+  try {  // the lock and the table's growth may throw; nothing crosses the C boundary
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (!g_scratch_ptr[dev]) {
+      void* p = nullptr;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+      g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return SQA_OK;
+  } catch (...) {
+    return fail(SQA_ERR_HIP, "scratch lookup: out of host memory or lock failure");
   }
-  *out = g_scratch_ptr[dev];
-  return SQA_OK;
 }
 
 }  // namespace
