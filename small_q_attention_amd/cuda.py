@@ -46,7 +46,7 @@ MAX_ROWS = 64
 
 
 def _load(verbose: bool = False):
-    if _tracing():  # the traced call loads it through the plan (see _traced_op)
+    if _tracing():  # a traced call's custom op loads it when the graph runs (_traced_op)
         return None
     return _lib.load(verbose=bool(verbose))
 
@@ -195,7 +195,8 @@ def _check_launcher_contract(query, key_cache, value_cache, block_tables, seq_le
 
 def _run(query, key_cache, value_cache, block_tables, seq_lens, page_size,
          chunk_keys: Optional[int], max_seq_len: int):
-    """Plan the split-KV grid and run the custom op.
+    """Plan the split-KV grid and launch: eagerly through the library, or, while
+    torch.compile / torch.export trace, through the custom op (:func:`_traced_op`).
 
     ``max_seq_len``: > 0 known; -1 measure with ``seq_lens.max().item()`` (a host
     sync, as the reference v2 launcher always does and v3-v5 do for 0,
